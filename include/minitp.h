@@ -1,0 +1,212 @@
+/*
+ * minitp: C ABI of the MI355X (gfx950) Qwen2 token-loop library.
+ *
+ * Every entry point returns an int status (MINITP_OK == 0, negative on
+ * error), never throws or aborts across the ABI, only borrows caller-owned
+ * device pointers for the stream-ordered lifetime of the call, and never
+ * allocates device memory (scratch comes from a caller workspace sized by
+ * the matching *_workspace_bytes query). `stream` is a hipStream_t passed as
+ * void*. Tensors are row-major; `dtype` is MINITP_F32 or MINITP_BF16 and
+ * applies to every floating-point tensor of a call except the RoPE tables,
+ * which are always fp32 (minitp/rope.py:34-35 keeps them in fp32).
+ *
+ * Citations are file:line in the mini-tp reference; each names the
+ * reference function the entry point stands in for at tp_size == 1.
+ */
+#ifndef MINITP_H
+#define MINITP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MINITP_ABI_VERSION 1
+
+enum {
+  MINITP_OK = 0,
+  MINITP_ERR_ARG = -1,         /* bad pointer, shape, alignment or dtype   */
+  MINITP_ERR_HIP = -2,         /* a HIP runtime call failed                */
+  MINITP_ERR_OVERFLOW = -3,    /* KV cache overflow (kv_cache.py:49-52)    */
+  MINITP_ERR_RANGE = -4,       /* index out of range (rope.py:37-45)       */
+  MINITP_ERR_UNSUPPORTED = -5, /* valid request this build does not serve  */
+  MINITP_ERR_DIVISIBLE = -6    /* TP divisibility (config.py:56-68)        */
+};
+
+enum { MINITP_F32 = 0, MINITP_BF16 = 1 };
+
+/* Linear epilogues (see minitp_linear). */
+enum {
+  MINITP_EPI_NONE = 0,   /* y = x W^T (+ bias)                                     */
+  MINITP_EPI_RESID = 1,  /* y = aux + (x W^T), each rounded to dtype (layer.py:63-64) */
+  MINITP_EPI_SWIGLU = 2  /* W is [2N, K] = [gate; up]; y = silu(gate) * up (mlp.py:38) */
+};
+
+const char* minitp_status_string(int status);
+/* Detail message of the last error raised on the calling thread. */
+const char* minitp_last_error(void);
+int minitp_abi_version(void);
+
+/* ---- synthetic initialisation (seeded, bit-identical to the CPU spec) ---- */
+/* dst[i] = dtype(float32(std * z_i)), z from the polar-method normal stream. */
+int minitp_fill_normal(void* stream, int dtype, void* dst, int64_t count, uint64_t seed,
+                       uint64_t stream_id, double std_dev);
+/* dst[i] = uniform integer in [0, vocab). */
+int minitp_fill_uniform_ids(void* stream, int64_t* dst, int64_t count, uint64_t seed,
+                            uint64_t stream_id, int64_t vocab);
+/* dst[i] = value (KVCache.poison, kv_cache.py:60-63; zeros init, kv_cache.py:33). */
+int minitp_fill(void* stream, int dtype, void* dst, int64_t count, float value);
+
+/* ---- elementwise / normalisation ---------------------------------------- */
+/* VocabParallelEmbedding.forward at tp=1: F.embedding (embedding.py:44-46).
+ * out[n, :] = table[ids[n], :]; an id outside [0, vocab) yields a NaN row. */
+int minitp_embedding(void* stream, int dtype, const void* table, const int64_t* ids, void* out,
+                     int64_t n_tokens, int64_t hidden, int64_t vocab);
+/* RMSNorm.forward "reference" math (layer.py:39-42), fp32 internally:
+ * out = dtype((x * rsqrt(mean(x^2) + eps)) * w). x, out: [rows, hidden]. */
+int minitp_rmsnorm(void* stream, int dtype, const void* x, const void* w, void* out, int64_t rows,
+                   int64_t hidden, float eps);
+/* Residual add in the model dtype (layer.py:63-64): out[i] = dtype(a[i] + b[i % b_period]).
+ * b_period == n is elementwise; b_period == hidden broadcasts one row (the
+ * post-reduce bias add of RowParallelLinear, linear.py:120-121). */
+int minitp_add(void* stream, int dtype, const void* a, const void* b, void* out, int64_t n, int64_t b_period);
+/* SwiGLU gate (mlp.py:38): out = dtype(dtype(silu(gate)) * up).
+ * gate/up rows have stride ld_in, out rows stride ld_out; [rows, n]. */
+int minitp_silu_mul(void* stream, int dtype, const void* gate, const void* up, int64_t ld_in,
+                    void* out, int64_t ld_out, int64_t rows, int64_t n);
+
+/* ---- linear layers ------------------------------------------------------ */
+/* F.linear(x, W, bias) with fp32 accumulation (linear.py:57-58, 111-122;
+ * fused.py:57-61, 102-104), result rounded to dtype, then the epilogue.
+ * x: [M, K] (row stride ldx), W: [N, K] (or [2N, K] for SWIGLU), bias: [N]
+ * or NULL, y: [M, N] (row stride ldy), aux: [M, N] (stride ldy) for RESID
+ * (may alias y). Small M streams W once as a GEMV; larger M runs an MFMA
+ * GEMM. K must be a multiple of 8; pointers 16-byte aligned. */
+int minitp_linear(void* stream, int dtype, const void* x, int64_t ldx, const void* w,
+                  const void* bias, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                  int epilogue, const void* aux);
+
+/* ---- rotary embedding and KV cache -------------------------------------- */
+/* RotaryEmbedding.apply (rope.py:47-64): q [B, Hq, T, D] and k [B, Hkv, T, D]
+ * (contiguous) rotated by rows positions[t] of the fp32 tables [max_pos, D];
+ * rotate_half pairs (i, i + D/2). Results go to q_out / k_out. Positions are
+ * not range-checked here (the caller checks; rope.py:37-45). */
+int minitp_rope(void* stream, int dtype, const void* q, const void* k, void* q_out, void* k_out,
+                const float* cos_tab, const float* sin_tab, const int64_t* positions, int64_t B,
+                int64_t Hq, int64_t Hkv, int64_t T, int64_t D);
+/* KVCache.update write half (kv_cache.py:53-54): copy k_new / v_new
+ * [B, H, T, D] (contiguous) into cache[b, h, cache_len + t, :] of the layer
+ * buffers [B, H, S, D]. Returns MINITP_ERR_OVERFLOW if cache_len + T > S. */
+int minitp_kv_write(void* stream, int dtype, const void* k_new, const void* v_new, void* k_cache,
+                    void* v_cache, int64_t B, int64_t H, int64_t T, int64_t D, int64_t S,
+                    int64_t cache_len);
+/* Fused QKV split + RoPE + KV write (fused.py:60, attention.py:59-73):
+ * qkv [B*T, (Hq+2Hkv)*D] (row stride ld_qkv, bias already added) ->
+ * q_out [B, T, Hq, D] rotated, k rotated and v copied into the layer caches
+ * [B, Hkv, S, D] at cache_len + t. Out-of-table positions give NaN rows. */
+int minitp_rope_kv_write(void* stream, int dtype, const void* qkv, int64_t ld_qkv, void* q_out,
+                         void* k_cache, void* v_cache, const float* cos_tab, const float* sin_tab,
+                         const int64_t* positions, int64_t max_pos, int64_t B, int64_t T,
+                         int64_t Hq, int64_t Hkv, int64_t D, int64_t S, int64_t cache_len);
+
+/* ---- attention ---------------------------------------------------------- */
+/* GQA scaled-dot-product attention over the cache (attention.py:77-105):
+ * q [B, T, Hq, D]; caches [B, Hkv, S, D] hold cache_len + T valid rows;
+ * query t of head h attends keys 0..cache_len + t of KV head h / (Hq/Hkv)
+ * (T == 1: all keys; cache_len == 0: is_causal; else tril(diagonal=cache_len)).
+ * out [B, T, Hq * D]. Scale 1/sqrt(D). Workspace from the query below. */
+int64_t minitp_attention_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D,
+                                         int64_t S);
+int minitp_attention(void* stream, int dtype, const void* q, const void* k_cache,
+                     const void* v_cache, void* out, int64_t B, int64_t T, int64_t Hq,
+                     int64_t Hkv, int64_t D, int64_t S, int64_t cache_len, void* workspace,
+                     int64_t workspace_bytes);
+
+/* ---- greedy selection --------------------------------------------------- */
+/* distributed_argmax tp=1 fast path (embedding.py:146-147; generation.py:59):
+ * out[b * out_stride] = argmax over logits[b * ld + 0 .. V), torch.argmax
+ * order (first maximum; NaN wins). Workspace from the query below. */
+int64_t minitp_argmax_workspace_bytes(int64_t B, int64_t V);
+int minitp_argmax(void* stream, int dtype, const void* logits, int64_t ld, int64_t B, int64_t V,
+                  int64_t* out, int64_t out_stride, void* workspace, int64_t workspace_bytes);
+
+/* ---- whole-model programs ------------------------------------------------ */
+/* TPQwen2ForCausalLM (layer.py:68-124) at tp_size == 1, run as one native
+ * launch sequence; the decode step can be replayed as one hipGraph. */
+typedef struct minitp_qwen2_config {
+  int32_t dtype;
+  int32_t num_layers;
+  int32_t hidden;
+  int32_t heads;
+  int32_t kv_heads;
+  int32_t head_dim;
+  int32_t intermediate;
+  int32_t vocab;
+  int32_t max_pos; /* rows of the RoPE tables */
+  float eps;
+} minitp_qwen2_config;
+
+/* Per-layer pointer order in `layers` (7 per layer). */
+enum {
+  MINITP_W_LN1 = 0,
+  MINITP_W_LN2 = 1,
+  MINITP_W_QKV = 2,
+  MINITP_W_QKV_BIAS = 3,
+  MINITP_W_O = 4,
+  MINITP_W_GATE_UP = 5,
+  MINITP_W_DOWN = 6,
+  MINITP_W_PER_LAYER = 7
+};
+
+typedef struct minitp_qwen2_weights {
+  const void* embed;      /* [V, H] */
+  const void* lm_head;    /* [V, H]; equals embed when tied (layer.py:88-89) */
+  const void* final_norm; /* [H] */
+  const float* rope_cos;  /* [max_pos, D] fp32 */
+  const float* rope_sin;
+  const void* const* layers; /* [num_layers * MINITP_W_PER_LAYER] */
+} minitp_qwen2_weights;
+
+/* One forward over ids [B, T]. logits: [B, T, V] when logits_all, else the
+ * last position only [B, V]. next_tok (optional): argmax of the last
+ * position per row, written to next_tok[b * next_tok_ld]. The KV caches are
+ * [L, B, Hkv, S, D]; rows cache_len .. cache_len + T - 1 are written. */
+typedef struct minitp_qwen2_step {
+  const int64_t* ids;
+  int64_t ids_ld;
+  const int64_t* positions; /* [T] absolute positions */
+  int64_t batch;
+  int64_t tokens;
+  int64_t cache_len;
+  void* k_cache;
+  void* v_cache;
+  int64_t max_seq;
+  void* logits;
+  int32_t logits_all;
+  int64_t* next_tok;
+  int64_t next_tok_ld;
+  void* workspace;
+  int64_t workspace_bytes;
+} minitp_qwen2_step;
+
+int minitp_qwen2_create(const minitp_qwen2_config* cfg, const minitp_qwen2_weights* w,
+                        void** handle);
+int minitp_qwen2_destroy(void* handle);
+/* Workspace for forwards of up to max_tokens = B*T rows, batch B, cache S. */
+int64_t minitp_qwen2_workspace_bytes(void* handle, int64_t max_tokens, int64_t batch,
+                                     int64_t max_seq);
+/* GenerationState.prefill / TPQwen2ForCausalLM.forward (generation.py:112-117,
+ * layer.py:91-124): direct launches. */
+int minitp_qwen2_forward(void* handle, void* stream, const minitp_qwen2_step* step);
+/* GenerationState.decode_step (generation.py:129-130): T == 1 forward
+ * replayed from a hipGraph captured on first use for (batch, max_seq,
+ * workspace); per-step scalars and pointers are patched into the graph's
+ * first node, so replays need no re-capture. */
+int minitp_qwen2_decode(void* handle, void* stream, const minitp_qwen2_step* step);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MINITP_H */

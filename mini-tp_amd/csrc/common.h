@@ -1,0 +1,168 @@
+// Shared device/host helpers for the minitp HIP library (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <algorithm>
+
+#include "../../include/minitp.h"
+
+namespace minitp {
+
+// ---------------------------------------------------------------------------
+// Storage types. bf16 is kept as raw uint16 so every conversion (and its
+// rounding) is explicit: float -> bf16 rounds to nearest even like
+// torch's Tensor.to(torch.bfloat16); NaN maps to a quiet NaN.
+struct bf16 {
+  uint16_t bits;
+};
+
+__device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
+
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x0040u);  // quiet NaN
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Round a float to the model's storage precision and back (identity for f32).
+template <typename T>
+__device__ __forceinline__ float round_to(float v);
+template <>
+__device__ __forceinline__ float round_to<float>(float v) { return v; }
+template <>
+__device__ __forceinline__ float round_to<bf16>(float v) { return bf16_to_f32(f32_to_bf16(v)); }
+
+template <typename T>
+__device__ __forceinline__ float load_f32(const T* p, int64_t i);
+template <>
+__device__ __forceinline__ float load_f32<float>(const float* p, int64_t i) { return p[i]; }
+template <>
+__device__ __forceinline__ float load_f32<bf16>(const bf16* p, int64_t i) { return bf16_to_f32(p[i].bits); }
+
+template <typename T>
+__device__ __forceinline__ void store_f32(T* p, int64_t i, float v);
+template <>
+__device__ __forceinline__ void store_f32<float>(float* p, int64_t i, float v) { p[i] = v; }
+template <>
+__device__ __forceinline__ void store_f32<bf16>(bf16* p, int64_t i, float v) { p[i].bits = f32_to_bf16(v); }
+
+// 16-byte vector of elements: 8 bf16 or 4 f32.
+template <typename T>
+struct Vec;
+template <>
+struct Vec<bf16> {
+  static constexpr int N = 8;
+};
+template <>
+struct Vec<float> {
+  static constexpr int N = 4;
+};
+
+// Streaming 16-byte load (weights are read once per step: non-temporal).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+__device__ __forceinline__ uint4 load_stream16(const uint4* p) {
+  u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+__device__ __forceinline__ void unpack16(const uint4& v, float* out, bf16*) {
+  const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    out[2 * i] = __uint_as_float(w[i] << 16);
+    out[2 * i + 1] = __uint_as_float(w[i] & 0xffff0000u);
+  }
+}
+__device__ __forceinline__ void unpack16(const uint4& v, float* out, float*) {
+  out[0] = __uint_as_float(v.x);
+  out[1] = __uint_as_float(v.y);
+  out[2] = __uint_as_float(v.z);
+  out[3] = __uint_as_float(v.w);
+}
+
+// Separately rounded multiply and add, for the places where the reference
+// rounds each elementwise op on its own. HIP's __fmul_rn / __fadd_rn are
+// plain operators that the compiler may contract into an FMA, so contraction
+// is switched off here (and for the whole library in the Makefile; every
+// intended fused multiply-add is written as fmaf).
+__device__ __forceinline__ float mul_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a * b;
+}
+__device__ __forceinline__ float add_rn(float a, float b) {
+#pragma clang fp contract(off)
+  return a + b;
+}
+
+// SwiGLU on values already rounded to the dtype (mlp.py:38):
+// silu(g) = g / (1 + exp(-g)) in fp32, rounded to the dtype, times up, rounded.
+__device__ __forceinline__ float silu_f32(float g) { return __fdiv_rn(g, add_rn(1.0f, expf(-g))); }
+template <typename T>
+__device__ __forceinline__ float swiglu(float g, float u) {
+  return round_to<T>(mul_rn(round_to<T>(silu_f32(g)), u));
+}
+
+// ---------------------------------------------------------------------------
+// Wave64 reductions (butterfly; every lane ends with the result).
+__device__ __forceinline__ float wave_sum(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+__device__ __forceinline__ float wave_max(float v) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// torch.argmax order: NaN beats any number; equal values (and two NaNs)
+// resolve to the smaller index.
+__device__ __forceinline__ bool argmax_better(float va, int64_t ia, float vb, int64_t ib) {
+  bool na = va != va, nb = vb != vb;
+  if (na || nb) return na && (!nb || ia < ib);
+  return va > vb || (va == vb && ia < ib);
+}
+
+__device__ __forceinline__ void wave_argmax(float& v, int64_t& i) {
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    float ov = __shfl_xor(v, o, 64);
+    int64_t oi = __shfl_xor(i, o, 64);
+    if (argmax_better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side: status plumbing.
+void set_error(const char* fmt, ...);
+
+#define MINITP_CHECK_ARG(cond, ...)                     \
+  do {                                                  \
+    if (!(cond)) {                                      \
+      ::minitp::set_error(__VA_ARGS__);                 \
+      return MINITP_ERR_ARG;                            \
+    }                                                   \
+  } while (0)
+
+#define MINITP_RETURN_HIP(call)                                                      \
+  do {                                                                               \
+    hipError_t _e = (call);                                                          \
+    if (_e != hipSuccess) {                                                          \
+      ::minitp::set_error("%s failed: %s", #call, hipGetErrorString(_e));             \
+      return MINITP_ERR_HIP;                                                         \
+    }                                                                                \
+  } while (0)
+
+// Check the launch status right after a <<<>>> launch.
+#define MINITP_LAUNCH_CHECK() MINITP_RETURN_HIP(hipGetLastError())
+
+inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+__host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
+
+}  // namespace minitp

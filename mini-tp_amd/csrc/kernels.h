@@ -1,0 +1,114 @@
+// Host-side launch interface of the minitp kernels (internal to the library).
+#pragma once
+
+#include "common.h"
+
+namespace minitp {
+
+// Per-forward scalars and pointers the decode sequence reads from device
+// memory, so a captured hipGraph stays valid from step to step: only the
+// first node's arguments change, and it writes this struct.
+struct StepState {
+  const int64_t* ids;  // [B, T] token ids, row stride ids_ld
+  int64_t ids_ld;
+  const int64_t* positions;  // [T]
+  int64_t cache_len;         // KV rows already filled
+  void* k_cache;             // [L, B, Hkv, S, D]
+  void* v_cache;
+  void* logits;  // [B, V] last-position logits
+  int64_t* next_tok;
+  int64_t next_tok_ld;
+  int32_t error;  // bit 0: a position was outside the RoPE table
+  int32_t pad_;
+};
+
+// Layer-independent shape of the attention / KV layout.
+struct AttnShape {
+  int B, T, Hq, Hkv, D;
+  int64_t S;  // cache capacity per (b, kv head)
+};
+
+enum GemvPro { PRO_NONE = 0, PRO_NORM = 1 };
+enum GemvEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV_ROPE = 3, EPI_ARGMAX = 4 };
+
+struct GemvArgs {
+  const void* x;  // [M, K] input rows (pre-norm residual when PRO_NORM)
+  int64_t ldx;
+  const void* norm_w;  // [K] RMSNorm weight (PRO_NORM)
+  float eps;
+  const void* w;     // weight rows, each K long
+  const void* bias;  // [N] or null (EPI_STORE, EPI_QKV_ROPE)
+  void* y;           // output [M, N] (row stride ldy)
+  int64_t ldy;
+  const void* aux;  // residual [M, N] (EPI_RESID; may alias y)
+  int64_t M, N, K;  // N: logical outputs (EPI_SWIGLU: weight has 2N rows)
+  // EPI_QKV_ROPE: q -> y as [B, T, Hq, D]; k, v -> caches of layer `layer`
+  const StepState* st;
+  const float* cos_tab;
+  const float* sin_tab;
+  int64_t max_pos;
+  int layer;
+  AttnShape a;
+  // EPI_ARGMAX: logits -> st->logits (ld N), token -> st->next_tok
+  float* part_val;  // [M, gridDim.x] block partials
+  int64_t* part_idx;
+  unsigned* counter;  // zero before the launch, zero again after it
+};
+
+// gemv.hip
+int64_t gemv_argmax_partials(int64_t N);
+int launch_gemv(hipStream_t st, int dtype, int pro, int epi, const GemvArgs& a);
+bool gemv_supported(int dtype, int64_t M, int64_t K);
+
+// gemm.hip: y[M, N] = epilogue(x[M, K] W[N, K]^T (+ bias)), MFMA tiles.
+// When `state` is non-null the output base is state->logits (graph replays).
+int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
+                int64_t ldy, int64_t M, int64_t N, int64_t K, int epi, const void* aux,
+                const StepState* state = nullptr);
+
+// elementwise.hip
+int launch_fill_normal(hipStream_t st, int dtype, void* dst, int64_t count, uint64_t seed, uint64_t sid,
+                       double std_dev);
+int launch_fill_ids(hipStream_t st, int64_t* dst, int64_t count, uint64_t seed, uint64_t sid, int64_t vocab);
+int launch_fill(hipStream_t st, int dtype, void* dst, int64_t count, float value);
+int launch_embedding(hipStream_t st, int dtype, const void* table, const int64_t* ids, int64_t ids_ld, int64_t B,
+                     int64_t T, void* out, int64_t hidden, int64_t vocab);
+int launch_rmsnorm(hipStream_t st, int dtype, const void* x, const void* w, void* out, int64_t rows, int64_t hidden,
+                   float eps);
+int launch_add(hipStream_t st, int dtype, const void* a, const void* b, void* out, int64_t n, int64_t b_period);
+int launch_silu_mul(hipStream_t st, int dtype, const void* gate, const void* up, int64_t ld_in, void* out,
+                    int64_t ld_out, int64_t rows, int64_t n);
+
+// rope.hip
+int launch_rope(hipStream_t st, int dtype, const void* q, const void* k, void* q_out, void* k_out, const float* cos_tab,
+                const float* sin_tab, const int64_t* positions, int64_t B, int64_t Hq, int64_t Hkv, int64_t T,
+                int64_t D);
+int launch_kv_write(hipStream_t st, int dtype, const void* k_new, const void* v_new, void* k_cache, void* v_cache,
+                    int64_t B, int64_t H, int64_t T, int64_t D, int64_t S, int64_t cache_len);
+int launch_rope_kv_write(hipStream_t st, int dtype, const void* qkv, int64_t ld_qkv, void* q_out, void* k_cache,
+                         void* v_cache, const float* cos_tab, const float* sin_tab, const int64_t* positions,
+                         int64_t max_pos, int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t S,
+                         int64_t cache_len, int32_t* error_flag, const StepState* state = nullptr,
+                         int layer = 0);
+
+// attention.hip. Decode (T == 1) may read cache_len and the cache bases
+// from a StepState (graph replay); prefill takes them by value.
+int64_t attention_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t S);
+int launch_decode_attention(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,
+                            void* out, const AttnShape& a, int64_t cache_len, const StepState* state, int layer,
+                            void* workspace, int64_t workspace_bytes);
+int launch_prefill_attention(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,
+                             void* out, const AttnShape& a, int64_t cache_len);
+
+// argmax.hip
+int64_t argmax_workspace_bytes(int64_t B, int64_t V);
+// With `state`: logits = state->logits + row_offset, out = state->next_tok
+// (stride state->next_tok_ld); row b of the logits starts at b * ld.
+int launch_argmax(hipStream_t st, int dtype, const void* logits, int64_t ld, int64_t B, int64_t V, int64_t* out,
+                  int64_t out_stride, void* workspace, int64_t workspace_bytes, const StepState* state = nullptr,
+                  int64_t row_offset = 0);
+
+// Raise the dynamic-LDS limit of a kernel once (needed above 64 KiB).
+int ensure_lds_limit(const void* kernel, int bytes);
+
+}  // namespace minitp

@@ -1,0 +1,457 @@
+// Whole-model Qwen2 program at tp_size == 1: TPQwen2ForCausalLM.forward
+// (layer.py:91-124) as one native launch sequence, and the decode step as a
+// replayable hipGraph.
+//
+// Per-forward values (ids, positions, cache cursor, cache / logits / token
+// pointers) travel in a StepState that the first kernel writes into the
+// workspace; every later kernel reads it from there. A captured decode graph
+// therefore never needs re-capture: each replay patches only the first
+// node's by-value argument.
+//
+// Rows M = B * T <= 4 take the fused GEMV path, 5 kernels per layer:
+//   [RMSNorm -> QKV + bias -> RoPE -> q, KV write] [attention]
+//   [o_proj + residual] [RMSNorm -> gate/up -> SwiGLU] [down + residual]
+// and the final RMSNorm -> LM head -> argmax is one more kernel. Larger M
+// runs MFMA GEMMs with separate norm / RoPE / SwiGLU kernels.
+#include <mutex>
+#include <vector>
+
+#include "common.h"
+#include "kernels.h"
+
+namespace minitp {
+
+namespace {
+
+template <typename T>
+__global__ void step_embed_kernel(StepState* dst, StepState val, const T* __restrict__ table, T* __restrict__ out,
+                                  int64_t hidden, int64_t vocab, int64_t T_) {
+  if (blockIdx.x == 0 && threadIdx.x == 0) *dst = val;
+  const int64_t n = blockIdx.x, b = n / T_, t = n % T_;
+  const int64_t id = val.ids[b * val.ids_ld + t];
+  T* o = out + n * hidden;
+  if (id < 0 || id >= vocab) {
+    for (int64_t i = threadIdx.x; i < hidden; i += blockDim.x) store_f32<T>(o, i, __builtin_nanf(""));
+    return;
+  }
+  const uint4* src = reinterpret_cast<const uint4*>(table + id * hidden);
+  uint4* d4 = reinterpret_cast<uint4*>(o);
+  const int64_t nv = hidden * (int64_t)sizeof(T) / 16;
+  for (int64_t i = threadIdx.x; i < nv; i += blockDim.x) d4[i] = src[i];
+}
+
+constexpr int EMBED_THREADS = 128;
+
+struct Ws {
+  StepState* st;
+  void *x, *h, *qkv, *q, *attn, *gu, *act;
+  void* attn_ws;
+  int64_t attn_ws_bytes;
+  float* part_val;
+  int64_t* part_idx;
+  unsigned* counter;
+  void* amax_ws;
+  int64_t amax_ws_bytes;
+  int64_t bytes;
+};
+
+struct GraphEntry {
+  int64_t batch, max_seq;
+  void* workspace;
+  hipGraph_t graph;
+  hipGraphExec_t exec;
+  hipGraphNode_t first;
+};
+
+inline int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
+
+}  // namespace
+
+struct Qwen2Program {
+  minitp_qwen2_config c;
+  const void* embed;
+  const void* lm_head;
+  const void* final_norm;
+  const float* cos_tab;
+  const float* sin_tab;
+  std::vector<const void*> lw;
+  std::mutex mu;
+  std::vector<GraphEntry> graphs;
+  hipStream_t capture_stream = nullptr;
+
+  int es() const { return c.dtype == MINITP_F32 ? 4 : 2; }
+  int qkv_rows() const { return (c.heads + 2 * c.kv_heads) * c.head_dim; }
+  int q_rows() const { return c.heads * c.head_dim; }
+  const void* L(int layer, int which) const { return lw[(size_t)layer * MINITP_W_PER_LAYER + which]; }
+
+  Ws layout(void* base, int64_t M, int64_t B, int64_t S) const {
+    Ws w{};
+    char* p = (char*)base;
+    int64_t off = 0;
+    auto take = [&](int64_t bytes) {
+      char* r = p ? p + off : nullptr;
+      off += align256(bytes);
+      return (void*)r;
+    };
+    w.st = (StepState*)take(sizeof(StepState));
+    w.x = take(M * c.hidden * es());
+    w.h = take(M * c.hidden * es());
+    w.qkv = take(M * qkv_rows() * es());
+    w.q = take(M * q_rows() * es());
+    w.attn = take(M * q_rows() * es());
+    w.gu = take(M * 2LL * c.intermediate * es());
+    w.act = take(M * (int64_t)c.intermediate * es());
+    w.attn_ws_bytes = attention_workspace_bytes(B, 1, c.heads, c.kv_heads, c.head_dim, S);
+    w.attn_ws = take(w.attn_ws_bytes);
+    const int64_t np = gemv_argmax_partials(c.vocab);
+    w.part_val = (float*)take(std::min<int64_t>(B, 4) * np * 4);
+    w.part_idx = (int64_t*)take(std::min<int64_t>(B, 4) * np * 8);
+    w.counter = (unsigned*)take(4);
+    w.amax_ws_bytes = argmax_workspace_bytes(B, c.vocab);
+    w.amax_ws = take(w.amax_ws_bytes);
+    w.bytes = off;
+    return w;
+  }
+
+  bool fused(int64_t M) const {
+    return gemv_supported(c.dtype, M, c.hidden) && gemv_supported(c.dtype, M, c.intermediate) &&
+           gemv_supported(c.dtype, M, q_rows());
+  }
+
+  // The launch sequence of one forward (also what a decode graph records).
+  int run(hipStream_t st, const minitp_qwen2_step& s, const Ws& w) {
+    const int64_t B = s.batch, T = s.tokens, M = B * T;
+    const int64_t H = c.hidden, I = c.intermediate, V = c.vocab;
+    const int D = c.head_dim;
+    int rc;
+    StepState val{};
+    val.ids = s.ids;
+    val.ids_ld = s.ids_ld;
+    val.positions = s.positions;
+    val.cache_len = s.cache_len;
+    val.k_cache = s.k_cache;
+    val.v_cache = s.v_cache;
+    val.logits = s.logits;
+    val.next_tok = s.next_tok;
+    val.next_tok_ld = s.next_tok_ld;
+    if (c.dtype == MINITP_F32)
+      hipLaunchKernelGGL(step_embed_kernel<float>, dim3((unsigned)M), dim3(EMBED_THREADS), 0, st, w.st, val,
+                         (const float*)embed, (float*)w.x, H, (int64_t)V, T);
+    else
+      hipLaunchKernelGGL(step_embed_kernel<bf16>, dim3((unsigned)M), dim3(EMBED_THREADS), 0, st, w.st, val,
+                         (const bf16*)embed, (bf16*)w.x, H, (int64_t)V, T);
+    MINITP_LAUNCH_CHECK();
+
+    const bool fz = fused(M);
+    AttnShape as{(int)B, (int)T, c.heads, c.kv_heads, D, s.max_seq};
+    const int64_t layer_elems = B * c.kv_heads * s.max_seq * D;
+    for (int l = 0; l < c.num_layers; ++l) {
+      // ---- attention block --------------------------------------------------
+      if (fz) {
+        GemvArgs g{};
+        g.x = w.x;
+        g.ldx = H;
+        g.norm_w = L(l, MINITP_W_LN1);
+        g.eps = c.eps;
+        g.w = L(l, MINITP_W_QKV);
+        g.bias = L(l, MINITP_W_QKV_BIAS);
+        g.y = w.q;
+        g.ldy = q_rows();
+        g.M = M;
+        g.N = qkv_rows();
+        g.K = H;
+        g.st = w.st;
+        g.cos_tab = cos_tab;
+        g.sin_tab = sin_tab;
+        g.max_pos = c.max_pos;
+        g.layer = l;
+        g.a = as;
+        if ((rc = launch_gemv(st, c.dtype, PRO_NORM, EPI_QKV_ROPE, g))) return rc;
+      } else {
+        if ((rc = launch_rmsnorm(st, c.dtype, w.x, L(l, MINITP_W_LN1), w.h, M, H, c.eps))) return rc;
+        if ((rc = launch_gemm(st, c.dtype, w.h, H, L(l, MINITP_W_QKV), L(l, MINITP_W_QKV_BIAS), w.qkv, qkv_rows(), M,
+                              qkv_rows(), H, MINITP_EPI_NONE, nullptr)))
+          return rc;
+        if ((rc = launch_rope_kv_write(st, c.dtype, w.qkv, qkv_rows(), w.q, nullptr, nullptr, cos_tab, sin_tab, nullptr,
+                                       c.max_pos, B, T, c.heads, c.kv_heads, D, s.max_seq, 0, nullptr, w.st, l)))
+          return rc;
+      }
+      if (T == 1) {
+        if ((rc = launch_decode_attention(st, c.dtype, w.q, nullptr, nullptr, w.attn, as, s.cache_len, w.st, l,
+                                          w.attn_ws, w.attn_ws_bytes)))
+          return rc;
+      } else {
+        const char* kc = (const char*)s.k_cache + l * layer_elems * es();
+        const char* vc = (const char*)s.v_cache + l * layer_elems * es();
+        if ((rc = launch_prefill_attention(st, c.dtype, w.q, kc, vc, w.attn, as, s.cache_len))) return rc;
+      }
+      if (fz) {
+        GemvArgs g{};
+        g.x = w.attn;
+        g.ldx = q_rows();
+        g.w = L(l, MINITP_W_O);
+        g.y = w.x;
+        g.ldy = H;
+        g.aux = w.x;
+        g.M = M;
+        g.N = H;
+        g.K = q_rows();
+        if ((rc = launch_gemv(st, c.dtype, PRO_NONE, EPI_RESID, g))) return rc;
+      } else {
+        if ((rc = launch_gemm(st, c.dtype, w.attn, q_rows(), L(l, MINITP_W_O), nullptr, w.x, H, M, H, q_rows(),
+                              MINITP_EPI_RESID, w.x)))
+          return rc;
+      }
+      // ---- MLP block ----------------------------------------------------------
+      if (fz) {
+        GemvArgs g{};
+        g.x = w.x;
+        g.ldx = H;
+        g.norm_w = L(l, MINITP_W_LN2);
+        g.eps = c.eps;
+        g.w = L(l, MINITP_W_GATE_UP);
+        g.y = w.act;
+        g.ldy = I;
+        g.M = M;
+        g.N = I;
+        g.K = H;
+        if ((rc = launch_gemv(st, c.dtype, PRO_NORM, EPI_SWIGLU, g))) return rc;
+        GemvArgs d{};
+        d.x = w.act;
+        d.ldx = I;
+        d.w = L(l, MINITP_W_DOWN);
+        d.y = w.x;
+        d.ldy = H;
+        d.aux = w.x;
+        d.M = M;
+        d.N = H;
+        d.K = I;
+        if ((rc = launch_gemv(st, c.dtype, PRO_NONE, EPI_RESID, d))) return rc;
+      } else {
+        if ((rc = launch_rmsnorm(st, c.dtype, w.x, L(l, MINITP_W_LN2), w.h, M, H, c.eps))) return rc;
+        if ((rc = launch_gemm(st, c.dtype, w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.gu, 2 * I, M, 2 * I, H,
+                              MINITP_EPI_NONE, nullptr)))
+          return rc;
+        const char* up = (const char*)w.gu + I * es();
+        if ((rc = launch_silu_mul(st, c.dtype, w.gu, up, 2 * I, w.act, I, M, I))) return rc;
+        if ((rc = launch_gemm(st, c.dtype, w.act, I, L(l, MINITP_W_DOWN), nullptr, w.x, H, M, H, I, MINITP_EPI_RESID,
+                              w.x)))
+          return rc;
+      }
+    }
+    // ---- final norm, LM head, greedy pick ----------------------------------------
+    if (!s.logits_all && gemv_supported(c.dtype, B, H) && B <= 4) {
+      GemvArgs g{};
+      g.x = (const char*)w.x + (T - 1) * H * es();  // last position of each row
+      g.ldx = T * H;
+      g.norm_w = final_norm;
+      g.eps = c.eps;
+      g.w = lm_head;
+      g.M = B;
+      g.N = V;
+      g.K = H;
+      g.st = w.st;
+      g.part_val = w.part_val;
+      g.part_idx = w.part_idx;
+      g.counter = w.counter;
+      return launch_gemv(st, c.dtype, PRO_NORM, EPI_ARGMAX, g);
+    }
+    if (s.logits_all && fz) {  // same kernel family as the module path at this M
+      GemvArgs g{};
+      g.x = w.x;
+      g.ldx = H;
+      g.norm_w = final_norm;
+      g.eps = c.eps;
+      g.w = lm_head;
+      g.y = s.logits;  // forwards with every position's logits are never captured
+      g.ldy = V;
+      g.M = M;
+      g.N = V;
+      g.K = H;
+      if ((rc = launch_gemv(st, c.dtype, PRO_NORM, EPI_STORE, g))) return rc;
+      if (s.next_tok)
+        return launch_argmax(st, c.dtype, nullptr, T * V, B, V, nullptr, 0, w.amax_ws, w.amax_ws_bytes, w.st,
+                             (T - 1) * V);
+      return MINITP_OK;
+    }
+    if ((rc = launch_rmsnorm(st, c.dtype, w.x, final_norm, w.h, M, H, c.eps))) return rc;
+    if (s.logits_all) {
+      if ((rc = launch_gemm(st, c.dtype, w.h, H, lm_head, nullptr, nullptr, V, M, V, H, MINITP_EPI_NONE, nullptr,
+                            w.st)))
+        return rc;
+      if (s.next_tok)
+        return launch_argmax(st, c.dtype, nullptr, T * V, B, V, nullptr, 0, w.amax_ws, w.amax_ws_bytes, w.st,
+                             (T - 1) * V);
+      return MINITP_OK;
+    }
+    const char* hl = (const char*)w.h + (T - 1) * H * es();
+    if ((rc = launch_gemm(st, c.dtype, hl, T * H, lm_head, nullptr, nullptr, V, B, V, H, MINITP_EPI_NONE, nullptr,
+                          w.st)))
+      return rc;
+    if (s.next_tok) return launch_argmax(st, c.dtype, nullptr, V, B, V, nullptr, 0, w.amax_ws, w.amax_ws_bytes, w.st, 0);
+    return MINITP_OK;
+  }
+
+  int check_step(const minitp_qwen2_step* s, Ws& w) {
+    MINITP_CHECK_ARG(s != nullptr, "step is NULL");
+    MINITP_CHECK_ARG(s->batch >= 1 && s->tokens >= 1, "batch=%lld tokens=%lld", (long long)s->batch,
+                     (long long)s->tokens);
+    MINITP_CHECK_ARG(s->ids && s->positions && s->k_cache && s->v_cache && s->workspace, "NULL pointer in step");
+    MINITP_CHECK_ARG(s->logits != nullptr || s->next_tok != nullptr, "step produces nothing (no logits, no next_tok)");
+    MINITP_CHECK_ARG(s->ids_ld >= s->tokens, "ids_ld=%lld < tokens", (long long)s->ids_ld);
+    if (s->cache_len < 0 || s->cache_len + s->tokens > s->max_seq) {
+      set_error("KV cache overflow: seq %lld+%lld > max_seq_len=%lld", (long long)s->cache_len, (long long)s->tokens,
+                (long long)s->max_seq);
+      return MINITP_ERR_OVERFLOW;
+    }
+    const int64_t M = s->batch * s->tokens;
+    w = layout(s->workspace, M, s->batch, s->max_seq);
+    if (s->workspace_bytes < w.bytes) {
+      set_error("workspace %lld B < %lld B needed for %lld rows, batch %lld, max_seq %lld",
+                (long long)s->workspace_bytes, (long long)w.bytes, (long long)M, (long long)s->batch,
+                (long long)s->max_seq);
+      return MINITP_ERR_ARG;
+    }
+    return MINITP_OK;
+  }
+
+  ~Qwen2Program() {
+    for (auto& g : graphs) {
+      (void)hipGraphExecDestroy(g.exec);
+      (void)hipGraphDestroy(g.graph);
+    }
+    if (capture_stream) (void)hipStreamDestroy(capture_stream);
+  }
+};
+
+static int patch_and_launch(Qwen2Program* p, GraphEntry& g, hipStream_t st, const minitp_qwen2_step& s, const Ws& w) {
+  StepState val{};
+  val.ids = s.ids;
+  val.ids_ld = s.ids_ld;
+  val.positions = s.positions;
+  val.cache_len = s.cache_len;
+  val.k_cache = s.k_cache;
+  val.v_cache = s.v_cache;
+  val.logits = s.logits;
+  val.next_tok = s.next_tok;
+  val.next_tok_ld = s.next_tok_ld;
+  StepState* dst = w.st;
+  const void* table = p->embed;
+  void* out = w.x;
+  int64_t hidden = p->c.hidden, vocab = p->c.vocab, tt = 1;
+  void* args[] = {&dst, &val, (void*)&table, &out, &hidden, &vocab, &tt};
+  hipKernelNodeParams kp{};
+  kp.func = p->c.dtype == MINITP_F32 ? (void*)step_embed_kernel<float> : (void*)step_embed_kernel<bf16>;
+  kp.gridDim = dim3((unsigned)s.batch);
+  kp.blockDim = dim3(EMBED_THREADS);
+  kp.sharedMemBytes = 0;
+  kp.kernelParams = args;
+  kp.extra = nullptr;
+  MINITP_RETURN_HIP(hipGraphExecKernelNodeSetParams(g.exec, g.first, &kp));
+  MINITP_RETURN_HIP(hipGraphLaunch(g.exec, st));
+  return MINITP_OK;
+}
+
+}  // namespace minitp
+
+using minitp::Qwen2Program;
+
+extern "C" {
+
+int minitp_qwen2_create(const minitp_qwen2_config* cfg, const minitp_qwen2_weights* w, void** handle) {
+  MINITP_CHECK_ARG(cfg && w && handle, "NULL argument");
+  const auto& c = *cfg;
+  MINITP_CHECK_ARG(c.dtype == MINITP_F32 || c.dtype == MINITP_BF16, "dtype %d", c.dtype);
+  MINITP_CHECK_ARG(c.num_layers > 0 && c.hidden > 0 && c.heads > 0 && c.kv_heads > 0 && c.head_dim > 0 &&
+                       c.intermediate > 0 && c.vocab > 0 && c.max_pos > 0,
+                   "non-positive dimension in config");
+  MINITP_CHECK_ARG(c.heads % c.kv_heads == 0, "num_attention_heads=%d not divisible by num_key_value_heads=%d",
+                   c.heads, c.kv_heads);
+  MINITP_CHECK_ARG(c.head_dim % 8 == 0 && c.hidden % 8 == 0 && c.intermediate % 8 == 0,
+                   "hidden, intermediate and head_dim must be multiples of 8");
+  MINITP_CHECK_ARG(w->embed && w->lm_head && w->final_norm && w->rope_cos && w->rope_sin && w->layers,
+                   "NULL weight pointer");
+  for (int i = 0; i < c.num_layers * MINITP_W_PER_LAYER; ++i)
+    MINITP_CHECK_ARG(w->layers[i] != nullptr && minitp::aligned16(w->layers[i]), "layer weight %d NULL or unaligned",
+                     i);
+  auto* p = new (std::nothrow) Qwen2Program();
+  if (!p) {
+    minitp::set_error("out of host memory");
+    return MINITP_ERR_HIP;
+  }
+  p->c = c;
+  p->embed = w->embed;
+  p->lm_head = w->lm_head;
+  p->final_norm = w->final_norm;
+  p->cos_tab = w->rope_cos;
+  p->sin_tab = w->rope_sin;
+  p->lw.assign(w->layers, w->layers + (size_t)c.num_layers * MINITP_W_PER_LAYER);
+  *handle = p;
+  return MINITP_OK;
+}
+
+int minitp_qwen2_destroy(void* handle) {
+  delete (Qwen2Program*)handle;
+  return MINITP_OK;
+}
+
+int64_t minitp_qwen2_workspace_bytes(void* handle, int64_t max_tokens, int64_t batch, int64_t max_seq) {
+  if (!handle || max_tokens < 1 || batch < 1 || max_seq < 1) return -1;
+  return ((Qwen2Program*)handle)->layout(nullptr, max_tokens, batch, max_seq).bytes;
+}
+
+int minitp_qwen2_forward(void* handle, void* stream, const minitp_qwen2_step* step) {
+  MINITP_CHECK_ARG(handle != nullptr, "NULL handle");
+  auto* p = (Qwen2Program*)handle;
+  minitp::Ws w;
+  int rc = p->check_step(step, w);
+  if (rc) return rc;
+  return p->run((hipStream_t)stream, *step, w);
+}
+
+int minitp_qwen2_decode(void* handle, void* stream, const minitp_qwen2_step* step) {
+  MINITP_CHECK_ARG(handle != nullptr, "NULL handle");
+  auto* p = (Qwen2Program*)handle;
+  minitp::Ws w;
+  int rc = p->check_step(step, w);
+  if (rc) return rc;
+  MINITP_CHECK_ARG(step->tokens == 1, "decode expects tokens == 1, got %lld", (long long)step->tokens);
+  hipStream_t st = (hipStream_t)stream;
+  std::lock_guard<std::mutex> lock(p->mu);
+  for (auto& g : p->graphs)
+    if (g.batch == step->batch && g.max_seq == step->max_seq && g.workspace == step->workspace)
+      return minitp::patch_and_launch(p, g, st, *step, w);
+  // First step with this shape: run eagerly, then record the same sequence.
+  if ((rc = p->run(st, *step, w))) return rc;
+  if (!p->capture_stream) MINITP_RETURN_HIP(hipStreamCreateWithFlags(&p->capture_stream, hipStreamNonBlocking));
+  minitp::GraphEntry g{};
+  g.batch = step->batch;
+  g.max_seq = step->max_seq;
+  g.workspace = step->workspace;
+  MINITP_RETURN_HIP(hipStreamBeginCapture(p->capture_stream, hipStreamCaptureModeRelaxed));
+  rc = p->run(p->capture_stream, *step, w);
+  hipError_t e = hipStreamEndCapture(p->capture_stream, &g.graph);
+  if (rc) {
+    if (e == hipSuccess) (void)hipGraphDestroy(g.graph);
+    return rc;
+  }
+  MINITP_RETURN_HIP(e);
+  size_t n_roots = 0;
+  MINITP_RETURN_HIP(hipGraphGetRootNodes(g.graph, nullptr, &n_roots));
+  if (n_roots != 1) {
+    (void)hipGraphDestroy(g.graph);
+    minitp::set_error("decode graph has %zu root nodes, expected 1", n_roots);
+    return MINITP_ERR_HIP;
+  }
+  MINITP_RETURN_HIP(hipGraphGetRootNodes(g.graph, &g.first, &n_roots));
+  MINITP_RETURN_HIP(hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0));
+  if (p->graphs.size() >= 8) {  // bounded cache: drop the oldest shape
+    (void)hipGraphExecDestroy(p->graphs.front().exec);
+    (void)hipGraphDestroy(p->graphs.front().graph);
+    p->graphs.erase(p->graphs.begin());
+  }
+  p->graphs.push_back(g);
+  return MINITP_OK;
+}
+
+}  // extern "C"
