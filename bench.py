@@ -116,7 +116,7 @@ def dominant_kernel(model, reps: int = 20):
     torch.cuda.synchronize()
     us = a.elapsed_time(b) * 1e3 / n
     nbytes = 2 * (2 * cfg.intermediate_size * cfg.hidden_size + cfg.hidden_size + cfg.intermediate_size)
-    return {"name": "gemv_kernel<bf16,M=1,KSPLIT=1,PRO_NONE,EPI_SWIGLU> (gate/up [9728,896] + SwiGLU)",
+    return {"name": "gemv_reg_kernel<bf16,MM=1,KSPLIT=1,JMAX=2,PRO_NONE,EPI_SWIGLU> (gate/up [9728,896] + SwiGLU)",
             "bytes_per_launch": nbytes, "us_per_launch": us, "launches": n}
 
 

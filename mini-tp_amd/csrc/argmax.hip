@@ -1,7 +1,7 @@
 // Greedy selection over a logits row (embedding.py:146-147, generation.py:59).
 // torch.argmax order: the first maximum wins; a NaN beats every number.
-// Grid (slices, rows): each block reduces one slice of a row, writes a
-// (value, index) partial, and the last block of the row merges them.
+// Grid (slices, rows): each block reduces one slice of a row to a (value,
+// index) partial; a one-block-per-row kernel merges the partials.
 #include "common.h"
 #include "kernels.h"
 
@@ -11,18 +11,13 @@ namespace {
 
 constexpr int SLICE = 256 * 16;  // elements per block
 
+// Block partial of one slice of a row: (value, index) into pv / pi [row][nb].
 template <typename T>
-__global__ __launch_bounds__(256) void argmax_kernel(const T* logits, int64_t ld, int64_t V, int64_t* out,
-                                                     int64_t out_stride, unsigned* counters, float* pv, int64_t* pi,
-                                                     const StepState* state, int64_t row_offset) {
-  if (state != nullptr) {
-    logits = (const T*)state->logits + row_offset;
-    out = state->next_tok;
-    out_stride = state->next_tok_ld;
-  }
+__global__ __launch_bounds__(256) void argmax_slice_kernel(const T* logits, int64_t ld, int64_t V, float* pv,
+                                                           int64_t* pi, const StepState* state, int64_t row_offset) {
+  if (state != nullptr) logits = (const T*)state->args.logits + row_offset;
   __shared__ float wv[4];
   __shared__ int64_t wi[4];
-  __shared__ bool last_block;
   const int64_t row = blockIdx.y, nb = gridDim.x;
   const T* lr = logits + row * ld;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -50,24 +45,33 @@ __global__ __launch_bounds__(256) void argmax_kernel(const T* logits, int64_t ld
       }
     pv[row * nb + blockIdx.x] = v;
     pi[row * nb + blockIdx.x] = i;
-    __threadfence();
-    last_block = atomicAdd(&counters[row], 1u) == (unsigned)nb - 1;
   }
-  __syncthreads();
-  if (!last_block) return;
-  __threadfence();
-  v = -__builtin_inff();
-  i = INT64_MAX;
+}
+
+// Winner of each row's nb partials (block = row). A separate launch: the
+// partials of the previous kernel are visible without a grid-wide fence,
+// which on a multi-XCD part writes back and invalidates L2 per block.
+__global__ __launch_bounds__(256) void argmax_merge_kernel(const float* pv, const int64_t* pi, int64_t nb,
+                                                           int64_t* out, int64_t out_stride, const StepState* state) {
+  if (state != nullptr) {
+    out = state->args.next_tok;
+    out_stride = state->args.next_tok_ld;
+  }
+  __shared__ float wv[4];
+  __shared__ int64_t wi[4];
+  const int64_t row = blockIdx.x;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float v = -__builtin_inff();
+  int64_t i = INT64_MAX;
   for (int64_t j = tid; j < nb; j += 256) {
-    const float x = __hip_atomic_load(&pv[row * nb + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    const int64_t xi = __hip_atomic_load(&pi[row * nb + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    const float x = pv[row * nb + j];
+    const int64_t xi = pi[row * nb + j];
     if (argmax_better(x, xi, v, i)) {
       v = x;
       i = xi;
     }
   }
   wave_argmax(v, i);
-  __syncthreads();
   if (lane == 0) {
     wv[wave] = v;
     wi[wave] = i;
@@ -80,7 +84,6 @@ __global__ __launch_bounds__(256) void argmax_kernel(const T* logits, int64_t ld
         i = wi[s];
       }
     if (out != nullptr) out[row * out_stride] = i;
-    counters[row] = 0u;
   }
 }
 
@@ -88,8 +91,14 @@ int64_t nslices(int64_t V) { return std::max<int64_t>(1, cdiv(V, SLICE)); }
 
 }  // namespace
 
-int64_t argmax_workspace_bytes(int64_t B, int64_t V) {
-  return cdiv(B * 4, 256) * 256 + B * nslices(V) * (4 + 8);
+int64_t argmax_workspace_bytes(int64_t B, int64_t V) { return B * nslices(V) * (4 + 8); }
+
+int launch_argmax_merge(hipStream_t st, const float* pv, const int64_t* pi, int64_t nb, int64_t rows, int64_t* out,
+                        int64_t out_stride, const StepState* state) {
+  if (rows == 0) return MINITP_OK;
+  argmax_merge_kernel<<<(unsigned)rows, 256, 0, st>>>(pv, pi, nb, out, out_stride, state);
+  MINITP_LAUNCH_CHECK();
+  return MINITP_OK;
 }
 
 int launch_argmax(hipStream_t st, int dtype, const void* logits, int64_t ld, int64_t B, int64_t V, int64_t* out,
@@ -105,21 +114,15 @@ int launch_argmax(hipStream_t st, int dtype, const void* logits, int64_t ld, int
     return MINITP_ERR_ARG;
   }
   const int64_t nb = nslices(V);
-  char* ws = (char*)workspace;
-  unsigned* counters = (unsigned*)ws;
-  ws += cdiv(B * 4, 256) * 256;
-  int64_t* pi = (int64_t*)ws;
-  ws += B * nb * 8;
-  float* pv = (float*)ws;
+  int64_t* pi = (int64_t*)workspace;
+  float* pv = (float*)(pi + B * nb);
   dim3 grid((unsigned)nb, (unsigned)B);
   if (dtype == MINITP_F32)
-    argmax_kernel<float><<<grid, 256, 0, st>>>((const float*)logits, ld, V, out, out_stride, counters, pv, pi,
-                                                 state, row_offset);
+    argmax_slice_kernel<float><<<grid, 256, 0, st>>>((const float*)logits, ld, V, pv, pi, state, row_offset);
   else
-    argmax_kernel<bf16><<<grid, 256, 0, st>>>((const bf16*)logits, ld, V, out, out_stride, counters, pv, pi,
-                                                state, row_offset);
+    argmax_slice_kernel<bf16><<<grid, 256, 0, st>>>((const bf16*)logits, ld, V, pv, pi, state, row_offset);
   MINITP_LAUNCH_CHECK();
-  return MINITP_OK;
+  return launch_argmax_merge(st, pv, pi, nb, B, out, out_stride, state);
 }
 
 }  // namespace minitp

@@ -11,8 +11,20 @@ namespace minitp {
 
 namespace {
 
-constexpr int CHUNK = 256;  // decode: key positions per block (one per thread)
-constexpr int GMAX = 8;     // max q heads per KV head served
+constexpr int GMAX = 8;  // max q heads per KV head served
+constexpr int NW = 8;    // waves per decode block
+
+// Decode geometry: a lane owns 8 consecutive elements of a key row, so LPR
+// lanes cover a row and one load instruction of a wave covers PPI rows. A
+// wave chunk is NI such loads (CP key positions).
+template <int D>
+struct DecodeGeom {
+  static constexpr int LPR = D / 8;
+  static constexpr int PPI = 64 / LPR;
+  static constexpr int NI = LPR < 8 ? LPR : 8;
+  static constexpr int CP = NI * PPI;
+  static constexpr int DUP = LPR / NI;  // lanes holding the same reduced score
+};
 
 struct DecodeArgs {
   const void* q;  // [B, Hq, D] (T == 1)
@@ -24,158 +36,306 @@ struct DecodeArgs {
   const StepState* st;
   int layer;
   float scale;
-  unsigned* counters;  // [B * Hkv]
-  float* ws_ml;        // [B * Hkv][nsplit][GMAX][2]
-  float* ws_o;         // [B * Hkv][nsplit][GMAX][D]
-  int nsplit_cap;
+  float* ws_ml;  // [B * Hkv][nsplit][GMAX][2]  (split partials, nsplit > 1)
+  float* ws_o;   // [B * Hkv][nsplit][GMAX][D]
 };
 
-template <typename T, int D>
-__global__ __launch_bounds__(256) void decode_attn_kernel(DecodeArgs a) {
-  constexpr int NPART = 256 / D;
-  __shared__ float qs[GMAX][D];
-  __shared__ float ps[GMAX][CHUNK];
-  __shared__ float stat[GMAX][2];  // max, sum
-  __shared__ float part[NPART > 1 ? NPART : 1][GMAX][D];
-  __shared__ bool last_block;
+// Value held by lane j ^ (2 * MK - 1) (rows of 16 lanes, DPP). Used for a
+// reduce-scatter whose masks fall from high to low: the bits above MK are
+// already equal between the two lanes and the bits below are still free.
+template <int MK>
+__device__ __forceinline__ float flip_low(float v) {
+  static_assert(MK == 1 || MK == 2 || MK == 4 || MK == 8, "mask within a row");
+  if constexpr (MK == 1) return dpp_f32<0xB1>(0.f, v);   // quad_perm [1,0,3,2]
+  if constexpr (MK == 2) return dpp_f32<0x1B>(0.f, v);   // quad_perm [3,2,1,0]
+  if constexpr (MK == 4) return dpp_f32<0x141>(0.f, v);  // row_half_mirror
+  if constexpr (MK == 8) return dpp_f32<0x140>(0.f, v);  // row_mirror
+}
+
+// Scores: v[r][h] holds this lane's partial dot for load r, head h. Sum over
+// the LPR lanes of a row, scattering r: afterwards v[0][h] is the full score
+// of load (lane % LPR) / DUP.
+template <int N, int MK, int GP>
+__device__ __forceinline__ void score_scatter(float (&v)[8][GP], int lane) {
+  if constexpr (MK >= 1) {
+    if constexpr (N > 1) {
+      const bool hi = lane & MK;
+#pragma unroll
+      for (int r = 0; r < N / 2; ++r)
+#pragma unroll
+        for (int h = 0; h < GP; ++h) {
+          const float keep = hi ? v[r + N / 2][h] : v[r][h];
+          const float send = hi ? v[r][h] : v[r + N / 2][h];
+          v[r][h] = keep + flip_low<MK>(send);
+        }
+      score_scatter<N / 2, MK / 2, GP>(v, lane);
+    } else {
+#pragma unroll
+      for (int h = 0; h < GP; ++h) v[0][h] += flip_low<MK>(v[0][h]);
+      score_scatter<1, MK / 2, GP>(v, lane);
+    }
+  }
+}
+
+// Output: a[h * 8 + e] is this lane's partial for head h, element e of its
+// slice. Sum over the lanes sharing the slice (lane masks MK, 2 MK, ... 32);
+// the first steps scatter the flat index, later ones (once one value is
+// left) are plain sums.
+template <int N, int MK, int NA>
+__device__ __forceinline__ void out_scatter(float (&a)[NA], int lane) {
+  if constexpr (MK < 64) {
+    if constexpr (N > 1) {
+      const bool hi = lane & MK;
+#pragma unroll
+      for (int i = 0; i < N / 2; ++i) {
+        const float keep = hi ? a[i + N / 2] : a[i];
+        const float send = hi ? a[i] : a[i + N / 2];
+        a[i] = keep + __shfl_xor(send, MK, 64);
+      }
+      out_scatter<N / 2, MK * 2, NA>(a, lane);
+    } else {
+      a[0] += __shfl_xor(a[0], MK, 64);
+      out_scatter<1, MK * 2, NA>(a, lane);
+    }
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ float dot8(const uint4 (&k)[sizeof(T) / 2], const T* q) {
+  if constexpr (sizeof(T) == 2) {
+    const uint4 qv = *reinterpret_cast<const uint4*>(q);
+    float acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, k[0].x),
+                                                __builtin_bit_cast(bf16x2_t, qv.x), 0.f, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, k[0].y), __builtin_bit_cast(bf16x2_t, qv.y),
+                                          acc, false);
+    acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, k[0].z), __builtin_bit_cast(bf16x2_t, qv.z),
+                                          acc, false);
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, k[0].w), __builtin_bit_cast(bf16x2_t, qv.w),
+                                           acc, false);
+  } else {
+    const float4 q0 = *reinterpret_cast<const float4*>(q);
+    const float4 q1 = *reinterpret_cast<const float4*>(q + 4);
+    float acc = __uint_as_float(k[0].x) * q0.x;
+    acc = fmaf(__uint_as_float(k[0].y), q0.y, acc);
+    acc = fmaf(__uint_as_float(k[0].z), q0.z, acc);
+    acc = fmaf(__uint_as_float(k[0].w), q0.w, acc);
+    acc = fmaf(__uint_as_float(k[1].x), q1.x, acc);
+    acc = fmaf(__uint_as_float(k[1].y), q1.y, acc);
+    acc = fmaf(__uint_as_float(k[1].z), q1.z, acc);
+    return fmaf(__uint_as_float(k[1].w), q1.w, acc);
+  }
+}
+
+template <typename T>
+__device__ __forceinline__ void unpack8(const uint4 (&v)[sizeof(T) / 2], float (&f)[8]) {
+  if constexpr (sizeof(T) == 2) {
+    unpack16(v[0], f, (bf16*)nullptr);
+  } else {
+    unpack16(v[0], f, (float*)nullptr);
+    unpack16(v[1], f + 4, (float*)nullptr);
+  }
+}
+
+// Orders LDS traffic between the lanes of one wave (no hardware barrier).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+// One block per (batch row, KV head, split, group of HP query heads). Its NW
+// waves take CP-position chunks of the cache in turn (chunk c goes to split
+// c % nsplit); each wave keeps an online softmax for its HP heads, so a wave
+// never waits on another until the end, where the waves merge through LDS.
+// Inside a chunk a lane loads 8 elements of NI key rows and of NI value rows
+// in one go (16-byte loads, a row spread over LPR lanes), reduces the scores
+// over the row's lanes with DPP, and reads the probabilities of the rows it
+// holds back from wave-private LDS for P V. A wave's VALU work per chunk
+// grows with HP: small batches run HP = 1 (more blocks, K/V re-read from
+// L2 per head), large ones the whole group (K/V read once).
+template <typename T, int D, int HP>
+__global__ __launch_bounds__(NW * 64) void decode_attn_kernel(DecodeArgs a) {
+  using Geo = DecodeGeom<D>;
+  constexpr int LPR = Geo::LPR, PPI = Geo::PPI, NI = Geo::NI, CP = Geo::CP, DUP = Geo::DUP;
+  constexpr int U = (int)sizeof(T) / 2;  // 16-byte loads per 8 elements
+  constexpr int NA = HP * 8;             // output partials per lane
+  __shared__ __attribute__((aligned(16))) T qs[HP][D];
+  __shared__ __attribute__((aligned(16))) float ps[NW][CP][HP];
+  __shared__ __attribute__((aligned(16))) float po[NW][HP][D];
+  __shared__ float pm[NW][HP], pl[NW][HP];
 
   const AttnShape& s = a.s;
   const int G = s.Hq / s.Hkv;
   const int bh = blockIdx.x, b = bh / s.Hkv, g = bh % s.Hkv;
-  const int64_t cache_len = a.st ? a.st->cache_len : a.cache_len;
-  const int64_t ctx = cache_len + 1;
-  const int64_t j0 = (int64_t)blockIdx.y * CHUNK;
-  if (j0 >= ctx) return;  // split beyond the filled cache (block-uniform)
-  const int64_t j1 = std::min<int64_t>(j0 + CHUNK, ctx);
-  const int nsplit = (int)cdiv(ctx, CHUNK);
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int split = blockIdx.y, nsplit = gridDim.y;
+  const int h0 = blockIdx.z * HP;  // first query head (within the group) of this block
+  const int nh = std::min(HP, G - h0);
+  const int64_t ctx = (a.st ? a.st->args.cache_len : a.cache_len) + 1;
+  const int64_t nchunk = cdiv(ctx, CP);
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int col = lane % LPR, grow = lane / LPR;
+  const int rbase = col / DUP;
+  const bool owner = col % DUP == 0;
 
   const int64_t layer_off = (int64_t)a.layer * s.B * s.Hkv * s.S * D;
-  const T* kc = (const T*)(a.st ? a.st->k_cache : a.k) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
-  const T* vc = (const T*)(a.st ? a.st->v_cache : a.v) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
-  const T* q = (const T*)a.q;
+  const T* kc = (const T*)(a.st ? a.st->args.k_cache : a.k) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
+  const T* vc = (const T*)(a.st ? a.st->args.v_cache : a.v) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
 
-  for (int i = tid; i < GMAX * D; i += 256) {
-    const int gi = i / D, d = i % D;
-    qs[gi][d] = gi < G ? load_f32<T>(q, ((int64_t)b * s.Hq + g * G + gi) * D + d) : 0.f;
+  {
+    const T* q = (const T*)a.q + ((int64_t)b * s.Hq + (int64_t)g * G + h0) * D;
+    for (int i = tid; i < HP * D; i += NW * 64) (&qs[0][0])[i] = i < nh * D ? q[i] : T{};
   }
   __syncthreads();
 
-  // scores: one key row per thread
-  {
-    float sc[GMAX];
+  float m[HP], lsum[HP], acc[NA];
 #pragma unroll
-    for (int gi = 0; gi < GMAX; ++gi) sc[gi] = 0.f;
-    const int64_t j = j0 + tid;
-    if (j < j1) {
-      constexpr int V = Vec<T>::N;
-      const uint4* kr = reinterpret_cast<const uint4*>(kc + j * D);
+  for (int h = 0; h < HP; ++h) {
+    m[h] = -__builtin_inff();
+    lsum[h] = 0.f;
+  }
 #pragma unroll
-      for (int c = 0; c < D / V; ++c) {
-        float kf[V];
-        unpack16(kr[c], kf, (T*)nullptr);
+  for (int i = 0; i < NA; ++i) acc[i] = 0.f;
+
+  for (int64_t c = (int64_t)w * nsplit + split; c < nchunk; c += (int64_t)NW * nsplit) {
+    const int64_t p0 = c * CP;
+    uint4 kr[NI][U], vr[NI][U];
 #pragma unroll
-        for (int gi = 0; gi < GMAX; ++gi)
+    for (int r = 0; r < NI; ++r) {
+      const int64_t pos = p0 + r * PPI + grow;
+      const bool ok = pos < ctx;
+      const uint4* kp = reinterpret_cast<const uint4*>(kc + pos * D + col * 8);
+      const uint4* vp = reinterpret_cast<const uint4*>(vc + pos * D + col * 8);
 #pragma unroll
-          for (int e = 0; e < V; ++e) sc[gi] = fmaf(qs[gi][c * V + e], kf[e], sc[gi]);
+      for (int u = 0; u < U; ++u) {
+        kr[r][u] = ok ? kp[u] : make_uint4(0, 0, 0, 0);
+        vr[r][u] = ok ? vp[u] : make_uint4(0, 0, 0, 0);
       }
     }
+    // scores of this lane's 8-element slices, summed across each row
+    float sc[8][HP];
 #pragma unroll
-    for (int gi = 0; gi < GMAX; ++gi) ps[gi][tid] = j < j1 ? sc[gi] * a.scale : -__builtin_inff();
-  }
-  __syncthreads();
-
-  // softmax statistics per head over this chunk (wave w takes heads w, w+4)
-  for (int gi = wave; gi < G; gi += 4) {
-    float mx = -__builtin_inff();
-    for (int i = lane; i < CHUNK; i += 64) mx = fmaxf(mx, ps[gi][i]);
-    mx = wave_max(mx);
-    float sum = 0.f;
-    for (int i = lane; i < CHUNK; i += 64) {
-      const float p = expf(ps[gi][i] - mx);
-      ps[gi][i] = p;
-      sum += p;
+    for (int r = 0; r < NI; ++r)
+#pragma unroll
+      for (int h = 0; h < HP; ++h) sc[r][h] = dot8<T>(kr[r], &qs[h][col * 8]);
+    score_scatter<NI, LPR / 2, HP>(sc, lane);
+    const int prow = rbase * PPI + grow;  // chunk row whose score this lane holds
+    const bool valid = p0 + prow < ctx;
+    float alpha[HP];
+#pragma unroll
+    for (int h = 0; h < HP; ++h) {
+      const float sv = valid ? sc[0][h] * a.scale : -__builtin_inff();
+      const float mn = fmaxf(m[h], wave_max(sv));  // finite: the chunk's first row is valid
+      alpha[h] = expf(m[h] - mn);
+      const float p = expf(sv - mn);
+      sc[0][h] = p;
+      lsum[h] = fmaf(lsum[h], alpha[h], owner ? p : 0.f);
+      m[h] = mn;
     }
-    sum = wave_sum(sum);
+    if (owner) {
+#pragma unroll
+      for (int h = 0; h < HP; ++h) ps[w][prow][h] = sc[0][h];
+    }
+    wave_lds_sync();
+#pragma unroll
+    for (int h = 0; h < HP; ++h)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[h * 8 + e] *= alpha[h];
+#pragma unroll
+    for (int r = 0; r < NI; ++r) {
+      float vf[8], pr[HP];
+      unpack8<T>(vr[r], vf);
+#pragma unroll
+      for (int h = 0; h < HP; ++h) pr[h] = ps[w][r * PPI + grow][h];
+#pragma unroll
+      for (int h = 0; h < HP; ++h)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[h * 8 + e] = fmaf(pr[h], vf[e], acc[h * 8 + e]);
+    }
+    wave_lds_sync();
+  }
+
+  // ---- wave results -> LDS ---------------------------------------------------
+  out_scatter<NA, LPR, NA>(acc, lane);
+  {
+    // flat indices [ibase, ibase + nv) survive in this lane
+    constexpr int STEPS = __builtin_ctz(PPI);
+    constexpr int SC = __builtin_ctz(NA) < STEPS ? __builtin_ctz(NA) : STEPS;
+    constexpr int NV = NA >> SC;
+    int ibase = 0;
+#pragma unroll
+    for (int j = 0; j < SC; ++j) ibase += ((grow >> j) & 1) * (NA >> (j + 1));
+    const bool out_owner = (grow >> SC) == 0;
+    if (out_owner) {
+#pragma unroll
+      for (int i = 0; i < NV; ++i) {
+        const int f = ibase + i, h = f / 8, e = f % 8;
+        po[w][h][col * 8 + e] = acc[i];
+      }
+    }
+  }
+#pragma unroll
+  for (int h = 0; h < HP; ++h) {
+    const float l = wave_sum(lsum[h]);
     if (lane == 0) {
-      stat[gi][0] = mx;
-      stat[gi][1] = sum;
+      pm[w][h] = m[h];
+      pl[w][h] = l;
     }
   }
   __syncthreads();
 
-  // P V: thread = (part, d); part p sums keys p, p + NPART, ...
-  {
-    const int d = tid % D, p = tid / D;
-    float acc[GMAX];
-#pragma unroll
-    for (int gi = 0; gi < GMAX; ++gi) acc[gi] = 0.f;
-    if (p < NPART) {
-      for (int64_t jj = p; jj < j1 - j0; jj += NPART) {
-        const float vv = load_f32<T>(vc, (j0 + jj) * D + d);
-#pragma unroll
-        for (int gi = 0; gi < GMAX; ++gi) acc[gi] = fmaf(ps[gi][jj], vv, acc[gi]);
-      }
-#pragma unroll
-      for (int gi = 0; gi < GMAX; ++gi) part[p][gi][d] = acc[gi];
-    }
-  }
-  __syncthreads();
-
+  // ---- merge the waves ---------------------------------------------------------
   T* out = (T*)a.out;
-  if (nsplit == 1) {
-    for (int i = tid; i < G * D; i += 256) {
-      const int gi = i / D, d = i % D;
-      float o = 0.f;
-      for (int p = 0; p < NPART; ++p) o += part[p][gi][d];
-      store_f32<T>(out, ((int64_t)b * s.Hq + g * G + gi) * D + d, o / stat[gi][1]);
-    }
-    return;
-  }
-
-  // split-K: publish partials; the last split of this (b, kv head) merges
-  const int64_t slot = (int64_t)bh * a.nsplit_cap + blockIdx.y;
-  for (int i = tid; i < G * D; i += 256) {
-    const int gi = i / D, d = i % D;
-    float o = 0.f;
-    for (int p = 0; p < NPART; ++p) o += part[p][gi][d];
-    a.ws_o[(slot * GMAX + gi) * D + d] = o;
-  }
-  if (tid < G) {
-    a.ws_ml[(slot * GMAX + tid) * 2 + 0] = stat[tid][0];
-    a.ws_ml[(slot * GMAX + tid) * 2 + 1] = stat[tid][1];
-  }
-  __threadfence();
-  __syncthreads();
-  if (tid == 0) {
-    const unsigned prev = atomicAdd(&a.counters[bh], 1u);
-    last_block = prev == (unsigned)nsplit - 1;
-  }
-  __syncthreads();
-  if (!last_block) return;
-  __threadfence();
-  for (int i = tid; i < G * D; i += 256) {
-    const int gi = i / D, d = i % D;
-    const int64_t base = (int64_t)bh * a.nsplit_cap;
+  for (int i = tid; i < nh * D; i += NW * 64) {
+    const int h = i / D, d = i % D;
     float mx = -__builtin_inff();
-    for (int sp = 0; sp < nsplit; ++sp)
-      mx = fmaxf(mx, __hip_atomic_load(&a.ws_ml[((base + sp) * GMAX + gi) * 2], __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT));
+#pragma unroll
+    for (int j = 0; j < NW; ++j) mx = fmaxf(mx, pm[j][h]);
+    float l = 0.f, o = 0.f;
+    if (mx != -__builtin_inff()) {
+#pragma unroll
+      for (int j = 0; j < NW; ++j) {
+        if (pm[j][h] == -__builtin_inff()) continue;  // wave saw no chunk
+        const float sc = expf(pm[j][h] - mx);
+        l = fmaf(sc, pl[j][h], l);
+        o = fmaf(sc, po[j][h][d], o);
+      }
+    }
+    if (nsplit == 1) {
+      store_f32<T>(out, ((int64_t)b * s.Hq + g * G + h0 + h) * D + d, o / l);
+    } else {
+      const int64_t slot = ((int64_t)bh * nsplit + split) * GMAX + h0 + h;
+      a.ws_o[slot * D + d] = o;
+      if (d == 0) {
+        a.ws_ml[slot * 2] = mx;
+        a.ws_ml[slot * 2 + 1] = l;
+      }
+    }
+  }
+}
+
+// Merge of the splits of each (batch row, KV head) (a separate launch, so
+// the partials are visible without any grid-wide fence).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a, int nsplit) {
+  const AttnShape& s = a.s;
+  const int G = s.Hq / s.Hkv;
+  const int bh = blockIdx.x, b = bh / s.Hkv, g = bh % s.Hkv;
+  T* out = (T*)a.out;
+  for (int i = threadIdx.x; i < G * D; i += 256) {
+    const int h = i / D, d = i % D;
+    float mx = -__builtin_inff();
+    for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, a.ws_ml[(((int64_t)bh * nsplit + sp) * GMAX + h) * 2]);
     float l = 0.f, o = 0.f;
     for (int sp = 0; sp < nsplit; ++sp) {
-      const float m_s = __hip_atomic_load(&a.ws_ml[((base + sp) * GMAX + gi) * 2], __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-      const float l_s = __hip_atomic_load(&a.ws_ml[((base + sp) * GMAX + gi) * 2 + 1], __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-      const float o_s = __hip_atomic_load(&a.ws_o[((base + sp) * GMAX + gi) * D + d], __ATOMIC_RELAXED,
-                                          __HIP_MEMORY_SCOPE_AGENT);
-      const float w = expf(m_s - mx);
-      l = fmaf(w, l_s, l);
-      o = fmaf(w, o_s, o);
+      const int64_t slot = ((int64_t)bh * nsplit + sp) * GMAX + h;
+      const float ms = a.ws_ml[slot * 2];
+      if (ms == -__builtin_inff()) continue;  // split saw no chunk
+      const float sc = expf(ms - mx);
+      l = fmaf(sc, a.ws_ml[slot * 2 + 1], l);
+      o = fmaf(sc, a.ws_o[slot * D + d], o);
     }
-    store_f32<T>(out, ((int64_t)b * s.Hq + g * G + gi) * D + d, o / l);
+    store_f32<T>(out, ((int64_t)b * s.Hq + g * G + h) * D + d, o / l);
   }
-  if (tid == 0) a.counters[bh] = 0u;
 }
 
 // ---------------------------------------------------------------------------
@@ -254,25 +414,41 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const T* q, const T* 
   }
 }
 
-template <typename T, int D>
-int decode_dispatch(hipStream_t st, DecodeArgs& a, int64_t max_ctx) {
-  const int nsplit = (int)cdiv(max_ctx, CHUNK);
-  hipLaunchKernelGGL((decode_attn_kernel<T, D>), dim3(a.s.B * a.s.Hkv, nsplit), dim3(256), 0, st, a);
+template <typename T, int D, int HP>
+int decode_launch(hipStream_t st, DecodeArgs& a, int nsplit) {
+  const int G = a.s.Hq / a.s.Hkv;
+  const dim3 grid(a.s.B * a.s.Hkv, nsplit, (unsigned)cdiv(G, HP));
+  hipLaunchKernelGGL((decode_attn_kernel<T, D, HP>), grid, dim3(NW * 64), 0, st, a);
   MINITP_LAUNCH_CHECK();
+  if (nsplit > 1) {
+    hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(a.s.B * a.s.Hkv), dim3(256), 0, st, a, nsplit);
+    MINITP_LAUNCH_CHECK();
+  }
   return MINITP_OK;
 }
 
+// Heads per wave: one while (batch rows x KV heads x splits) leaves most CUs
+// idle, else the whole group.
+template <typename T, int D>
+int decode_dispatch(hipStream_t st, DecodeArgs& a, int nsplit) {
+  const int G = a.s.Hq / a.s.Hkv;
+  if ((int64_t)a.s.B * a.s.Hkv * nsplit < 128 || G == 1) return decode_launch<T, D, 1>(st, a, nsplit);
+  if (G == 2) return decode_launch<T, D, 2>(st, a, nsplit);
+  if (G <= 4) return decode_launch<T, D, 4>(st, a, nsplit);
+  return decode_launch<T, D, 8>(st, a, nsplit);
+}
+
 template <typename T>
-int decode_by_d(hipStream_t st, DecodeArgs& a, int64_t max_ctx) {
+int decode_by_d(hipStream_t st, DecodeArgs& a, int nsplit) {
   switch (a.s.D) {
     case 16:
-      return decode_dispatch<T, 16>(st, a, max_ctx);
+      return decode_dispatch<T, 16>(st, a, nsplit);
     case 32:
-      return decode_dispatch<T, 32>(st, a, max_ctx);
+      return decode_dispatch<T, 32>(st, a, nsplit);
     case 64:
-      return decode_dispatch<T, 64>(st, a, max_ctx);
+      return decode_dispatch<T, 64>(st, a, nsplit);
     case 128:
-      return decode_dispatch<T, 128>(st, a, max_ctx);
+      return decode_dispatch<T, 128>(st, a, nsplit);
   }
   set_error("attention: head_dim %d not supported (16, 32, 64, 128)", a.s.D);
   return MINITP_ERR_UNSUPPORTED;
@@ -305,16 +481,23 @@ int prefill_by_d(hipStream_t st, const void* q, const void* k, const void* v, vo
   return MINITP_ERR_UNSUPPORTED;
 }
 
-int64_t decode_nsplit(int64_t S) { return cdiv(std::max<int64_t>(S, 1), CHUNK); }
+// Blocks per (b, KV head) for contexts up to `ctx`: one while each wave has
+// at most four chunks to walk, more (up to about one block per CU overall)
+// beyond that.
+int64_t decode_nsplit(int64_t units, int64_t ctx, int64_t D) {
+  const int64_t cp = D >= 128 ? 32 : 64;
+  const int64_t chunks = cdiv(std::max<int64_t>(ctx, 1), cp);
+  const int64_t want = cdiv(chunks, 4 * NW);
+  return std::max<int64_t>(1, std::min<int64_t>(want, std::max<int64_t>(1, 256 / std::max<int64_t>(units, 1))));
+}
 
 }  // namespace
 
 int64_t attention_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t S) {
   (void)T;
   (void)Hq;
-  const int64_t units = B * Hkv, ns = decode_nsplit(S);
-  const int64_t counters = cdiv(units * 4, 256) * 256;
-  return counters + units * ns * GMAX * 2 * 4 + units * ns * GMAX * D * 4;
+  const int64_t units = B * Hkv, ns = decode_nsplit(units, S, D);
+  return units * ns * GMAX * 2 * 4 + units * ns * GMAX * D * 4;
 }
 
 int launch_decode_attention(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,
@@ -329,6 +512,7 @@ int launch_decode_attention(hipStream_t st, int dtype, const void* q, const void
     set_error("attention: workspace %lld B < %lld B", (long long)workspace_bytes, (long long)need);
     return MINITP_ERR_ARG;
   }
+  if (s.B == 0) return MINITP_OK;
   DecodeArgs a;
   a.q = q;
   a.k = k_cache;
@@ -340,16 +524,11 @@ int launch_decode_attention(hipStream_t st, int dtype, const void* q, const void
   a.layer = layer;
   a.scale = 1.0f / sqrtf((float)s.D);
   const int64_t units = (int64_t)s.B * s.Hkv;
-  a.nsplit_cap = (int)decode_nsplit(s.S);
-  char* ws = (char*)workspace;
-  a.counters = (unsigned*)ws;
-  ws += cdiv(units * 4, 256) * 256;
-  a.ws_ml = (float*)ws;
-  ws += units * a.nsplit_cap * GMAX * 2 * 4;
-  a.ws_o = (float*)ws;
   // graph replays size the grid for a full cache; direct calls for this step
-  const int64_t max_ctx = state ? s.S : cache_len + 1;
-  return dtype == MINITP_F32 ? decode_by_d<float>(st, a, max_ctx) : decode_by_d<bf16>(st, a, max_ctx);
+  const int nsplit = (int)decode_nsplit(units, state ? s.S : cache_len + 1, s.D);
+  a.ws_ml = (float*)workspace;
+  a.ws_o = a.ws_ml + units * nsplit * GMAX * 2;
+  return dtype == MINITP_F32 ? decode_by_d<float>(st, a, nsplit) : decode_by_d<bf16>(st, a, nsplit);
 }
 
 int launch_prefill_attention(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,

@@ -17,6 +17,8 @@ namespace minitp {
 struct bf16 {
   uint16_t bits;
 };
+// Operand type of the packed bf16 dot instructions.
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
@@ -61,11 +63,19 @@ struct Vec<float> {
   static constexpr int N = 4;
 };
 
-// Streaming 16-byte load (weights are read once per step: non-temporal).
+// 16-byte weight load. Weights are read once per step; MINITP_NT_LOADS=1
+// marks the loads non-temporal (a cache-policy hint), 0 issues plain loads.
+#ifndef MINITP_NT_LOADS
+#define MINITP_NT_LOADS 1
+#endif
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ uint4 load_stream16(const uint4* p) {
+#if MINITP_NT_LOADS
   u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
   return make_uint4(v.x, v.y, v.z, v.w);
+#else
+  return *p;
+#endif
 }
 
 __device__ __forceinline__ void unpack16(const uint4& v, float* out, bf16*) {
@@ -106,17 +116,47 @@ __device__ __forceinline__ float swiglu(float g, float u) {
 }
 
 // ---------------------------------------------------------------------------
-// Wave64 reductions (butterfly; every lane ends with the result).
+// Wave64 reductions on DPP (data-parallel primitives run in the VALU, no LDS
+// crossbar): an inclusive row scan with row_shr 1/2/4/8 leaves each 16-lane
+// row's total in its lane 15, row_bcast15 / row_bcast31 fold the rows into
+// lane 63, and readlane broadcasts it. Masked-off rows and out-of-row sources
+// read `identity`, so they contribute nothing.
+template <int CTRL, int ROW_MASK = 0xf, int BANK_MASK = 0xf>
+__device__ __forceinline__ float dpp_f32(float identity, float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(__builtin_bit_cast(int, identity),
+                                                               __builtin_bit_cast(int, v), CTRL, ROW_MASK,
+                                                               BANK_MASK, false));
+}
+
 __device__ __forceinline__ float wave_sum(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  v += dpp_f32<0x111>(0.f, v);          // row_shr:1
+  v += dpp_f32<0x112>(0.f, v);          // row_shr:2
+  v += dpp_f32<0x114>(0.f, v);          // row_shr:4
+  v += dpp_f32<0x118>(0.f, v);          // row_shr:8
+  v += dpp_f32<0x142, 0xa>(0.f, v);     // row_bcast:15 into rows 1, 3
+  v += dpp_f32<0x143, 0xc>(0.f, v);     // row_bcast:31 into rows 2, 3
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
 }
+
 __device__ __forceinline__ float wave_max(float v) {
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  const float ninf = -__builtin_inff();
+  v = fmaxf(v, dpp_f32<0x111>(ninf, v));
+  v = fmaxf(v, dpp_f32<0x112>(ninf, v));
+  v = fmaxf(v, dpp_f32<0x114>(ninf, v));
+  v = fmaxf(v, dpp_f32<0x118>(ninf, v));
+  v = fmaxf(v, dpp_f32<0x142, 0xa>(ninf, v));
+  v = fmaxf(v, dpp_f32<0x143, 0xc>(ninf, v));
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), 63));
+}
+
+// Sum over aligned groups of 4 lanes (quad_perm xor 1, xor 2); every lane of
+// the group ends with the group total.
+__device__ __forceinline__ float quad_sum(float v) {
+  v += dpp_f32<0xB1>(0.f, v);  // quad_perm [1,0,3,2]
+  v += dpp_f32<0x4E>(0.f, v);  // quad_perm [2,3,0,1]
   return v;
 }
+__device__ __forceinline__ float pair_sum(float v) { return v + dpp_f32<0xB1>(0.f, v); }
 
 // torch.argmax order: NaN beats any number; equal values (and two NaNs)
 // resolve to the smaller index.

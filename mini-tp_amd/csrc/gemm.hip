@@ -54,7 +54,7 @@ template <typename T, int EPI>
 __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ x, int64_t ldx, const T* __restrict__ w,
                                                    const T* __restrict__ bias, T* y, int64_t ldy, const T* aux,
                                                    int64_t M, int64_t N, int64_t K, const StepState* state) {
-  if (state != nullptr) y = (T*)state->logits;
+  if (state != nullptr) y = (T*)state->args.logits;
   __shared__ __attribute__((aligned(16))) char As[BM * ROWB];
   __shared__ __attribute__((aligned(16))) char Bs[BN * ROWB];
   constexpr int V = Vec<T>::N;              // elements per 16 B

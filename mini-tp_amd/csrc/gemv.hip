@@ -1,17 +1,24 @@
 // Decode GEMV: y = epilogue(x W^T) for M <= 4 input rows, streaming W once.
 //
-// Layout and mapping (wave64, 256-thread blocks = 4 waves):
-//  * The M input rows (optionally RMSNorm-ed, rounded to the model dtype
-//    exactly as layer.py:39-42 rounds) are staged in LDS as fp32.
-//  * Work unit = a "tuple" of 2P weight rows: P pairs (row_a + p, row_b + p).
+// Mapping (wave64, 256-thread blocks = 4 waves):
+//  * Work unit = a "tuple" of 2P weight rows, P pairs (row_a + p, row_b + p).
 //    The pairing lets an epilogue see two rows at once: SwiGLU pairs gate
 //    row j with up row I + j (mlp.py:38), RoPE pairs head dims i and
 //    i + D/2 (rope.py:57-62); plain stores use 2P contiguous rows.
-//  * KSPLIT waves of a block share one tuple and split K; the block holds
+//  * KSPLIT waves of a block share one tuple and split K; a block holds
 //    4 / KSPLIT tuples and walks the tuple space with a grid stride.
-//  * Each lane streams 16-byte chunks of every row of the tuple (coalesced:
-//    consecutive lanes read consecutive 16 B of a row), accumulates in fp32,
-//    then a butterfly reduces across the wave and LDS across the K-split.
+//  * Lane l of K-split wave kw owns the 16-byte chunks c = kw*64 + l +
+//    j*64*KSPLIT of every row: consecutive lanes read consecutive 16 B, so a
+//    wave-load is one contiguous 1 KiB of a row.
+//
+// gemv_reg_kernel (rows up to 1024 chunks of 16 B, i.e. K <= 8192 bf16) is
+// built for latency, which is what decode at these sizes is bound by: the
+// first tuple's weight loads are issued before anything else; the input
+// row(s), the RMSNorm weight and the epilogue's side inputs (RoPE table
+// entries, residual) load underneath them; the input stays in registers (no
+// LDS staging, no barrier unless K is split across waves); and each tuple
+// prefetches the next tuple's weights before its own reduction and epilogue.
+// gemv_lds_kernel stages the input in LDS and serves longer rows.
 #include "common.h"
 #include "kernels.h"
 
@@ -21,8 +28,10 @@ namespace {
 
 constexpr int P = 2;  // pairs per tuple (R = 4 rows)
 constexpr int R = 2 * P;
-constexpr int U = 2;  // chunk unroll: U * R 16-byte loads in flight per lane
+constexpr int U = 2;  // gemv_lds_kernel chunk unroll
 constexpr int MAX_GRID = 2048;
+constexpr int64_t REG_MAX_CHUNKS = 1024;
+
 
 template <int EPI>
 __device__ __forceinline__ void tuple_rows(int64_t t, const GemvArgs& a, int64_t& ra, int64_t& rb) {
@@ -42,7 +51,7 @@ __device__ __forceinline__ void tuple_rows(int64_t t, const GemvArgs& a, int64_t
 }
 
 template <int EPI>
-__device__ __forceinline__ int64_t num_tuples(const GemvArgs& a) {
+__host__ __device__ __forceinline__ int64_t num_tuples(const GemvArgs& a) {
   if constexpr (EPI == EPI_SWIGLU) return a.N / P;
   if constexpr (EPI == EPI_QKV_ROPE) return (int64_t)(a.a.Hq + 2 * a.a.Hkv) * (a.a.D / 2) / P;
   return cdiv(a.N, R);
@@ -55,14 +64,378 @@ __device__ __forceinline__ bool row_valid(int64_t r, const GemvArgs& a) {
   return true;
 }
 
+// acc += <w chunk, x chunk> for one 16-byte chunk: fp32 FMAs, or for bf16
+// the packed-pair dot product v_dot2_f32_bf16 (fp32 accumulate).
+template <typename T>
+__device__ __forceinline__ float dot_chunk(const uint4& w, const float* xf, const uint4& xb, float acc);
+template <>
+__device__ __forceinline__ float dot_chunk<float>(const uint4& w, const float* xf, const uint4&, float acc) {
+  acc = fmaf(__uint_as_float(w.x), xf[0], acc);
+  acc = fmaf(__uint_as_float(w.y), xf[1], acc);
+  acc = fmaf(__uint_as_float(w.z), xf[2], acc);
+  return fmaf(__uint_as_float(w.w), xf[3], acc);
+}
+template <>
+__device__ __forceinline__ float dot_chunk<bf16>(const uint4& w, const float*, const uint4& xb, float acc) {
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.x), __builtin_bit_cast(bf16x2_t, xb.x), acc,
+                                        false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.y), __builtin_bit_cast(bf16x2_t, xb.y), acc,
+                                        false);
+  acc = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.z), __builtin_bit_cast(bf16x2_t, xb.z), acc,
+                                        false);
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w.w), __builtin_bit_cast(bf16x2_t, xb.w), acc,
+                                         false);
+}
+
+__device__ __forceinline__ uint4 pack_bf16x8(const float* f) {
+  uint4 r;
+  r.x = (uint32_t)f32_to_bf16(f[0]) | ((uint32_t)f32_to_bf16(f[1]) << 16);
+  r.y = (uint32_t)f32_to_bf16(f[2]) | ((uint32_t)f32_to_bf16(f[3]) << 16);
+  r.z = (uint32_t)f32_to_bf16(f[4]) | ((uint32_t)f32_to_bf16(f[5]) << 16);
+  r.w = (uint32_t)f32_to_bf16(f[6]) | ((uint32_t)f32_to_bf16(f[7]) << 16);
+  return r;
+}
+
+// Epilogue side inputs a lane needs for pair ep of row em of tuple rows[]:
+// RoPE: cos/sin of both rows (single-token forwards read the rows the first
+// kernel copied into the StepState); RESID: both residual values.
+template <typename T, int EPI>
+__device__ __forceinline__ void load_side(const GemvArgs& a, int em, int ep, const int64_t* rows, const bool* rok,
+                                          int64_t pos, float* side) {
+  if constexpr (EPI == EPI_QKV_ROPE) {
+    const int D = a.a.D;
+    const int64_t head = rows[ep] / D;
+    if (head < a.a.Hq + a.a.Hkv) {
+      const int i = (int)(rows[ep] % D);
+      if (a.a.T == 1) {
+        side[0] = a.st->rope_cos[i];
+        side[1] = a.st->rope_sin[i];
+        side[2] = a.st->rope_cos[i + D / 2];
+        side[3] = a.st->rope_sin[i + D / 2];
+      } else if (pos >= 0 && pos < a.max_pos) {
+        side[0] = a.cos_tab[pos * D + i];
+        side[1] = a.sin_tab[pos * D + i];
+        side[2] = a.cos_tab[pos * D + i + D / 2];
+        side[3] = a.sin_tab[pos * D + i + D / 2];
+      }
+    }
+  } else if constexpr (EPI == EPI_RESID) {
+    const T* aux = (const T*)a.aux;
+    if (rok[ep]) side[0] = load_f32<T>(aux, em * a.ldy + rows[ep]);
+    if (rok[P + ep]) side[1] = load_f32<T>(aux, em * a.ldy + rows[P + ep]);
+  }
+}
+
+// Epilogue of one (row m, pair) for the non-argmax epilogues.
+template <typename T, int EPI>
+__device__ __forceinline__ void finish_pair(const GemvArgs& a, int m, int64_t row_a, int64_t row_b, bool oka,
+                                            bool okb, float va, float vb, const float* side, int64_t pos) {
+  if constexpr (EPI == EPI_STORE) {
+    T* y = (T*)a.y;
+    const T* bias = (const T*)a.bias;
+    if (oka) store_f32<T>(y, m * a.ldy + row_a, va + (bias ? load_f32<T>(bias, row_a) : 0.f));
+    if (okb) store_f32<T>(y, m * a.ldy + row_b, vb + (bias ? load_f32<T>(bias, row_b) : 0.f));
+  } else if constexpr (EPI == EPI_RESID) {
+    T* y = (T*)a.y;
+    if (oka) store_f32<T>(y, m * a.ldy + row_a, add_rn(side[0], round_to<T>(va)));
+    if (okb) store_f32<T>(y, m * a.ldy + row_b, add_rn(side[1], round_to<T>(vb)));
+  } else if constexpr (EPI == EPI_SWIGLU) {
+    store_f32<T>((T*)a.y, m * a.ldy + row_a, swiglu<T>(round_to<T>(va), round_to<T>(vb)));
+  } else if constexpr (EPI == EPI_QKV_ROPE) {
+    const T* bias = (const T*)a.bias;
+    // F.linear output with bias, rounded to the dtype (fused.py:58)
+    va = round_to<T>(va + load_f32<T>(bias, row_a));
+    vb = round_to<T>(vb + load_f32<T>(bias, row_b));
+    const StepState* st = a.st;
+    const AttnShape& s = a.a;
+    const int D = s.D, half = D / 2;
+    const int64_t head = row_a / D;
+    const int i = (int)(row_a % D);
+    const int b = m / s.T, tt = m % s.T;
+    if (head < s.Hq + s.Hkv) {
+      // rotate(x) = x * cos + rotate_half(x) * sin in fp32, each multiply
+      // and the add rounded separately, then cast (rope.py:61-62)
+      float oa, ob;
+      if (s.T > 1 && (pos < 0 || pos >= a.max_pos)) {
+        oa = ob = __builtin_nanf("");
+        ((StepState*)st)->error = 1;
+      } else {
+        oa = add_rn(mul_rn(va, side[0]), -mul_rn(vb, side[1]));
+        ob = add_rn(mul_rn(vb, side[2]), mul_rn(va, side[3]));
+      }
+      if (head < s.Hq) {
+        T* q = (T*)a.y;  // [B, T, Hq, D]
+        const int64_t base = ((int64_t)m * s.Hq + head) * D;
+        store_f32<T>(q, base + i, oa);
+        store_f32<T>(q, base + i + half, ob);
+      } else {
+        T* kc = (T*)st->args.k_cache + (int64_t)a.layer * s.B * s.Hkv * s.S * D;
+        const int64_t base = (((int64_t)b * s.Hkv + (head - s.Hq)) * s.S + st->args.cache_len + tt) * D;
+        store_f32<T>(kc, base + i, oa);
+        store_f32<T>(kc, base + i + half, ob);
+      }
+    } else {
+      T* vc = (T*)st->args.v_cache + (int64_t)a.layer * s.B * s.Hkv * s.S * D;
+      const int64_t base = (((int64_t)b * s.Hkv + (head - s.Hq - s.Hkv)) * s.S + st->args.cache_len + tt) * D;
+      store_f32<T>(vc, base + i, va);
+      store_f32<T>(vc, base + i + half, vb);
+    }
+  }
+}
+
+// LM-head argmax: each block publishes its best (value, index) per row into
+// part_val / part_idx [m][block]; argmax_merge_kernel (a separate launch)
+// picks the winner. The order of a (value, index) comparison under
+// argmax_better is total, so the merge order cannot change the winner.
+template <int MM, int SLOTS>
+__device__ __forceinline__ void argmax_finish(const GemvArgs& a, int M, int slot, int kw, const float* bv,
+                                              const int64_t* bi, float (*best_v)[MM], int64_t (*best_i)[MM]) {
+  const int tid = threadIdx.x, lane = tid & 63;
+  if (kw == 0 && lane == 0) {
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      best_v[slot][m] = bv[m];
+      best_i[slot][m] = bi[m];
+    }
+  }
+  __syncthreads();
+  if (tid < M) {
+    const int m = tid;
+    float v = best_v[0][m];
+    int64_t i = best_i[0][m];
+    for (int s = 1; s < SLOTS; ++s)
+      if (argmax_better(best_v[s][m], best_i[s][m], v, i)) {
+        v = best_v[s][m];
+        i = best_i[s][m];
+      }
+    a.part_val[(int64_t)m * gridDim.x + blockIdx.x] = v;
+    a.part_idx[(int64_t)m * gridDim.x + blockIdx.x] = i;
+  }
+}
+
+template <typename T, int MM, int KSPLIT, int JMAX, int PRO, int EPI>
+__global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
+  constexpr int V = Vec<T>::N;
+  constexpr int SLOTS = 4 / KSPLIT;
+  __shared__ float red[4][MM * R];
+  __shared__ float nrm[4][MM];
+  __shared__ float best_v[4][MM];
+  __shared__ int64_t best_i[4][MM];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kw = wave % KSPLIT, slot = wave / KSPLIT;
+  const int M = (int)a.M;
+  const int64_t nchunk = a.K / V;
+  const int64_t ntup = num_tuples<EPI>(a);
+  const int64_t tstride = (int64_t)gridDim.x * SLOTS;
+  const uint4* W = (const uint4*)a.w;
+
+  // Load order matters: vector loads retire in issue order, so everything
+  // the prologue consumes (input rows, RMSNorm weight, epilogue side inputs)
+  // is requested before the weights; the norm math then overlaps the weight
+  // loads still in flight.
+  int64_t t = (int64_t)blockIdx.x * SLOTS + slot;
+  int64_t rows[R];
+  bool rok[R];
+  uint4 wv[JMAX][R];
+  auto set_rows = [&](int64_t tt) {
+    int64_t ra = 0, rb = 0;
+    const bool ok = tt < ntup;
+    if (ok) tuple_rows<EPI>(tt, a, ra, rb);
+#pragma unroll
+    for (int p = 0; p < P; ++p) {
+      rows[p] = ra + p;
+      rows[P + p] = rb + p;
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) rok[r] = ok && row_valid<EPI>(rows[r], a);
+  };
+  auto load_w = [&]() {
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) {
+      const int64_t c = (int64_t)kw * 64 + lane + (int64_t)j * 64 * KSPLIT;
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+        wv[j][r] = (rok[r] && c < nchunk) ? load_stream16(W + rows[r] * nchunk + c) : make_uint4(0, 0, 0, 0);
+    }
+  };
+  set_rows(t);
+
+  // ---- 1. input rows and RMSNorm weight ---------------------------------------
+  const T* x = (const T*)a.x;
+  float xf[MM][JMAX][V];
+  uint4 xb[MM][JMAX];
+  uint4 nw[JMAX];
+#pragma unroll
+  for (int j = 0; j < JMAX; ++j) {
+    const int64_t c = (int64_t)kw * 64 + lane + (int64_t)j * 64 * KSPLIT;
+    nw[j] = (PRO == PRO_NORM && c < nchunk) ? *reinterpret_cast<const uint4*>((const T*)a.norm_w + c * V)
+                                            : make_uint4(0, 0, 0, 0);
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+      xb[m][j] = (m < M && c < nchunk) ? *reinterpret_cast<const uint4*>(x + m * a.ldx + c * V)
+                                       : make_uint4(0, 0, 0, 0);
+  }
+
+  // ---- 2. the epilogue's side inputs for the first tuple -----------------------
+  const int em = lane / P, ep = lane % P;  // this lane finishes pair ep of row em
+  float side[4] = {0.f, 0.f, 0.f, 0.f};
+  int64_t pos = 0;
+  if constexpr (EPI == EPI_QKV_ROPE) {
+    if (em < M && a.a.T > 1) pos = a.st->args.positions[em % a.a.T];
+  }
+  if (em < M && t < ntup) load_side<T, EPI>(a, em, ep, rows, rok, pos, side);
+
+  // ---- 3. the first tuple's weights -----------------------------------------
+  load_w();
+
+  // ---- 4. input rows in registers (normed and rounded like layer.py:39-42) --
+#pragma unroll
+  for (int m = 0; m < MM; ++m)
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) unpack16(xb[m][j], xf[m][j], (T*)nullptr);
+  if constexpr (PRO == PRO_NORM) {
+    float tot[MM];
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      float ss = 0.f;
+#pragma unroll
+      for (int j = 0; j < JMAX; ++j)
+#pragma unroll
+        for (int e = 0; e < V; ++e) ss = add_rn(ss, mul_rn(xf[m][j][e], xf[m][j][e]));
+      tot[m] = wave_sum(ss);
+    }
+    if constexpr (KSPLIT > 1) {
+      if (lane == 0)
+#pragma unroll
+        for (int m = 0; m < MM; ++m) nrm[wave][m] = tot[m];
+      __syncthreads();
+#pragma unroll
+      for (int m = 0; m < MM; ++m) {
+        float s = 0.f;
+        for (int k = 0; k < KSPLIT; ++k) s += nrm[slot * KSPLIT + k][m];
+        tot[m] = s;
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < MM; ++m) {
+      const float r = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(tot[m], (float)a.K), a.eps)));
+#pragma unroll
+      for (int j = 0; j < JMAX; ++j) {
+        float wf[V];
+        unpack16(nw[j], wf, (T*)nullptr);
+#pragma unroll
+        for (int e = 0; e < V; ++e) xf[m][j][e] = m < M ? round_to<T>(mul_rn(mul_rn(xf[m][j][e], r), wf[e])) : 0.f;
+        if constexpr (sizeof(T) == 2) xb[m][j] = pack_bf16x8(xf[m][j]);
+      }
+    }
+  }
+
+  float bv[MM];
+  int64_t bi[MM];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    bv[m] = -__builtin_inff();
+    bi[m] = INT64_MAX;
+  }
+
+  // ---- 5. tuples (grid stride), next tuple's weights prefetched -----------
+  for (int64_t t0 = (int64_t)blockIdx.x * SLOTS; t0 < ntup; t0 += tstride) {
+    float acc[MM][R];
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float s = 0.f;
+#pragma unroll
+        for (int j = 0; j < JMAX; ++j) s = dot_chunk<T>(wv[j][r], xf[m][j], xb[m][j], s);
+        acc[m][r] = s;
+      }
+    const int64_t cur_t = t;
+    int64_t cur_rows[R];
+    bool cur_ok[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      cur_rows[r] = rows[r];
+      cur_ok[r] = rok[r];
+    }
+    t += tstride;
+    if (t0 + tstride < ntup) {
+      set_rows(t);
+      load_w();
+    }
+
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+      for (int r = 0; r < R; ++r) acc[m][r] = wave_sum(acc[m][r]);
+    if constexpr (KSPLIT > 1) {
+      if (lane == 0) {
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+#pragma unroll
+          for (int r = 0; r < R; ++r) red[wave][m * R + r] = acc[m][r];
+      }
+      __syncthreads();
+      if (kw == 0) {
+#pragma unroll
+        for (int m = 0; m < MM; ++m)
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            float s = red[wave][m * R + r];
+            for (int k = 1; k < KSPLIT; ++k) s += red[wave + k][m * R + r];
+            acc[m][r] = s;
+          }
+      }
+      __syncthreads();
+    }
+
+    if (kw != 0 || cur_t >= ntup) continue;
+    if constexpr (EPI == EPI_ARGMAX) {
+      T* logits = (T*)a.st->args.logits;
+#pragma unroll
+      for (int m = 0; m < MM; ++m) {
+        if (m < M) {
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            if (cur_ok[r]) {
+              const float v = round_to<T>(acc[m][r]);
+              if (logits != nullptr && lane == m * R + r) store_f32<T>(logits, m * a.N + cur_rows[r], v);
+              if (argmax_better(v, cur_rows[r], bv[m], bi[m])) {
+                bv[m] = v;
+                bi[m] = cur_rows[r];
+              }
+            }
+          }
+        }
+      }
+    } else if (em < M) {
+      float va = 0.f, vb = 0.f;
+#pragma unroll
+      for (int m = 0; m < MM; ++m)
+#pragma unroll
+        for (int p = 0; p < P; ++p)
+          if (m == em && p == ep) {
+            va = acc[m][p];
+            vb = acc[m][P + p];
+          }
+      if (cur_t != (int64_t)blockIdx.x * SLOTS + slot) load_side<T, EPI>(a, em, ep, cur_rows, cur_ok, pos, side);
+      finish_pair<T, EPI>(a, em, cur_rows[ep], cur_rows[P + ep], cur_ok[ep], cur_ok[P + ep], va, vb, side, pos);
+    }
+  }
+  if constexpr (EPI == EPI_ARGMAX) argmax_finish<MM, SLOTS>(a, M, slot, kw, bv, bi, best_v, best_i);
+}
+
+// ---------------------------------------------------------------------------
+// gemv_lds_kernel: the input rows staged in LDS (any K that fits), for rows
+// longer than the register path serves.
 template <typename T, int MM, int KSPLIT, int PRO, int EPI>
-__global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
+__global__ __launch_bounds__(256) void gemv_lds_kernel(GemvArgs a) {
   extern __shared__ float xs[];  // [MM][K]
   __shared__ float red[4][MM * R];
   __shared__ float nrm[4][MM];
   __shared__ float best_v[4][MM];
   __shared__ int64_t best_i[4][MM];
-  __shared__ bool last_block;
 
   constexpr int V = Vec<T>::N;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -206,7 +579,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
       if constexpr (EPI == EPI_ARGMAX) {
         // every lane holds the tuple totals; fold them into the running best
         const int64_t ld = a.N;
-        T* logits = (T*)a.st->logits;
+        T* logits = (T*)a.st->args.logits;
 #pragma unroll
         for (int m = 0; m < MM; ++m) {
           if (m < M) {
@@ -260,7 +633,7 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
                 if (head < s.Hq + s.Hkv) {
                   // rotate(x) = x * cos + rotate_half(x) * sin, fp32, each op
                   // rounded, then cast (rope.py:61-62)
-                  const int64_t pos = st->positions[tt];
+                  const int64_t pos = st->args.positions[tt];
                   float oa, ob;
                   if (pos < 0 || pos >= a.max_pos) {
                     oa = ob = __builtin_nanf("");
@@ -278,15 +651,15 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
                     store_f32<T>(q, base + i + half, ob);
                   } else {
                     const int64_t g = head - s.Hq;
-                    T* kc = (T*)st->k_cache + (int64_t)a.layer * s.B * s.Hkv * s.S * D;
-                    const int64_t base = (((int64_t)b * s.Hkv + g) * s.S + st->cache_len + tt) * D;
+                    T* kc = (T*)st->args.k_cache + (int64_t)a.layer * s.B * s.Hkv * s.S * D;
+                    const int64_t base = (((int64_t)b * s.Hkv + g) * s.S + st->args.cache_len + tt) * D;
                     store_f32<T>(kc, base + i, oa);
                     store_f32<T>(kc, base + i + half, ob);
                   }
                 } else {
                   const int64_t g = head - s.Hq - s.Hkv;
-                  T* vc = (T*)st->v_cache + (int64_t)a.layer * s.B * s.Hkv * s.S * D;
-                  const int64_t base = (((int64_t)b * s.Hkv + g) * s.S + st->cache_len + tt) * D;
+                  T* vc = (T*)st->args.v_cache + (int64_t)a.layer * s.B * s.Hkv * s.S * D;
+                  const int64_t base = (((int64_t)b * s.Hkv + g) * s.S + st->args.cache_len + tt) * D;
                   store_f32<T>(vc, base + i, va);
                   store_f32<T>(vc, base + i + half, vb);
                 }
@@ -298,104 +671,53 @@ __global__ __launch_bounds__(256) void gemv_kernel(GemvArgs a) {
     }
   }
 
-  if constexpr (EPI == EPI_ARGMAX) {
-    // block partial per row m (slots in wave order, then tuples ascending
-    // inside each wave, so ties still resolve to the smallest index)
-    if (kw == 0 && lane == 0) {
-#pragma unroll
-      for (int m = 0; m < MM; ++m) {
-        best_v[slot][m] = bv[m];
-        best_i[slot][m] = bi[m];
-      }
-    }
-    __syncthreads();
-    if (tid == 0) {
-      for (int m = 0; m < M; ++m) {
-        float v = best_v[0][m];
-        int64_t i = best_i[0][m];
-        for (int s = 1; s < SLOTS; ++s)
-          if (argmax_better(best_v[s][m], best_i[s][m], v, i)) {
-            v = best_v[s][m];
-            i = best_i[s][m];
-          }
-        a.part_val[(int64_t)m * gridDim.x + blockIdx.x] = v;
-        a.part_idx[(int64_t)m * gridDim.x + blockIdx.x] = i;
-      }
-      __threadfence();
-      unsigned prev = atomicAdd(a.counter, 1u);
-      last_block = prev == gridDim.x - 1;
-    }
-    __syncthreads();
-    if (last_block) {
-      __threadfence();
-      for (int m = 0; m < M; ++m) {
-        float v = -__builtin_inff();
-        int64_t i = INT64_MAX;
-        for (int64_t j = tid; j < gridDim.x; j += 256) {
-          float pv = __hip_atomic_load(&a.part_val[(int64_t)m * gridDim.x + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          int64_t pi = __hip_atomic_load(&a.part_idx[(int64_t)m * gridDim.x + j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          if (argmax_better(pv, pi, v, i)) {
-            v = pv;
-            i = pi;
-          }
-        }
-        wave_argmax(v, i);
-        if (lane == 0) {
-          best_v[wave][m] = v;
-          best_i[wave][m] = i;
-        }
-      }
-      __syncthreads();
-      if (tid == 0) {
-        for (int m = 0; m < M; ++m) {
-          float v = best_v[0][m];
-          int64_t i = best_i[0][m];
-          for (int s = 1; s < 4; ++s)
-            if (argmax_better(best_v[s][m], best_i[s][m], v, i)) {
-              v = best_v[s][m];
-              i = best_i[s][m];
-            }
-          if (a.st->next_tok != nullptr) a.st->next_tok[m * a.st->next_tok_ld] = i;
-        }
-        *a.counter = 0u;
-      }
-    }
-  }
+  if constexpr (EPI == EPI_ARGMAX) argmax_finish<MM, SLOTS>(a, M, slot, kw, bv, bi, best_v, best_i);
 }
 
-template <typename T, int MM, int KSPLIT, int PRO, int EPI>
-int launch_cfg(hipStream_t st, const GemvArgs& a) {
-  auto kern = gemv_kernel<T, MM, KSPLIT, PRO, EPI>;
-  const int lds = (int)(MM * a.K * sizeof(float));
-  int rc = ensure_lds_limit((const void*)kern, lds);
-  if (rc) return rc;
-  int64_t ntup;
-  if (EPI == EPI_SWIGLU)
-    ntup = a.N / P;
-  else if (EPI == EPI_QKV_ROPE)
-    ntup = (int64_t)(a.a.Hq + 2 * a.a.Hkv) * (a.a.D / 2) / P;
-  else
-    ntup = cdiv(a.N, R);
+
+template <typename T, int MM, int KSPLIT, int JMAX, int PRO, int EPI>
+int launch_reg(hipStream_t st, const GemvArgs& a) {
   const int64_t slots = 4 / KSPLIT;
-  int grid = (int)std::min<int64_t>(cdiv(ntup, slots), EPI == EPI_ARGMAX ? gemv_argmax_partials(a.N) : MAX_GRID);
-  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, a);
+  const int64_t cap = EPI == EPI_ARGMAX ? gemv_argmax_partials(a.N) : MAX_GRID;
+  const int grid = (int)std::min<int64_t>(cdiv(num_tuples<EPI>(a), slots), cap);
+  hipLaunchKernelGGL((gemv_reg_kernel<T, MM, KSPLIT, JMAX, PRO, EPI>), dim3(grid), dim3(256), 0, st, a);
   MINITP_LAUNCH_CHECK();
+  if constexpr (EPI == EPI_ARGMAX) return launch_argmax_merge(st, a.part_val, a.part_idx, grid, a.M, nullptr, 0, a.st);
   return MINITP_OK;
 }
 
 template <typename T, int MM, int PRO, int EPI>
-int pick_ksplit(hipStream_t st, const GemvArgs& a) {
+int launch_lds(hipStream_t st, const GemvArgs& a) {
+  auto kern = gemv_lds_kernel<T, MM, 4, PRO, EPI>;
+  const int lds = (int)(MM * a.K * sizeof(float));
+  int rc = ensure_lds_limit((const void*)kern, lds);
+  if (rc) return rc;
+  const int64_t cap = EPI == EPI_ARGMAX ? gemv_argmax_partials(a.N) : MAX_GRID;
+  const int grid = (int)std::min<int64_t>(num_tuples<EPI>(a), cap);
+  hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, a);
+  MINITP_LAUNCH_CHECK();
+  if constexpr (EPI == EPI_ARGMAX) return launch_argmax_merge(st, a.part_val, a.part_idx, grid, a.M, nullptr, 0, a.st);
+  return MINITP_OK;
+}
+
+template <typename T, int MM, int PRO, int EPI>
+int pick_k(hipStream_t st, const GemvArgs& a) {
   const int64_t nchunk = a.K / Vec<T>::N;
-  if (nchunk >= 512) return launch_cfg<T, MM, 4, PRO, EPI>(st, a);
-  if (nchunk >= 192) return launch_cfg<T, MM, 2, PRO, EPI>(st, a);
-  return launch_cfg<T, MM, 1, PRO, EPI>(st, a);
+  if (nchunk <= 128) return launch_reg<T, MM, 1, 2, PRO, EPI>(st, a);
+  if constexpr (MM <= 2) {
+    if (nchunk <= 512) return launch_reg<T, MM, 2, 4, PRO, EPI>(st, a);
+    if (nchunk <= REG_MAX_CHUNKS) return launch_reg<T, MM, 4, 4, PRO, EPI>(st, a);
+  }
+  if constexpr (MM == 1) return launch_lds<T, MM, PRO, EPI>(st, a);
+  set_error("gemv: M=%lld with K=%lld is served by the GEMM path", (long long)a.M, (long long)a.K);
+  return MINITP_ERR_UNSUPPORTED;
 }
 
 template <typename T, int PRO, int EPI>
 int pick_m(hipStream_t st, const GemvArgs& a) {
-  if (a.M == 1) return pick_ksplit<T, 1, PRO, EPI>(st, a);
-  if (a.M == 2) return pick_ksplit<T, 2, PRO, EPI>(st, a);
-  return pick_ksplit<T, 4, PRO, EPI>(st, a);
+  if (a.M == 1) return pick_k<T, 1, PRO, EPI>(st, a);
+  if (a.M == 2) return pick_k<T, 2, PRO, EPI>(st, a);
+  return pick_k<T, 4, PRO, EPI>(st, a);
 }
 
 template <typename T, int PRO>
@@ -421,9 +743,16 @@ int pick_epi(hipStream_t st, int epi, const GemvArgs& a) {
 // Block count (and so partial count per row) of the LM-head argmax GEMV.
 int64_t gemv_argmax_partials(int64_t N) { return std::min<int64_t>(cdiv(cdiv(N, R), 4), 1024); }
 
+// The register path keeps the input rows in registers (M * JMAX chunks per
+// lane): M <= 4 up to 128 chunks per row, M <= 2 up to 1024; M == 1 beyond
+// that stages the input in LDS (up to 80 KiB). Other shapes run the GEMM.
 bool gemv_supported(int dtype, int64_t M, int64_t K) {
-  const int64_t mm = M == 1 ? 1 : M == 2 ? 2 : 4;
-  return M >= 1 && M <= 4 && mm * K * 4 <= 80 * 1024 && K % (dtype == MINITP_F32 ? 4 : 8) == 0;
+  const int v = dtype == MINITP_F32 ? 4 : 8;
+  if (M < 1 || M > 4 || K % v != 0) return false;
+  const int64_t nchunk = K / v;
+  if (nchunk <= 128) return true;
+  if (nchunk <= REG_MAX_CHUNKS) return M <= 2;
+  return M == 1 && K * 4 <= 80 * 1024;
 }
 
 int launch_gemv(hipStream_t st, int dtype, int pro, int epi, const GemvArgs& a) {

@@ -8,18 +8,33 @@ namespace minitp {
 // Per-forward scalars and pointers the decode sequence reads from device
 // memory, so a captured hipGraph stays valid from step to step: only the
 // first node's arguments change, and it writes this struct.
-struct StepState {
+constexpr int MAX_HEAD_DIM = 128;
+
+// Per-forward scalars and pointers (passed by value to the first kernel).
+struct StepArgs {
   const int64_t* ids;  // [B, T] token ids, row stride ids_ld
   int64_t ids_ld;
   const int64_t* positions;  // [T]
   int64_t cache_len;         // KV rows already filled
   void* k_cache;             // [L, B, Hkv, S, D]
   void* v_cache;
-  void* logits;  // [B, V] last-position logits
+  void* logits;  // [B, V] (or [B, T, V]) logits output
   int64_t* next_tok;
   int64_t next_tok_ld;
-  int32_t error;  // bit 0: a position was outside the RoPE table
+};
+
+// What the forward's later kernels read from device memory, so a captured
+// hipGraph stays valid from step to step: only the first node's arguments
+// change, and that node writes this struct.
+struct StepState {
+  StepArgs args;
+  int32_t error;  // 1: a position was outside the RoPE table
   int32_t pad_;
+  // T == 1: the RoPE table rows of positions[0], copied by the first kernel of
+  // the forward so the QKV epilogue reads them at a fixed address (NaN when
+  // the position is outside the table).
+  float rope_cos[MAX_HEAD_DIM];
+  float rope_sin[MAX_HEAD_DIM];
 };
 
 // Layer-independent shape of the attention / KV layout.
@@ -49,10 +64,10 @@ struct GemvArgs {
   int64_t max_pos;
   int layer;
   AttnShape a;
-  // EPI_ARGMAX: logits -> st->logits (ld N), token -> st->next_tok
+  // EPI_ARGMAX: logits -> st->logits (ld N), token -> st->next_tok (through
+  // argmax_merge_kernel, launched right after the GEMV)
   float* part_val;  // [M, gridDim.x] block partials
   int64_t* part_idx;
-  unsigned* counter;  // zero before the launch, zero again after it
 };
 
 // gemv.hip
@@ -102,6 +117,10 @@ int launch_prefill_attention(hipStream_t st, int dtype, const void* q, const voi
 
 // argmax.hip
 int64_t argmax_workspace_bytes(int64_t B, int64_t V);
+// Winner of each of `rows` rows of nb (value, index) partials -> out (or
+// state->next_tok when state is non-null; nothing when that is null).
+int launch_argmax_merge(hipStream_t st, const float* pv, const int64_t* pi, int64_t nb, int64_t rows, int64_t* out,
+                        int64_t out_stride, const StepState* state);
 // With `state`: logits = state->logits + row_offset, out = state->next_tok
 // (stride state->next_tok_ld); row b of the logits starts at b * ld.
 int launch_argmax(hipStream_t st, int dtype, const void* logits, int64_t ld, int64_t B, int64_t V, int64_t* out,

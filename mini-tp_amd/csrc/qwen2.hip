@@ -23,10 +23,29 @@ namespace minitp {
 
 namespace {
 
+// First kernel of every forward: publishes the per-forward values (StepState)
+// for the rest of the sequence, copies the RoPE rows of a single-token
+// forward's position next to them, and gathers the embedding rows
+// (embedding.py:44-46).
 template <typename T>
-__global__ void step_embed_kernel(StepState* dst, StepState val, const T* __restrict__ table, T* __restrict__ out,
-                                  int64_t hidden, int64_t vocab, int64_t T_) {
-  if (blockIdx.x == 0 && threadIdx.x == 0) *dst = val;
+__global__ void step_embed_kernel(StepState* dst, StepArgs val, const T* __restrict__ table, T* __restrict__ out,
+                                  int64_t hidden, int64_t vocab, int64_t T_, const float* cos_tab,
+                                  const float* sin_tab, int64_t max_pos, int head_dim) {
+  if (blockIdx.x == 0) {
+    if (threadIdx.x == 0) {
+      dst->args = val;
+      dst->error = 0;
+    }
+    if (T_ == 1) {
+      const int64_t pos = val.positions[0];
+      const bool ok = pos >= 0 && pos < max_pos;
+      for (int i = threadIdx.x; i < head_dim; i += blockDim.x) {
+        dst->rope_cos[i] = ok ? cos_tab[pos * head_dim + i] : __builtin_nanf("");
+        dst->rope_sin[i] = ok ? sin_tab[pos * head_dim + i] : __builtin_nanf("");
+      }
+      if (!ok && threadIdx.x == 0) dst->error = 1;
+    }
+  }
   const int64_t n = blockIdx.x, b = n / T_, t = n % T_;
   const int64_t id = val.ids[b * val.ids_ld + t];
   T* o = out + n * hidden;
@@ -49,7 +68,6 @@ struct Ws {
   int64_t attn_ws_bytes;
   float* part_val;
   int64_t* part_idx;
-  unsigned* counter;
   void* amax_ws;
   int64_t amax_ws_bytes;
   int64_t bytes;
@@ -106,7 +124,6 @@ struct Qwen2Program {
     const int64_t np = gemv_argmax_partials(c.vocab);
     w.part_val = (float*)take(std::min<int64_t>(B, 4) * np * 4);
     w.part_idx = (int64_t*)take(std::min<int64_t>(B, 4) * np * 8);
-    w.counter = (unsigned*)take(4);
     w.amax_ws_bytes = argmax_workspace_bytes(B, c.vocab);
     w.amax_ws = take(w.amax_ws_bytes);
     w.bytes = off;
@@ -124,7 +141,7 @@ struct Qwen2Program {
     const int64_t H = c.hidden, I = c.intermediate, V = c.vocab;
     const int D = c.head_dim;
     int rc;
-    StepState val{};
+    StepArgs val{};
     val.ids = s.ids;
     val.ids_ld = s.ids_ld;
     val.positions = s.positions;
@@ -134,12 +151,13 @@ struct Qwen2Program {
     val.logits = s.logits;
     val.next_tok = s.next_tok;
     val.next_tok_ld = s.next_tok_ld;
+    const int64_t max_pos = c.max_pos;
     if (c.dtype == MINITP_F32)
       hipLaunchKernelGGL(step_embed_kernel<float>, dim3((unsigned)M), dim3(EMBED_THREADS), 0, st, w.st, val,
-                         (const float*)embed, (float*)w.x, H, (int64_t)V, T);
+                         (const float*)embed, (float*)w.x, H, (int64_t)V, T, cos_tab, sin_tab, max_pos, D);
     else
       hipLaunchKernelGGL(step_embed_kernel<bf16>, dim3((unsigned)M), dim3(EMBED_THREADS), 0, st, w.st, val,
-                         (const bf16*)embed, (bf16*)w.x, H, (int64_t)V, T);
+                         (const bf16*)embed, (bf16*)w.x, H, (int64_t)V, T, cos_tab, sin_tab, max_pos, D);
     MINITP_LAUNCH_CHECK();
 
     const bool fz = fused(M);
@@ -253,7 +271,6 @@ struct Qwen2Program {
       g.st = w.st;
       g.part_val = w.part_val;
       g.part_idx = w.part_idx;
-      g.counter = w.counter;
       return launch_gemv(st, c.dtype, PRO_NORM, EPI_ARGMAX, g);
     }
     if (s.logits_all && fz) {  // same kernel family as the module path at this M
@@ -325,7 +342,7 @@ struct Qwen2Program {
 };
 
 static int patch_and_launch(Qwen2Program* p, GraphEntry& g, hipStream_t st, const minitp_qwen2_step& s, const Ws& w) {
-  StepState val{};
+  StepArgs val{};
   val.ids = s.ids;
   val.ids_ld = s.ids_ld;
   val.positions = s.positions;
@@ -338,8 +355,12 @@ static int patch_and_launch(Qwen2Program* p, GraphEntry& g, hipStream_t st, cons
   StepState* dst = w.st;
   const void* table = p->embed;
   void* out = w.x;
-  int64_t hidden = p->c.hidden, vocab = p->c.vocab, tt = 1;
-  void* args[] = {&dst, &val, (void*)&table, &out, &hidden, &vocab, &tt};
+  int64_t hidden = p->c.hidden, vocab = p->c.vocab, tt = 1, max_pos = p->c.max_pos;
+  const float* cos_tab = p->cos_tab;
+  const float* sin_tab = p->sin_tab;
+  int head_dim = p->c.head_dim;
+  void* args[] = {&dst, &val, (void*)&table, &out, &hidden, &vocab, &tt, (void*)&cos_tab, (void*)&sin_tab,
+                  &max_pos, &head_dim};
   hipKernelNodeParams kp{};
   kp.func = p->c.dtype == MINITP_F32 ? (void*)step_embed_kernel<float> : (void*)step_embed_kernel<bf16>;
   kp.gridDim = dim3((unsigned)s.batch);

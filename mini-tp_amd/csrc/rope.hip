@@ -93,10 +93,10 @@ __global__ void rope_kv_write_kernel(const T* qkv, int64_t ld, T* q_out, T* k_ca
                                      int32_t* error_flag, const StepState* state, int layer) {
   if (state != nullptr) {  // graph replay: per-step values live in device memory
     const int64_t layer_off = (int64_t)layer * B * Hkv * S * D;
-    positions = state->positions;
-    cache_len = state->cache_len;
-    k_cache = (T*)state->k_cache + layer_off;
-    v_cache = (T*)state->v_cache + layer_off;
+    positions = state->args.positions;
+    cache_len = state->args.cache_len;
+    k_cache = (T*)state->args.k_cache + layer_off;
+    v_cache = (T*)state->args.v_cache + layer_off;
     error_flag = (int32_t*)&state->error;
   }
   const int64_t half = D / 2, heads = Hq + 2 * Hkv;

@@ -185,7 +185,7 @@ def test_graph_decode_equals_direct_forward(dtype):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_module_path_equals_native_program(dtype):
+def test_module_path_matches_native_program(dtype):
     from minitp.generation import generate_greedy, make_kv_cache
 
     model = _tiny(dtype)
@@ -200,7 +200,12 @@ def test_module_path_equals_native_program(dtype):
     kv_b = make_kv_cache(model, 1, 9)
     modules = model(prompt, positions=torch.arange(8, device=DEV), kv_cache=kv_b)
     mod_dec = model(prompt[:, :1], positions=torch.tensor([8], device=DEV), kv_cache=kv_b)
-    assert torch.equal(native, modules) and torch.equal(nat_dec, mod_dec)
+    # same kernels except the RMSNorm before each projection: fused into the
+    # GEMV prologue natively, a separate kernel on the module path (its sum of
+    # squares runs in a different order), so agreement is to rounding
+    tol = dict(atol=1e-5, rtol=1e-5) if dtype == torch.float32 else dict(atol=0.05, rtol=0.02)
+    torch.testing.assert_close(native, modules, **tol)
+    torch.testing.assert_close(nat_dec, mod_dec, **tol)
     ids_mod = generate_greedy(model, prompt, 6, early_stop=False)
     for layer in model.model.layers:
         layer.self_attn.use_fused_qkv = True
@@ -208,13 +213,15 @@ def test_module_path_equals_native_program(dtype):
     assert torch.equal(ids_mod, generate_greedy(model, prompt, 6, early_stop=False))
 
 
-def test_uncached_rope_toggle_matches_cached():
+def test_uncached_rope_toggle_matches_cached_values():
     model = _tiny()
     prompt = torch.tensor([[3, 17, 256, 999]], device=DEV)
     a = model(prompt)
     model.use_rotary_cache = False
     b = model(prompt)
-    assert torch.equal(a, b)
+    # identical tables (uncached rows equal cached rows); the toggle also moves
+    # the forward onto the module path, which normalises in its own kernel
+    torch.testing.assert_close(a, b, atol=1e-5, rtol=1e-5)
 
 
 # ---------------------------------------------------------------------------
