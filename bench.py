@@ -10,8 +10,10 @@ Reported beside the headline tok/s:
   * HBM roofline of the whole step: algorithmic bytes per token (weights once,
     LM head once, norms, QKV bias, KV read of ctx + 1 positions) / time,
     against MI355X's 8 TB/s;
-  * the dominant kernel (the fused gate/up GEMV) timed with HIP events on its
-    stream: algorithmic bytes per launch / mean launch time;
+  * the dominant kernel (the fused RMSNorm + gate/up GEMV + SwiGLU) timed
+    with HIP events on its stream: algorithmic bytes per launch / mean
+    launch time, and its measured HBM traffic per launch when the committed
+    rocprofv3 counter summary is present;
   * TTFT (prefill start -> first token selected) p50 / mean, TPOT percentiles;
   * the CPU baseline: the oracle restatement of the reference's TP=1 path on
     the host cores, bf16, over a bounded sample of the same workload.
@@ -54,6 +56,11 @@ def parse(argv=None):
     ap.add_argument("--ttft-iters", type=int, default=10)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain copy of MIB MiB (the --pmc byte-counter calibration) and exit")
+    ap.add_argument("--dominant-only", action="store_true",
+                    help="only launch the dominant kernel, eagerly (no graphs), once per layer 4 times over, and "
+                         "exit: the workload of the --pmc byte-counter passes")
     return ap.parse_args(argv)
 
 
@@ -89,35 +96,88 @@ def decode_run(model, prompt, n_steps, record_steps=False):
     return dt, ttft, [a.elapsed_time(b) for a, b in evs], st.out_ids
 
 
-def dominant_kernel(model, reps: int = 20):
-    """Fused gate/up + SwiGLU GEMV (the largest per-layer stream), timed on
-    the current stream with HIP events over launches cycling through all
-    layers' weights (so no launch re-reads a cache-resident matrix)."""
+DOMINANT = "gemv_reg_kernel<minitp::bf16, 1, 1, 2, 1, 2>"  # PRO_NORM, EPI_SWIGLU: rocprofv3's name for it
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gate_up_gemv_q05b_decode_traffic.json")
+
+
+def _dominant_launcher(model):
+    """A function launching the dominant kernel once per layer on the current
+    stream, with that layer's weights."""
     import torch
 
     from minitp import _native as N
     from minitp import kernels as K
 
     cfg = model.cfg
+    layers = list(model.model.layers)
     x = torch.randn(1, cfg.hidden_size, device="cuda").to(torch.bfloat16)
-    ws = [layer.mlp.gate_up_proj.weight for layer in model.model.layers]
     out = torch.empty(1, cfg.intermediate_size, dtype=torch.bfloat16, device="cuda")
-    for w in ws:
-        K.linear(x, w, out=out, epilogue=N.EPI_SWIGLU)
-    a, b = torch.cuda.Event(True), torch.cuda.Event(True)
+
+    def launch_all():
+        for layer in layers:
+            K.rmsnorm_linear(x, layer.post_attention_layernorm.weight, cfg.rms_norm_eps, layer.mlp.gate_up_proj.weight,
+                             out=out, epilogue=N.EPI_SWIGLU)
+
+    return launch_all
+
+
+def dominant_kernel(model, reps: int = 20):
+    """The kernel with the largest share of a decode step: the fused
+    post-attention RMSNorm + gate/up GEMV + SwiGLU that the decode graph runs
+    once per layer. The same entry point and the same per-layer weights,
+    launched once per layer in a captured graph (so no launch re-reads a
+    cache-resident matrix and no host launch cost is counted), timed with
+    HIP events on the stream the graph replays on."""
+    import torch
+
+    launch_all = _dominant_launcher(model)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        launch_all()
+    torch.cuda.current_stream().wait_stream(side)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        launch_all()
+    graph.replay()
     torch.cuda.synchronize()
+    a, b = torch.cuda.Event(True), torch.cuda.Event(True)
     a.record()
-    n = 0
     for _ in range(reps):
-        for w in ws:
-            K.linear(x, w, out=out, epilogue=N.EPI_SWIGLU)
-            n += 1
+        graph.replay()
     b.record()
     torch.cuda.synchronize()
+    n = reps * model.cfg.num_hidden_layers
     us = a.elapsed_time(b) * 1e3 / n
-    nbytes = 2 * (2 * cfg.intermediate_size * cfg.hidden_size + cfg.hidden_size + cfg.intermediate_size)
-    return {"name": "gemv_reg_kernel<bf16,MM=1,KSPLIT=1,JMAX=2,PRO_NONE,EPI_SWIGLU> (gate/up [9728,896] + SwiGLU)",
-            "bytes_per_launch": nbytes, "us_per_launch": us, "launches": n}
+    h, i = model.cfg.hidden_size, model.cfg.intermediate_size
+    nbytes = 2 * (2 * i * h + 2 * h + i)  # W_gate_up, x, norm weight, SwiGLU output (bf16)
+    return {"name": DOMINANT + " (RMSNorm + gate/up [9728, 896] + SwiGLU)", "bytes_per_launch": nbytes,
+            "us_per_launch": us, "launches": n}
+
+
+def measured_traffic():
+    """HBM bytes per launch of the dominant kernel from the committed
+    rocprofv3 --pmc summary (FETCH_SIZE, WRITE_SIZE scaled by a plain copy of
+    known size), or None when that summary is absent."""
+    try:
+        with open(TRAFFIC_FILE) as f:
+            return int(json.load(f)["traffic_bytes_per_launch"])
+    except (OSError, KeyError, ValueError):
+        return None
+
+
+def copy_calibration(mib: int) -> None:
+    """A plain device copy of `mib` MiB (bf16 tensor copy_), three times: the
+    known-size kernel that --pmc FETCH_SIZE / WRITE_SIZE are scaled by."""
+    import torch
+
+    n = mib * (1 << 20) // 2
+    src = torch.ones(n, dtype=torch.bfloat16, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n * 2, "copy_bytes_written": n * 2, "launches": 3}), flush=True)
 
 
 def cpu_baseline(model, prompt, budget_s: float):
@@ -174,6 +234,10 @@ def main(argv=None):
         sys.exit(2)
     import torch
 
+    if args.copy_calibration:
+        torch.cuda.set_device(0)
+        copy_calibration(args.copy_calibration)
+        return
     from minitp.bench.benchmark import _percentiles
     from minitp.synthetic import QWEN05B, build_synthetic_model, synthetic_prompt
 
@@ -181,6 +245,13 @@ def main(argv=None):
     cfg = QWEN05B
     with torch.inference_mode():
         model = build_synthetic_model(cfg, dtype=torch.bfloat16, device="cuda", seed=0)
+        if args.dominant_only:
+            launch_all = _dominant_launcher(model)
+            for _ in range(4):
+                launch_all()
+            torch.cuda.synchronize()
+            print(json.dumps({"kernel": DOMINANT, "launches": 4 * cfg.num_hidden_layers}), flush=True)
+            return
         prompt = synthetic_prompt(cfg.vocab_size, 1, args.prompt_len, seed=0, device="cuda")
         torch.cuda.synchronize()
 
@@ -230,7 +301,7 @@ def main(argv=None):
                                f"{args.steps + 1} greedy tokens",
                    "global_batch": 1, "seq_len": args.prompt_len + args.steps + 1, "parallelism": "tp1"},
         "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": None, "kernel": kern["name"],
+                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(), "kernel": kern["name"],
                      "bytes_per_launch": kern["bytes_per_launch"], "us_per_launch": round(kern["us_per_launch"], 3)},
         "step_roofline": {"achieved_gbs": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
                           "bytes_per_token_avg": int(total_bytes / args.steps),
@@ -238,7 +309,8 @@ def main(argv=None):
         "ttft_ms": {"p50": round(ttft_ms[(len(ttft_ms) + 1) // 2 - 1], 3),
                     "mean": round(sum(ttft_ms) / len(ttft_ms), 3), "samples": len(ttft_ms)},
         "tpot_ms": _percentiles(step_ms),
-        "decode_path": "one hipGraph replay per token: embedding, 5 kernels per layer, fused norm + LM head + argmax",
+        "decode_path": "one hipGraph replay per token: embedding; per layer norm+QKV+RoPE+KV write, attention, "
+                       "o_proj+residual, norm+gate/up+SwiGLU, down+residual; norm+LM head+argmax partials, merge",
     }
     if not args.no_cpu_baseline:
         result["cpu_baseline"] = cpu_baseline(model, prompt, args.cpu_budget_s)

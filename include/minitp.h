@@ -86,6 +86,18 @@ int minitp_silu_mul(void* stream, int dtype, const void* gate, const void* up, i
 int minitp_linear(void* stream, int dtype, const void* x, int64_t ldx, const void* w,
                   const void* bias, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                   int epilogue, const void* aux);
+/* RMSNorm (layer.py:39-42) feeding a linear (the decoder layer's
+ * input_layernorm -> qkv_proj and post_attention_layernorm -> gate_up_proj,
+ * layer.py:60-67) in one pass over W: every block normalises the x rows it
+ * needs (fp32, rounded to dtype) and streams its share of W. Arguments as
+ * minitp_linear plus norm_w [K] and eps. Serves the decode shapes only
+ * (M <= 4 rows, or M == 1 up to K = 20480); others return
+ * MINITP_ERR_UNSUPPORTED (use minitp_rmsnorm, then minitp_linear). The norm
+ * sums x^2 in a different order than minitp_rmsnorm, so the two agree to
+ * rounding, not bitwise. */
+int minitp_rmsnorm_linear(void* stream, int dtype, const void* x, int64_t ldx, const void* norm_w,
+                          float eps, const void* w, const void* bias, void* y, int64_t ldy, int64_t M,
+                          int64_t N, int64_t K, int epilogue, const void* aux);
 
 /* ---- rotary embedding and KV cache -------------------------------------- */
 /* RotaryEmbedding.apply (rope.py:47-64): q [B, Hq, T, D] and k [B, Hkv, T, D]

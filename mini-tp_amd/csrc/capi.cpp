@@ -123,8 +123,10 @@ int minitp_silu_mul(void* stream, int dtype, const void* gate, const void* up, i
   return launch_silu_mul(S(stream), dtype, gate, up, ld_in, out, ld_out, rows, n);
 }
 
-int minitp_linear(void* stream, int dtype, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
-                  int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const void* aux) {
+namespace {
+
+int linear_checks(int dtype, const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy,
+                  int64_t M, int64_t N, int64_t K, int epilogue, const void* aux) {
   CHECK_DTYPE(dtype);
   MINITP_CHECK_ARG(M >= 0 && N >= 0 && K > 0, "linear: M=%lld N=%lld K=%lld", (long long)M, (long long)N,
                    (long long)K);
@@ -138,29 +140,63 @@ int minitp_linear(void* stream, int dtype, const void* x, int64_t ldx, const voi
   MINITP_CHECK_ARG(aligned16(x) && aligned16(w), "linear: x and W must be 16-byte aligned");
   MINITP_CHECK_ARG(epilogue != MINITP_EPI_RESID || aux != nullptr, "linear: RESID needs aux");
   MINITP_CHECK_ARG(epilogue == MINITP_EPI_NONE || bias == nullptr, "linear: bias only with MINITP_EPI_NONE");
+  if (epilogue == MINITP_EPI_SWIGLU)
+    MINITP_CHECK_ARG(N % 2 == 0, "linear: SWIGLU output width %lld must be even", (long long)N);
+  return MINITP_OK;
+}
+
+GemvArgs gemv_args(const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy, int64_t M,
+                   int64_t N, int64_t K, const void* aux) {
+  GemvArgs g{};
+  g.x = x;
+  g.ldx = ldx;
+  g.w = w;
+  g.bias = bias;
+  g.y = y;
+  g.ldy = ldy;
+  g.aux = aux;
+  g.M = M;
+  g.N = N;
+  g.K = K;
+  return g;
+}
+
+int gemv_epilogue(int epilogue) {
+  return epilogue == MINITP_EPI_RESID ? EPI_RESID : epilogue == MINITP_EPI_SWIGLU ? EPI_SWIGLU : EPI_STORE;
+}
+
+}  // namespace
+
+int minitp_linear(void* stream, int dtype, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
+                  int64_t ldy, int64_t M, int64_t N, int64_t K, int epilogue, const void* aux) {
+  int rc = linear_checks(dtype, x, ldx, w, bias, y, ldy, M, N, K, epilogue, aux);
+  if (rc || M == 0 || N == 0) return rc;
   hipStream_t st = S(stream);
-  if (gemv_supported(dtype, M, K)) {
-    GemvArgs g{};
-    g.x = x;
-    g.ldx = ldx;
-    g.w = w;
-    g.bias = bias;
-    g.y = y;
-    g.ldy = ldy;
-    g.aux = aux;
-    g.M = M;
-    g.N = N;
-    g.K = K;
-    const int epi = epilogue == MINITP_EPI_RESID ? EPI_RESID : epilogue == MINITP_EPI_SWIGLU ? EPI_SWIGLU : EPI_STORE;
-    if (epi == EPI_SWIGLU)
-      MINITP_CHECK_ARG(N % 2 == 0, "linear: SWIGLU output width %lld must be even", (long long)N);
-    return launch_gemv(st, dtype, PRO_NONE, epi, g);
-  }
+  if (gemv_supported(dtype, M, K))
+    return launch_gemv(st, dtype, PRO_NONE, gemv_epilogue(epilogue), gemv_args(x, ldx, w, bias, y, ldy, M, N, K, aux));
   if (epilogue == MINITP_EPI_SWIGLU) {
     set_error("linear: SWIGLU epilogue is served by the GEMV path only (M <= 4); use NONE + minitp_silu_mul");
     return MINITP_ERR_UNSUPPORTED;
   }
   return launch_gemm(st, dtype, x, ldx, w, bias, y, ldy, M, N, K, epilogue, aux);
+}
+
+int minitp_rmsnorm_linear(void* stream, int dtype, const void* x, int64_t ldx, const void* norm_w, float eps,
+                          const void* w, const void* bias, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
+                          int epilogue, const void* aux) {
+  int rc = linear_checks(dtype, x, ldx, w, bias, y, ldy, M, N, K, epilogue, aux);
+  if (rc || M == 0 || N == 0) return rc;
+  MINITP_CHECK_ARG(norm_w != nullptr, "rmsnorm_linear: NULL norm weight");
+  MINITP_CHECK_ARG(epilogue != MINITP_EPI_RESID || aux != x, "rmsnorm_linear: RESID aux must not alias x");
+  if (!gemv_supported(dtype, M, K)) {
+    set_error("rmsnorm_linear: M=%lld K=%lld is not a decode shape; use minitp_rmsnorm + minitp_linear",
+              (long long)M, (long long)K);
+    return MINITP_ERR_UNSUPPORTED;
+  }
+  GemvArgs g = gemv_args(x, ldx, w, bias, y, ldy, M, N, K, aux);
+  g.norm_w = norm_w;
+  g.eps = eps;
+  return launch_gemv(S(stream), dtype, PRO_NORM, gemv_epilogue(epilogue), g);
 }
 
 int minitp_rope(void* stream, int dtype, const void* q, const void* k, void* q_out, void* k_out, const float* cos_tab,

@@ -315,6 +315,12 @@ struct Qwen2Program {
                      (long long)s->tokens);
     MINITP_CHECK_ARG(s->ids && s->positions && s->k_cache && s->v_cache && s->workspace, "NULL pointer in step");
     MINITP_CHECK_ARG(s->logits != nullptr || s->next_tok != nullptr, "step produces nothing (no logits, no next_tok)");
+    // Only the fused LM-head GEMV + argmax (last position, batch <= 4) can
+    // skip the logits store; the other LM-head paths always write them.
+    const bool fused_head = !s->logits_all && s->batch <= 4 && gemv_supported(c.dtype, s->batch, c.hidden);
+    MINITP_CHECK_ARG(fused_head || s->logits != nullptr,
+                     "logits buffer required (batch %lld, logits_all %d: the LM head stores logits before the argmax)",
+                     (long long)s->batch, (int)s->logits_all);
     MINITP_CHECK_ARG(s->ids_ld >= s->tokens, "ids_ld=%lld < tokens", (long long)s->ids_ld);
     if (s->cache_len < 0 || s->cache_len + s->tokens > s->max_seq) {
       set_error("KV cache overflow: seq %lld+%lld > max_seq_len=%lld", (long long)s->cache_len, (long long)s->tokens,
@@ -430,13 +436,18 @@ int minitp_qwen2_forward(void* handle, void* stream, const minitp_qwen2_step* st
   return p->run((hipStream_t)stream, *step, w);
 }
 
-int minitp_qwen2_decode(void* handle, void* stream, const minitp_qwen2_step* step) {
-  MINITP_CHECK_ARG(handle != nullptr, "NULL handle");
+int minitp_qwen2_decode(void* handle, void* stream, const minitp_qwen2_step* step_in) {
+  MINITP_CHECK_ARG(handle != nullptr && step_in != nullptr, "NULL argument");
   auto* p = (Qwen2Program*)handle;
+  MINITP_CHECK_ARG(step_in->tokens == 1, "decode expects tokens == 1, got %lld", (long long)step_in->tokens);
+  // With one token, [B, T, V] and [B, V] logits are the same layout: one
+  // graph shape serves both (and no logits pointer is baked into a graph).
+  minitp_qwen2_step one = *step_in;
+  one.logits_all = 0;
+  const minitp_qwen2_step* step = &one;
   minitp::Ws w;
   int rc = p->check_step(step, w);
   if (rc) return rc;
-  MINITP_CHECK_ARG(step->tokens == 1, "decode expects tokens == 1, got %lld", (long long)step->tokens);
   hipStream_t st = (hipStream_t)stream;
   std::lock_guard<std::mutex> lock(p->mu);
   for (auto& g : p->graphs)

@@ -150,6 +150,30 @@ def linear(x: torch.Tensor, w: torch.Tensor, bias: torch.Tensor | None = None, *
     return out
 
 
+def rmsnorm_linear(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: torch.Tensor,
+                   bias: torch.Tensor | None = None, *, out: torch.Tensor | None = None, epilogue: int = N.EPI_NONE,
+                   aux: torch.Tensor | None = None) -> torch.Tensor:
+    """linear(rmsnorm(x, norm_w, eps), w, bias) as one GEMV pass over ``w``
+    (decode shapes: at most 4 rows). Equal to the two-call form up to the
+    norm's summation order."""
+    N.require_gpu(x, norm_w, w, bias, what="rmsnorm_linear")
+    if x.dtype != w.dtype or norm_w.dtype != w.dtype or (bias is not None and bias.dtype != w.dtype):
+        raise TypeError(f"rmsnorm_linear: dtype mismatch x={x.dtype} norm={norm_w.dtype} w={w.dtype}")
+    w = w.contiguous()
+    xr, m, ldx = _as_rows(x)
+    n_out = w.shape[0] // 2 if epilogue == N.EPI_SWIGLU else w.shape[0]
+    if out is None:
+        out = torch.empty(*x.shape[:-1], n_out, dtype=x.dtype, device=x.device)
+        ldy = n_out
+    else:
+        ldy = out.stride(-2) if out.dim() > 1 else n_out
+    N.check(_lib().minitp_rmsnorm_linear(N.stream(), N.dtype_code(x.dtype), xr.data_ptr(), ldx,
+                                         norm_w.contiguous().data_ptr(), float(eps), w.data_ptr(),
+                                         N.ptr(bias.contiguous() if bias is not None else None), out.data_ptr(), ldy,
+                                         m, n_out, w.shape[1], epilogue, N.ptr(aux)), "rmsnorm_linear")
+    return out
+
+
 def rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor):
     """RotaryEmbedding.apply on contiguous [B, H, T, D] q and k."""
     N.require_gpu(q, k, cos, sin, positions, what="rope")

@@ -145,6 +145,58 @@ def test_linear_swiglu_epilogue_equals_split(m, dtype):
     torch.testing.assert_close(split.cpu().float(), ref.float(), atol=1e-6, rtol=2 ** -7)
 
 
+@pytest.mark.parametrize("m,k", [(1, 896), (2, 896), (4, 896), (1, 4864), (2, 4864)])
+@pytest.mark.parametrize("epilogue", ["none", "bias", "swiglu", "resid"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_rmsnorm_linear_matches_two_step_reference(m, k, epilogue, dtype):
+    """The fused norm + GEMV against float64 linear of the dtype-rounded norm
+    output (layer.py:39-42 then linear.py:57-58)."""
+    from minitp import _native as N
+
+    if dtype == torch.float32 and (m == 4 or k == 4864) and m > 1:
+        pytest.skip("fp32 rows this long take the register GEMV path only for fewer rows")
+    g = torch.Generator().manual_seed(m * 31 + k + len(epilogue))
+    n = 512
+    eps = 1e-6
+    x = torch.randn(m, k, generator=g).to(dtype)
+    nw = (1 + 0.1 * torch.randn(k, generator=g)).to(dtype)
+    w = (torch.randn(2 * n if epilogue == "swiglu" else n, k, generator=g) * 0.02).to(dtype)
+    b = (torch.randn(n, generator=g) * 0.02).to(dtype) if epilogue == "bias" else None
+    r = torch.randn(m, n, generator=g).to(dtype)
+    xn = (x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + eps) * nw.float()).to(dtype)
+    lin = xn.double() @ w.double().T
+    if b is not None:
+        lin = lin + b.double()
+    epi = {"none": N.EPI_NONE, "bias": N.EPI_NONE, "swiglu": N.EPI_SWIGLU, "resid": N.EPI_RESID}[epilogue]
+    kw = {}
+    if epilogue == "resid":
+        kw = {"out": r.clone().to(DEV), "aux": r.clone().to(DEV)}
+    got = _k().rmsnorm_linear(x.to(DEV), nw.to(DEV), eps, w.to(DEV), None if b is None else b.to(DEV),
+                              epilogue=epi, **kw).cpu().double()
+    if epilogue == "swiglu":
+        gate, up = lin[:, :n].to(dtype).double(), lin[:, n:].to(dtype).double()
+        ref = (F.silu(gate.float()).to(dtype).double() * up)
+        scale = (xn.double().abs() @ w.double().abs().T).max().item()
+        tol = ref.abs() * 2 ** -7 + 2e-3 * scale if dtype == torch.bfloat16 else ref.abs() * 1e-5 + 1e-5 * scale
+    elif epilogue == "resid":
+        ref = r.double() + lin
+        scale = (xn.double().abs() @ w.double().abs().T).max().item() + r.double().abs().max().item()
+        tol = ref.abs() * 2 ** -7 + 2e-3 * scale if dtype == torch.bfloat16 else ref.abs() * 1e-6 + 1e-5 * scale
+    else:
+        ref = lin
+        scale = (xn.double().abs() @ w.double().abs().T).max().item()
+        tol = ref.abs() * 2 ** -8 + 2e-3 * scale if dtype == torch.bfloat16 else ref.abs() * 1e-6 + 1e-5 * scale
+    assert ((got - ref).abs() <= tol).all(), (got - ref).abs().max().item()
+
+
+def test_rmsnorm_linear_refuses_prefill_shapes():
+    x = torch.randn(8, 896, device=DEV)
+    nw = torch.ones(896, device=DEV)
+    w = torch.randn(64, 896, device=DEV)
+    with pytest.raises(NotImplementedError, match="decode shape"):
+        _k().rmsnorm_linear(x, nw, 1e-6, w)
+
+
 # ---------------------------------------------------------------------------
 # RoPE and KV writes
 

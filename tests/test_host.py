@@ -179,6 +179,13 @@ def test_program_create_validates_and_sizes_workspace():
         step.ids_ld = 5
         with pytest.raises(ValueError, match="overflow"):
             N.check(lib.minitp_qwen2_forward(h, None, ctypes.byref(step)), "forward")
+        with pytest.raises(ValueError, match="tokens == 1"):
+            N.check(lib.minitp_qwen2_decode(h, None, ctypes.byref(step)), "decode")
+        # batch > 4 runs the GEMM LM head, which stores logits before the argmax
+        step.tokens, step.cache_len, step.ids_ld, step.batch = 1, 3, 1, 8
+        step.logits, step.next_tok, step.next_tok_ld = None, 4096, 1
+        with pytest.raises(ValueError, match="logits buffer required"):
+            N.check(lib.minitp_qwen2_decode(h, None, ctypes.byref(step)), "decode")
     finally:
         lib.minitp_qwen2_destroy(h)
     bad = N.Qwen2Config(N.BF16, 2, 64, 5, 2, 16, 128, 1000, 256, 1e-6)
