@@ -68,14 +68,19 @@ struct Vec<float> {
 #ifndef MINITP_NT_LOADS
 #define MINITP_NT_LOADS 1
 #endif
+// The pointer is cast to the global address space: weight pointers read from
+// memory (a device-side table) would otherwise compile to flat loads, which
+// also count against the LDS counter and so make every LDS wait of the wave
+// wait for its streamed weights.
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef __attribute__((address_space(1))) const u32x4 global_u32x4;
 __device__ __forceinline__ uint4 load_stream16(const uint4* p) {
 #if MINITP_NT_LOADS
-  u32x4 v = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
-  return make_uint4(v.x, v.y, v.z, v.w);
+  u32x4 v = __builtin_nontemporal_load((global_u32x4*)(p));
 #else
-  return *p;
+  u32x4 v = *(global_u32x4*)(p);
 #endif
+  return make_uint4(v.x, v.y, v.z, v.w);
 }
 
 __device__ __forceinline__ void unpack16(const uint4& v, float* out, bf16*) {

@@ -13,10 +13,13 @@
 //   [o_proj + residual] [RMSNorm -> gate/up -> SwiGLU] [down + residual]
 // and the final RMSNorm -> LM head -> argmax is one more kernel. Larger M
 // runs MFMA GEMMs with separate norm / RoPE / SwiGLU kernels.
+#include <cmath>
 #include <mutex>
+#include <string>
 #include <vector>
 
 #include "common.h"
+#include "decode_loop.h"
 #include "kernels.h"
 
 namespace minitp {
@@ -96,6 +99,20 @@ struct Qwen2Program {
   std::mutex mu;
   std::vector<GraphEntry> graphs;
   hipStream_t capture_stream = nullptr;
+  // persistent batch-1 decode (decode_loop.hip)
+  LoopLayout loop_ll{};
+  LoopLds loop_lds{};
+  const LoopLayerW* table = nullptr;
+  const void* loop_kern = nullptr;
+  int loop_nb = 0;
+  int64_t spin_ticks = 0;
+  std::string loop_why = "not initialised";
+  int decode_path = MINITP_DECODE_AUTO;
+  uint64_t* trace = nullptr;  // persistent-decode phase trace (profiling)
+
+  // Bytes at the start of every workspace kept for the persistent decode
+  // (step counter, error words, hand-off words).
+  int64_t loop_region() const { return align256(loop_ll.bytes); }
 
   int es() const { return c.dtype == MINITP_F32 ? 4 : 2; }
   int qkv_rows() const { return (c.heads + 2 * c.kv_heads) * c.head_dim; }
@@ -105,7 +122,7 @@ struct Qwen2Program {
   Ws layout(void* base, int64_t M, int64_t B, int64_t S) const {
     Ws w{};
     char* p = (char*)base;
-    int64_t off = 0;
+    int64_t off = loop_region();
     auto take = [&](int64_t bytes) {
       char* r = p ? p + off : nullptr;
       off += align256(bytes);
@@ -309,6 +326,105 @@ struct Qwen2Program {
     return MINITP_OK;
   }
 
+  // Writes the device weight table and decides whether (and with which grid
+  // and LDS layout) the persistent decode serves this model on the current
+  // device.
+  int init_loop(const minitp_qwen2_weights* w) {
+    loop_ll = loop_layout(c);
+    if (!w->device_table) {
+      loop_why = "no device table given at create";
+      return MINITP_OK;
+    }
+    const int64_t need = (int64_t)c.num_layers * (int64_t)sizeof(LoopLayerW);
+    MINITP_CHECK_ARG(w->device_table_bytes >= need && aligned16(w->device_table),
+                     "device_table: %lld B (need %lld, 16-byte aligned)", (long long)w->device_table_bytes,
+                     (long long)need);
+    std::vector<LoopLayerW> t((size_t)c.num_layers);
+    for (int l = 0; l < c.num_layers; ++l) {
+      t[l] = LoopLayerW{L(l, MINITP_W_LN1),     L(l, MINITP_W_LN2), L(l, MINITP_W_QKV), L(l, MINITP_W_QKV_BIAS),
+                        L(l, MINITP_W_O),       L(l, MINITP_W_GATE_UP), L(l, MINITP_W_DOWN), nullptr};
+    }
+    MINITP_RETURN_HIP(hipMemcpy(w->device_table, t.data(), (size_t)need, hipMemcpyHostToDevice));
+    table = (const LoopLayerW*)w->device_table;
+    int dev = 0, cus = 0, khz = 0;
+    MINITP_RETURN_HIP(hipGetDevice(&dev));
+    MINITP_RETURN_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
+    MINITP_RETURN_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
+    loop_nb = std::min(cus, LOOP_MAX_BLOCKS);
+    if (const char* why = loop_unsupported(c, loop_nb, &loop_lds)) {
+      loop_why = why;
+      return MINITP_OK;
+    }
+    loop_kern = loop_kernel(c.dtype, c.head_dim);
+    if (!loop_kern) {
+      loop_why = "no kernel instantiated for this dtype / head_dim";
+      return MINITP_OK;
+    }
+    int rc = ensure_lds_limit(loop_kern, loop_lds.bytes);
+    if (rc) return rc;
+    int occ = 0;
+    MINITP_RETURN_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, loop_kern, LOOP_THREADS, loop_lds.bytes));
+    if (occ < 1) {
+      loop_why = "persistent kernel does not fit one block per CU";
+      return MINITP_OK;
+    }
+    spin_ticks = (int64_t)khz * 1000 * 2;  // a wait may last 2 s
+    loop_why.clear();
+    return MINITP_OK;
+  }
+
+  // One batch-1 decode step as one persistent launch (decode_loop.hip).
+  int run_loop(hipStream_t st, const minitp_qwen2_step& s) {
+    LoopParams a{};
+    a.L = c.num_layers;
+    a.H = c.hidden;
+    a.Hq = c.heads;
+    a.Hkv = c.kv_heads;
+    a.G = c.heads / c.kv_heads;
+    a.I = c.intermediate;
+    a.V = c.vocab;
+    a.eps = c.eps;
+    a.scale = 1.0f / sqrtf((float)c.head_dim);  // SDPA default (attention.py:92)
+    a.S = s.max_seq;
+    a.max_pos = c.max_pos;
+    a.embed = embed;
+    a.lm_head = lm_head;
+    a.final_norm = final_norm;
+    a.cos_tab = cos_tab;
+    a.sin_tab = sin_tab;
+    a.layers = table;
+    a.ids = s.ids;
+    a.positions = s.positions;
+    a.cache_len = s.cache_len;
+    a.k_cache = s.k_cache;
+    a.v_cache = s.v_cache;
+    a.logits = s.logits;
+    a.next_tok = s.next_tok;
+    a.ctrl = (uint32_t*)s.workspace;
+    a.ll = (uint64_t*)((char*)s.workspace + LOOP_CTRL_BYTES);
+    a.ll_layer_words = loop_ll.layer_words;
+    a.off_qkv = loop_ll.off_qkv;
+    a.off_p = loop_ll.off_p;
+    a.off_act = loop_ll.off_act;
+    a.off_down = loop_ll.off_down;
+    a.off_lm = loop_ll.off_lm;
+    a.lds_xs = loop_lds.xs;
+    a.lds_xin = loop_lds.xin;
+    a.lds_stage = loop_lds.stage;
+    a.lds_qstage = loop_lds.qstage;
+    a.lds_rowres = loop_lds.rowres;
+    a.lds_norm = loop_lds.norm;
+    a.lds_tile = loop_lds.tile;
+    a.lds_misc = loop_lds.misc;
+    a.spin_limit = spin_ticks;
+    loop_roles(c, loop_nb, a.role);
+    a.trace = trace;
+    a.trace_slots = loop_trace_slots(c.num_layers);
+    void* args[] = {&a};
+    MINITP_RETURN_HIP(hipLaunchKernel(loop_kern, dim3(loop_nb), dim3(LOOP_THREADS), args, loop_lds.bytes, st));
+    return MINITP_OK;
+  }
+
   int check_step(const minitp_qwen2_step* s, Ws& w) {
     MINITP_CHECK_ARG(s != nullptr, "step is NULL");
     MINITP_CHECK_ARG(s->batch >= 1 && s->tokens >= 1, "batch=%lld tokens=%lld", (long long)s->batch,
@@ -413,8 +529,68 @@ int minitp_qwen2_create(const minitp_qwen2_config* cfg, const minitp_qwen2_weigh
   p->cos_tab = w->rope_cos;
   p->sin_tab = w->rope_sin;
   p->lw.assign(w->layers, w->layers + (size_t)c.num_layers * MINITP_W_PER_LAYER);
+  const int rc = p->init_loop(w);
+  if (rc) {
+    delete p;
+    return rc;
+  }
   *handle = p;
   return MINITP_OK;
+}
+
+int64_t minitp_qwen2_table_bytes(const minitp_qwen2_config* cfg) {
+  if (!cfg || cfg->num_layers < 1) return -1;
+  return (int64_t)cfg->num_layers * (int64_t)sizeof(minitp::LoopLayerW);
+}
+
+int minitp_qwen2_set_decode_path(void* handle, int path) {
+  MINITP_CHECK_ARG(handle != nullptr, "NULL handle");
+  MINITP_CHECK_ARG(path == MINITP_DECODE_AUTO || path == MINITP_DECODE_GRAPH || path == MINITP_DECODE_PERSISTENT,
+                   "decode path %d", path);
+  ((Qwen2Program*)handle)->decode_path = path;
+  return MINITP_OK;
+}
+
+int64_t minitp_qwen2_trace_bytes(void* handle) {
+  if (!handle) return -1;
+  auto* p = (Qwen2Program*)handle;
+  return (int64_t)minitp::LOOP_MAX_BLOCKS * minitp::loop_trace_slots(p->c.num_layers) * (minitp::LOOP_THREADS / 64) * 8;
+}
+
+int minitp_qwen2_set_trace(void* handle, void* trace, int64_t bytes) {
+  MINITP_CHECK_ARG(handle != nullptr, "NULL handle");
+  auto* p = (Qwen2Program*)handle;
+  MINITP_CHECK_ARG(trace == nullptr || bytes >= minitp_qwen2_trace_bytes(handle), "trace buffer too small");
+  p->trace = (uint64_t*)trace;
+  return MINITP_OK;
+}
+
+int minitp_qwen2_persistent_ok(void* handle) {
+  if (!handle) return 0;
+  auto* p = (Qwen2Program*)handle;
+  if (!p->loop_why.empty()) {
+    minitp::set_error("persistent decode unavailable: %s", p->loop_why.c_str());
+    return 0;
+  }
+  return 1;
+}
+
+int minitp_qwen2_decode_check(void* handle, void* stream, void* workspace) {
+  MINITP_CHECK_ARG(handle != nullptr && workspace != nullptr, "NULL argument");
+  MINITP_RETURN_HIP(hipStreamSynchronize((hipStream_t)stream));
+  uint32_t ctrl[4] = {0, 0, 0, 0};
+  MINITP_RETURN_HIP(hipMemcpy(ctrl, workspace, sizeof(ctrl), hipMemcpyDeviceToHost));
+  if (ctrl[minitp::LOOP_CTRL_ERROR] == 0 && ctrl[minitp::LOOP_CTRL_ABORT] == 0) return MINITP_OK;
+  const uint32_t err = ctrl[minitp::LOOP_CTRL_ERROR];
+  // clear the record (error and abort words; the step counter stays)
+  MINITP_RETURN_HIP(hipMemset((char*)workspace + 4 * minitp::LOOP_CTRL_ERROR, 0, 8));
+  if (err & minitp::LOOP_ERR_TIMEOUT || !(err & minitp::LOOP_ERR_POSITION)) {
+    minitp::set_error("persistent decode: a hand-off wait timed out (error bits 0x%x); the step's outputs are invalid",
+                      err);
+    return MINITP_ERR_HIP;
+  }
+  minitp::set_error("persistent decode: position outside the RoPE table");
+  return MINITP_ERR_RANGE;
 }
 
 int minitp_qwen2_destroy(void* handle) {
@@ -449,6 +625,14 @@ int minitp_qwen2_decode(void* handle, void* stream, const minitp_qwen2_step* ste
   int rc = p->check_step(step, w);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
+  const bool loop_ok = p->loop_why.empty() && step->batch == 1;
+  if (p->decode_path == MINITP_DECODE_PERSISTENT && !loop_ok) {
+    minitp::set_error("persistent decode unavailable: %s",
+                      step->batch != 1 ? "batch != 1" : p->loop_why.c_str());
+    return MINITP_ERR_UNSUPPORTED;
+  }
+  // AUTO takes the graph: it is the faster path at every measured shape
+  if (loop_ok && p->decode_path == MINITP_DECODE_PERSISTENT) return p->run_loop(st, *step);
   std::lock_guard<std::mutex> lock(p->mu);
   for (auto& g : p->graphs)
     if (g.batch == step->batch && g.max_seq == step->max_seq && g.workspace == step->workspace)

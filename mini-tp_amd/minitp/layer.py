@@ -84,9 +84,13 @@ class _Program:
                           cfg.head_dim, model.model.layers[0].mlp.intermediate_local, cfg.vocab_size,
                           model.rotary.max_seq_len, cfg.rms_norm_eps)
         arr = (ctypes.c_void_p * len(params))(*[p.data_ptr() for p in params])
+        # device memory for the persistent decode's per-layer weight table
+        nbytes = lib.minitp_qwen2_table_bytes(ctypes.byref(c))
+        self.table = torch.zeros(max(int(nbytes), 16), dtype=torch.uint8, device=head[0].device)
         w = N.Qwen2Weights(head[0].data_ptr(), head[1].data_ptr(), head[2].data_ptr(),
                            model.rotary.cos_cache.data_ptr(), model.rotary.sin_cache.data_ptr(),
-                           ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p)))
+                           ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p)), self.table.data_ptr(),
+                           self.table.numel())
         h = ctypes.c_void_p()
         N.check(lib.minitp_qwen2_create(ctypes.byref(c), ctypes.byref(w), ctypes.byref(h)), "qwen2_create")
         self.handle = h
@@ -94,6 +98,20 @@ class _Program:
         self.dtype = head[0].dtype
         self.fwd_ws: torch.Tensor | None = None
         self.decode_ws: dict[tuple[int, int], torch.Tensor] = {}
+
+    def set_decode_path(self, path: int) -> None:
+        """N.DECODE_AUTO (the graph of per-op kernels),
+        N.DECODE_GRAPH or N.DECODE_PERSISTENT."""
+        N.check(N.lib().minitp_qwen2_set_decode_path(self.handle, path), "qwen2_set_decode_path")
+
+    def persistent_ok(self) -> bool:
+        return bool(N.lib().minitp_qwen2_persistent_ok(self.handle))
+
+    def check_decode(self) -> None:
+        """Synchronise and raise if a persistent decode step on any of this
+        program's decode workspaces recorded a failure."""
+        for ws in self.decode_ws.values():
+            N.check(N.lib().minitp_qwen2_decode_check(self.handle, N.stream(), ws.data_ptr()), "qwen2_decode")
 
     def valid_for(self, model: "TPQwen2ForCausalLM") -> bool:
         return tuple(t.data_ptr() for t in self.tensors) == self.signature and \

@@ -130,6 +130,7 @@ def test_q05b_fp32_256_greedy_ids_bitexact():
     prompt = torch.from_numpy(fx["prompt"]).to(DEV)
     n = fx["ids"].shape[1] - prompt.shape[1]
     ids = generate_greedy(model, prompt, n, early_stop=False).cpu().numpy()
+    model.program().check_decode()
     mism = np.nonzero(ids[0] != fx["ids"][0])[0]
     assert mism.size == 0, f"first mismatch at column {mism[0]} (prompt {prompt.shape[1]})"
     rows, prefill = _teacher_forced_rows(model, prompt, torch.from_numpy(fx["ids"]), n)
@@ -167,9 +168,11 @@ def _tiny(dtype=torch.float32):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_graph_decode_equals_direct_forward(dtype):
+    from minitp import _native as N
     from minitp.generation import GenerationState, make_kv_cache
 
     model = _tiny(dtype)
+    model.program().set_decode_path(N.DECODE_GRAPH)  # the graph replays the direct launch sequence
     prompt = torch.tensor([[3, 17, 256, 999, 41]], device=DEV)
     st = GenerationState(model, prompt, 6)
     kv = make_kv_cache(model, 1, 11)
@@ -182,6 +185,70 @@ def test_graph_decode_equals_direct_forward(dtype):
         logits = st.decode_step(tok, pos)
         d = model(tok.unsqueeze(-1), positions=pos.reshape(1), kv_cache=kv)
         assert torch.equal(logits, d)
+
+
+def _decode_rows(model, prompt, ref_ids, n_steps, path):
+    from minitp import _native as N
+
+    model.program().set_decode_path(path)
+    try:
+        rows, _ = _teacher_forced_rows(model, prompt, ref_ids, n_steps)
+        model.program().check_decode()
+    finally:
+        model.program().set_decode_path(N.DECODE_AUTO)
+    return rows
+
+
+@pytest.mark.parametrize("shape_name", ["TINY", "QWEN05B"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_persistent_decode_matches_graph_decode(shape_name, dtype):
+    """The one-launch persistent decode and the graph of per-op kernels run
+    the same math with different summation orders: teacher-forced logits
+    agree to fp32 rounding (fp32) or within a few bf16 steps (bf16), and the
+    greedy picks agree wherever the top-2 margin is clear."""
+    from minitp import _native as N
+    from minitp.generation import generate_greedy
+
+    model = _synthetic(shape_name, dtype)
+    assert model.program().persistent_ok(), N.last_error()
+    v = model.cfg.vocab_size
+    prompt = torch.randint(0, v, (1, 16), generator=torch.Generator().manual_seed(5)).to(DEV)
+    model.program().set_decode_path(N.DECODE_PERSISTENT)
+    try:
+        ids = generate_greedy(model, prompt, 40, early_stop=False)
+        model.program().check_decode()
+    finally:
+        model.program().set_decode_path(N.DECODE_AUTO)
+    rp = _decode_rows(model, prompt, ids.cpu(), 40, N.DECODE_PERSISTENT)
+    rg = _decode_rows(model, prompt, ids.cpu(), 40, N.DECODE_GRAPH)
+    atol = 2e-4 if dtype == torch.float32 else 0.25
+    err = (rp - rg).abs().max().item()
+    assert err <= atol, err
+    top2 = rg.topk(2, dim=-1).values
+    clear = (top2[..., 0] - top2[..., 1]) > 2 * atol
+    assert torch.equal(rp.argmax(-1)[clear], rg.argmax(-1)[clear])
+    # the persistent path is what generate_greedy ran: its ids follow its own logits
+    assert torch.equal(rp.argmax(-1)[1:, 0].cpu(), ids[0, 17:].cpu())
+    print(f"{shape_name} {dtype}: persistent vs graph max logit diff {err:.3e}")
+
+
+def test_persistent_decode_steps_with_cursor_and_epochs():
+    """Many steps on one workspace (the step counter advances every launch)
+    and a fresh GenerationState reusing the program's workspace: the ids of
+    two identical generations match and no wait timed out."""
+    from minitp import _native as N
+    from minitp.generation import generate_greedy
+
+    model = _synthetic("TINY", torch.bfloat16)
+    prompt = torch.tensor([[5, 6, 7]], device=DEV)
+    model.program().set_decode_path(N.DECODE_PERSISTENT)
+    try:
+        a = generate_greedy(model, prompt, 60, early_stop=False)
+        b = generate_greedy(model, prompt, 60, early_stop=False)
+        model.program().check_decode()
+    finally:
+        model.program().set_decode_path(N.DECODE_AUTO)
+    assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
