@@ -29,21 +29,23 @@
 // stream x in LDS and applies both residual adds itself (layer.py:63-64), so
 // x never travels.
 //
-// Roles inside a block (8 waves): wave 0 is the only wave that waits on
-// hand-off words; it copies a phase's inputs into LDS and releases the block
-// through s_barrier, and it issues every other small global load. Waves 1..7
-// each stream the weights of ONE phase (the host splits them by bytes, e.g.
-// 1 QKV, 1 o_proj, 3 gate/up, 2 down at the 0.5B shape): a wave consumes its
-// phase's weights and at once issues the same phase's loads for the next
-// layer, so weights are requested one layer before they are used and HBM
-// latency stays off the critical path. Vector loads complete in issue order
-// per wave; giving each wave a single stream is what keeps a wait for one
-// load from also waiting for loads issued later (the compiler's waits are
-// conservative across the layer loop), and it is why the waiting is left to
-// wave 0 and why the barrier used here (s_barrier after the wave's own LDS
-// traffic) never waits on global loads. The o_proj wave(s) also copy the K/V
-// rows of the block's KV group global -> LDS (global_load_lds_dwordx4)
-// during phase A, ahead of attention.
+// Inside a block (8 waves): wave 0 is the only wave that waits on hand-off
+// words (it copies them global -> LDS with global_load_lds_dwordx4 and
+// re-reads only the copies still holding an older epoch); it also copies
+// the norm weights and the K / V rows of the block's KV group into LDS.
+// Waves 1..7 hold every phase's rows of the NEXT layer in registers
+// (buffer loads, issued after the current layer's results of that phase are
+// stored; the gate/up and down batches in three parts over three phases),
+// so weight latency stays off the critical path. All eight waves share the
+// glue (residual add + RMSNorm, one 4-element group per thread) and the
+// attention (scores and P V on MFMA 16x16x16 for bf16), meeting at
+// s_barrier; a weight wave's results go straight from its registers to its
+// hand-off words.
+//
+// Measured on MI355X at the 0.5B shape this path is slower than the graph of
+// per-op kernels: the hand-offs cost 2-7 us each, mostly waiting behind the
+// CU's own weight loads in the vector-memory queue, so it stays opt-in
+// (MINITP_DECODE_PERSISTENT).
 //
 // Every wait is bounded by the wall clock: a wave that times out raises an
 // abort word that ends every other wait, and sets an error bit the host
@@ -66,7 +68,8 @@ constexpr int GMAXL = 8;         // query heads per KV group served
 // Register batches (chunk columns x rows) of each role's weight stream:
 // everything a wave streams per layer at the 0.5B shape fits one batch;
 // larger shapes run several batches per phase.
-constexpr int JA = 2, SA = 8, JB = 2, SB = 8, JC = 2, SC = 14, JD = 10, SD = 2, JL = 2, SL = 14;  // J * S <= 28
+constexpr int JA = 2, SA = 2, JB = 1, SB = 2, JC = 2, SC = 8, JD = 10, SD = 1, JL = 2, SL = 14;
+constexpr int LOOP_ROWS_PER_WAVE = 64;  // LDS row results per weight wave (phases A, C)
 constexpr int ATT_KV_BYTES = 64 * 1024;  // LDS for one K + V position tile
 
 typedef __attribute__((address_space(3))) void lds_void;
@@ -80,6 +83,11 @@ __device__ __forceinline__ void ll_store(uint64_t* p, uint32_t epoch, uint32_t p
 // Block barrier over LDS: this wave's LDS operations complete, then
 // s_barrier. Outstanding global loads (prefetched weights) stay in flight.
 __device__ __forceinline__ void bar() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+// Waits for every outstanding vector-memory operation of this wave, as an
+// s_waitcnt the compiler sees: after it, the compiler knows that no LDS DMA
+// (global_load_lds) is in flight, so it adds no waits of its own before
+// later LDS reads in any wave (its analysis does not tell waves apart).
+__device__ __forceinline__ void wait_vm0() { __builtin_amdgcn_s_waitcnt(0x0F70); }  // vmcnt(0)
 // Orders LDS traffic between the lanes of one wave.
 __device__ __forceinline__ void wave_lds_fence() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
@@ -174,7 +182,7 @@ __device__ LOOP_GATHER_INLINE void ll_gather(const Ctx& c, const uint64_t* src, 
   uint64_t pending = nins >= 64 ? ~0ull : (1ull << nins) - 1;
   const int64_t t0 = wall_clock64();
   for (int it = 1;; ++it) {
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    wait_vm0();
     uint64_t still = 0;
     for (int j = 0; j < nins; ++j) {
       if (!((pending >> j) & 1)) continue;
@@ -205,8 +213,10 @@ __device__ LOOP_GATHER_INLINE void ll_gather(const Ctx& c, const uint64_t* src, 
 __device__ __forceinline__ uint32_t payload(uint64_t w) { return (uint32_t)w; }
 
 // A wave's rows of one weight matrix, read with buffer loads. Lane l owns
-// the contiguous 16-byte chunks [l * cpl, l * cpl + cpl) of every row (nch
-// chunks). The buffer resource covers the matrix from `base` (bytes bytes;
+// the 16-byte chunks l, l + 64, ... (cpl of them) of every row (nch chunks),
+// so one wave-instruction reads 1 KiB of a row contiguously and the LDS
+// input vector is read the same way, free of bank conflicts. The buffer
+// resource covers the matrix from `base` (bytes bytes;
 // the range check counts the scalar row offset too), and a chunk past the
 // row end gets a lane offset beyond that range, so it reads as zeros. The
 // wave has ns rows (slots); slot s starts at byte offset row_off(s).
@@ -229,9 +239,8 @@ __device__ __forceinline__ Rows make_rows(const void* base, int64_t bytes, int n
 
 typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 
-// A wave's register batch: BUFW 16-byte loads, used by each stream as
-// J chunk columns x S slots (J * S <= BUFW), load (j, s) at index j * S + s.
-constexpr int BUFW = 28;
+// A register batch of a stream: J chunk columns x S slots, load (j, s) at
+// index j * S + s.
 
 // Issue the batch of slots [sb, sb + S) x columns [jb, jb + J). Every load
 // is issued; loads outside the stream get an out-of-range lane offset and
@@ -247,36 +256,48 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const Rows& q) {
   return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, bytes, 0x00020000);
 }
 
-template <int J, int S, class RowFn>
-__device__ __forceinline__ void rows_issue(uint4 (&buf)[BUFW], const Rows& q, RowFn row_off, int sb, int jb,
-                                           int lane) {
-  static_assert(J * S <= BUFW, "batch larger than the register buffer");
-  const __amdgpu_buffer_rsrc_t rsrc = rows_rsrc(q);
-  uint32_t vo[J];
-#pragma unroll
-  for (int j = 0; j < J; ++j) {
-    const int cc = lane * q.cpl + jb + j;
-    vo[j] = (cc < q.nch && jb + j < q.cpl) ? (uint32_t)cc * 16u : OFF_RANGE;
-  }
-#pragma unroll
-  for (int s = 0; s < S; ++s) {
-    const bool live = sb + s < q.ns;
-    const uint32_t so = live ? row_off(sb + s) : 0u;
+// Issue loads [T0, T1) of the batch of slots [sb, sb + S) x columns
+// [jb, jb + J), load t being (slot t / J, column t % J): a batch can go out
+// in parts, spread over time. Every load is issued; loads outside the
+// stream get an out-of-range lane offset and return zeros without touching
+// memory, so the code has no branches.
+template <int J, int S, int T0, int T1, int N, class RowFn>
+__device__ __forceinline__ void rows_issue_part(uint4 (&buf)[N], const Rows& q, RowFn row_off, int sb, int jb,
+                                                int lane) {
+  static_assert(J * S <= N, "batch larger than the register buffer");
+  static_assert(0 <= T0 && T0 <= T1 && T1 <= J * S, "part outside the batch");
+  if constexpr (T1 > T0) {
+    const __amdgpu_buffer_rsrc_t rsrc = rows_rsrc(q);
+    uint32_t vo[J];
 #pragma unroll
     for (int j = 0; j < J; ++j) {
-      const u32x4v v = __builtin_bit_cast(
-          u32x4v, __builtin_amdgcn_raw_buffer_load_b128(rsrc, live ? vo[j] : OFF_RANGE,
-                                                        __builtin_amdgcn_readfirstlane(so), 2 /* nt */));
-      buf[j * S + s] = make_uint4(v.x, v.y, v.z, v.w);
+      const int cc = (jb + j) * 64 + lane;
+      vo[j] = cc < q.nch ? (uint32_t)cc * 16u : OFF_RANGE;
+    }
+#pragma unroll
+    for (int s = T0 / J; s <= (T1 - 1) / J; ++s) {
+      const bool live = sb + s < q.ns;
+      const uint32_t so = __builtin_amdgcn_readfirstlane(live ? row_off(sb + s) : 0u);
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        if (s * J + j < T0 || s * J + j >= T1) continue;
+        const u32x4v v = __builtin_bit_cast(
+            u32x4v, __builtin_amdgcn_raw_buffer_load_b128(rsrc, live ? vo[j] : OFF_RANGE, so, 2 /* nt */));
+        buf[j * S + s] = make_uint4(v.x, v.y, v.z, v.w);
+      }
     }
   }
+}
+template <int J, int S, int N, class RowFn>
+__device__ __forceinline__ void rows_issue(uint4 (&buf)[N], const Rows& q, RowFn row_off, int sb, int jb, int lane) {
+  rows_issue_part<J, S, 0, J * S>(buf, q, row_off, sb, jb, lane);
 }
 
 // Dot every row of the stream with the LDS input x, batch by batch; the
 // first batch (sb = 0, jb = 0) was issued by the caller. Hands each row's
 // wave-reduced sum to done(slot, value) (executed by every lane).
-template <typename T, int J, int S, class RowFn, class DoneFn>
-__device__ __forceinline__ void rows_consume(uint4 (&buf)[BUFW], const Rows& q, RowFn row_off, const uint4* x,
+template <typename T, int J, int S, int N, class RowFn, class DoneFn>
+__device__ __forceinline__ void rows_consume(uint4 (&buf)[N], const Rows& q, RowFn row_off, const uint4* x,
                                              int lane, DoneFn done) {
   for (int sb = 0; sb < q.ns; sb += S) {
     float acc[S];
@@ -287,8 +308,8 @@ __device__ __forceinline__ void rows_consume(uint4 (&buf)[BUFW], const Rows& q, 
       uint4 xj[J];
 #pragma unroll
       for (int j = 0; j < J; ++j) {
-        const int cc = lane * q.cpl + jb + j;
-        xj[j] = (cc < q.nch && jb + j < q.cpl) ? x[cc] : make_uint4(0, 0, 0, 0);
+        const int cc = (jb + j) * 64 + lane;
+        xj[j] = cc < q.nch ? x[cc] : make_uint4(0, 0, 0, 0);
       }
 #pragma unroll
       for (int s = 0; s < S; ++s)
@@ -301,24 +322,6 @@ __device__ __forceinline__ void rows_consume(uint4 (&buf)[BUFW], const Rows& q, 
       if (sb + s < q.ns) done(sb + s, v);
     }
   }
-}
-
-// xin = dtype((x * rsqrt(mean(x^2) + eps)) * w), fp32 math (layer.py:39-42).
-// w is the norm weight already copied into LDS (norm_fetch).
-template <typename T>
-__device__ __forceinline__ void block_rmsnorm(const Ctx& c, const float* xs, const T* w, T* xin, float* red) {
-  const int H = c.p->H;
-  float ss = 0.f;
-  for (int i = c.tid; i < H; i += LT) ss = add_rn(ss, mul_rn(xs[i], xs[i]));
-  ss = wave_sum(ss);
-  if (c.lane == 0) red[c.wave] = ss;
-  bar();
-  float tot = 0.f;
-#pragma unroll
-  for (int k = 0; k < LWAVES; ++k) tot += red[k];
-  const float r = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(tot, (float)H), c.p->eps)));
-  for (int i = c.tid; i < H; i += LT) store_f32<T>(xin, i, mul_rn(mul_rn(xs[i], r), load_f32<T>(w, i)));
-  bar();
 }
 
 // Wave 0: copy `bytes` bytes of a global vector into LDS (1 KiB per
@@ -365,6 +368,7 @@ struct Loop {
   static constexpr int TP = TP0 > 256 ? 256 : TP0;  // positions per K / V tile
   static constexpr int LPR = D / 8;                  // P V lanes per value row (8 elements each)
   static constexpr int RPI = 64 / LPR;               // value rows per P V step
+  static constexpr int RPW = LOOP_ROWS_PER_WAVE;     // per-wave row results in LDS (phases A, C)
 
   // Hand-off word of RoPE pair (head hd, dim i): grouped by KV group, each
   // group's G q heads, then its k head, then its v head, so that a phase-B
@@ -385,18 +389,25 @@ struct Loop {
     return ((int64_t)(g * (G + 2) + hh) * HALF + i) * WPP;
   }
 
+  // The weight waves w = 1 .. NCW take every phase's rows, rw = w - 1 of
+  // nrw = NCW. A stream built with live == false has no rows: its loads
+  // return zeros without touching memory (the last layer's "next layer").
+
   // ---------------------------------------------------------------- phase A
   // Pair p = (head hd, dim i < D/2): rows hd * D + i and hd * D + i + D/2 of
   // the fused QKV weight (q heads, then k, then v; fused.py:60). Pair p goes
-  // to block p % nb; local pair lp = p / nb to role wave lp % nrw, whose
+  // to block p % nb; local pair lp = p / nb to weight wave lp % nrw, whose
   // slots 2t, 2t + 1 are the two rows of its t-th pair.
   __device__ __forceinline__ static int a_pairs_block(const Ctx& c) {
     const int npa = (c.p->Hq + 2 * c.p->Hkv) * HALF;
     return c.b < npa ? (npa - 1 - c.b) / c.nb + 1 : 0;
   }
-  __device__ __forceinline__ static Rows a_q(const Ctx& c, const LoopLayerW& lw, int npb, int rw, int nrw) {
-    const int my = rw < npb ? (npb - 1 - rw) / nrw + 1 : 0;
-    return make_rows(lw.wqkv, (int64_t)(c.p->Hq + 2 * c.p->Hkv) * D * c.p->H * sizeof(T), c.p->H / VEC, 2 * my);
+  __device__ __forceinline__ static int a_my(int npb, int rw, int nrw) {
+    return rw < npb ? (npb - 1 - rw) / nrw + 1 : 0;
+  }
+  __device__ __forceinline__ static Rows a_q(const Ctx& c, const LoopLayerW& lw, int my, bool live) {
+    return make_rows(lw.wqkv, (int64_t)(c.p->Hq + 2 * c.p->Hkv) * D * c.p->H * sizeof(T), c.p->H / VEC,
+                     live ? 2 * my : 0);
   }
   __device__ __forceinline__ static auto a_rows(const Ctx& c, int rw, int nrw) {
     const int nb = c.nb, b = c.b;
@@ -407,11 +418,17 @@ struct Loop {
       return (uint32_t)(hd * D + i + (s & 1) * HALF) * row_bytes;
     };
   }
+  // (head, dim) of this wave's t-th pair
+  __device__ __forceinline__ static void a_pair(const Ctx& c, int rw, int nrw, int t, int& hd, int& i) {
+    const int p = c.b + c.nb * (rw + nrw * t);
+    hd = p / HALF;
+    i = p % HALF;
+  }
 
   // ---------------------------------------------------------------- phase B
   // Block b < Hkv * RS serves KV group g = b % Hkv and output rows
   // [r0, r1) = slice b / Hkv of RS equal slices of H; row r0 + k goes to
-  // role wave k % nrw. The buffer starts at the group's first column of
+  // weight wave k % nrw. The buffer starts at the group's first column of
   // o_proj, so a row is G * D long.
   __device__ __forceinline__ static void b_rows_range(const Ctx& c, int& g, int& r0, int& r1) {
     const int Hkv = c.p->Hkv, rs = c.nb / Hkv;
@@ -424,10 +441,12 @@ struct Loop {
     r0 = sl * c.p->H / rs;
     r1 = (sl + 1) * c.p->H / rs;
   }
-  __device__ __forceinline__ static Rows b_q(const Ctx& c, const LoopLayerW& lw, int g, int nrows, int rw, int nrw) {
+  __device__ __forceinline__ static Rows b_q(const Ctx& c, const LoopLayerW& lw, int g, int nrows, int rw, int nrw,
+                                             bool live) {
     const int my = rw < nrows ? (nrows - 1 - rw) / nrw + 1 : 0;
     const int64_t off = (int64_t)g * c.p->G * D;
-    return make_rows((const T*)lw.wo + off, ((int64_t)c.p->H * c.p->Hq * D - off) * sizeof(T), c.p->G * D / VEC, my);
+    return make_rows((const T*)lw.wo + off, ((int64_t)c.p->H * c.p->Hq * D - off) * sizeof(T), c.p->G * D / VEC,
+                     live ? my : 0);
   }
   __device__ __forceinline__ static auto b_rows(const Ctx& c, int r0, int rw, int nrw) {
     const uint32_t row_bytes = (uint32_t)c.p->Hq * D * sizeof(T);
@@ -435,38 +454,39 @@ struct Loop {
   }
 
   // ---------------------------------------------------------------- phase C
-  // Units of EPW intermediate indices; block b gets units [u0, u1). Block
-  // row br: index j = u0 * EPW + br / 2, gate (br even) or up (odd) row;
-  // block row br goes to role wave br % nrw.
+  // Units of EPW intermediate indices; block b gets units [u0, u1), unit
+  // u0 + k to weight wave k % nrw. A wave's t-th unit fills slots
+  // 2 EPW t .. 2 EPW t + 2 EPW - 1: slot 2 e + 0 / 1 is the gate / up row of
+  // index (u0 + rw + nrw t) * EPW + e.
   __device__ __forceinline__ static void c_range(const Ctx& c, int& u0, int& u1) {
     const int nu = c.p->I / EPW;
     u0 = c.b * nu / c.nb;
     u1 = (c.b + 1) * nu / c.nb;
   }
-  __device__ __forceinline__ static Rows c_q(const Ctx& c, const LoopLayerW& lw, int nrows, int rw, int nrw) {
-    const int my = rw < nrows ? (nrows - 1 - rw) / nrw + 1 : 0;
-    return make_rows(lw.wgu, (int64_t)2 * c.p->I * c.p->H * sizeof(T), c.p->H / VEC, my);
+  __device__ __forceinline__ static Rows c_q(const Ctx& c, const LoopLayerW& lw, int my_units, bool live) {
+    return make_rows(lw.wgu, (int64_t)2 * c.p->I * c.p->H * sizeof(T), c.p->H / VEC, live ? 2 * EPW * my_units : 0);
   }
   __device__ __forceinline__ static auto c_rows(const Ctx& c, int u0, int rw, int nrw) {
     const int I = c.p->I;
     const uint32_t row_bytes = (uint32_t)c.p->H * sizeof(T);
     return [=](int s) -> uint32_t {
-      const int br = rw + nrw * s;
-      return (uint32_t)((br & 1) * I + u0 * EPW + (br >> 1)) * row_bytes;
+      const int t = s / (2 * EPW), k = s % (2 * EPW);
+      return (uint32_t)((k & 1) * I + (u0 + rw + nrw * t) * EPW + (k >> 1)) * row_bytes;
     };
   }
 
   // ---------------------------------------------------------------- phase D
   // Units of EPW output rows; block b gets units [u0, u1); block row k goes
-  // to role wave k % nrw.
+  // to weight wave k % nrw.
   __device__ __forceinline__ static void d_range(const Ctx& c, int& u0, int& u1) {
     const int nu = c.p->H / EPW;
     u0 = c.b * nu / c.nb;
     u1 = (c.b + 1) * nu / c.nb;
   }
-  __device__ __forceinline__ static Rows d_q(const Ctx& c, const LoopLayerW& lw, int nrows, int rw, int nrw) {
+  __device__ __forceinline__ static Rows d_q(const Ctx& c, const LoopLayerW& lw, int nrows, int rw, int nrw,
+                                             bool live) {
     const int my = rw < nrows ? (nrows - 1 - rw) / nrw + 1 : 0;
-    return make_rows(lw.wdown, (int64_t)c.p->H * c.p->I * sizeof(T), c.p->I / VEC, my);
+    return make_rows(lw.wdown, (int64_t)c.p->H * c.p->I * sizeof(T), c.p->I / VEC, live ? my : 0);
   }
   __device__ __forceinline__ static auto d_rows(const Ctx& c, int u0, int rw, int nrw) {
     const uint32_t row_bytes = (uint32_t)c.p->I * sizeof(T);
@@ -502,15 +522,16 @@ struct Loop {
     float* kn;  // [D]
     float* vn;  // [D]
     float* sc;  // [GMAXL][TP]
+    float* st;  // [4][GMAXL] softmax factors
   };
 
-  // Copy cached rows [p0, p0 + np) of the group's K and V into the tiles,
-  // global -> LDS without registers. Wave-instruction j moves slots
-  // [64 j, 64 j + 64); instructions are dealt to waves w0, w0 + 1, ... < w1.
+  // Wave 0: copy cached rows [p0, p0 + np) of the group's K and V into the
+  // tiles, global -> LDS without registers; wave-instruction j moves slots
+  // [64 j, 64 j + 64). The caller waits (wait_vm0) before the tiles are read.
   __device__ __forceinline__ static void tile_load(const Ctx& c, const T* kc, const T* vc, int p0, int np,
-                                                   const AttnLds& s, int w0, int w1) {
+                                                   const AttnLds& s) {
     const int nins = (np * PPR + 63) / 64;
-    for (int j = c.wave - w0; j < 2 * nins; j += w1 - w0) {
+    for (int j = 0; j < 2 * nins; ++j) {
       const bool is_v = j >= nins;
       const int jj = is_v ? j - nins : j;
       const int slot = jj * 64 + c.lane;
@@ -522,6 +543,161 @@ struct Loop {
     }
   }
 
+  // bf16 attention on matrix cores. Per tile: scores S = Q K^T by MFMA
+  // 16x16x16 (rows = the group's q heads padded to 16, columns = 16
+  // positions; wave w takes position blocks w, w + 8, ...), kept in LDS
+  // pre-multiplied by scale * log2(e); wave h runs head h's online softmax in
+  // base 2 over the tile, leaving P = 2^(S - m) in place and the factor that
+  // rescales earlier tiles in s.st[h]; then O += P V by MFMA (rows = heads,
+  // columns = 16 dims, inner = 16 positions; P rounded to bf16 as the MFMA
+  // operand, accumulation in fp32), wave w owning dim block w % (D / 16) and
+  // every (8 / (D / 16))-th position step. Finally the current position
+  // (k, v from the hand-off) joins the softmax, the position-step partials
+  // are summed through LDS and the output, rounded to bf16, goes to xin.
+  __device__ __forceinline__ static void attention_mfma(const Ctx& c, int layer, int g, const AttnLds& s, T* xin,
+                                                        int trs) {
+    typedef short short4_t __attribute__((ext_vector_type(4)));
+    typedef float float4_t __attribute__((ext_vector_type(4)));
+    constexpr int KS = D / 16;                // 16-dim steps of a score
+    constexpr int NBK = D / 16;               // 16-dim output blocks
+    constexpr int KH = LWAVES / NBK;          // waves sharing an output block
+    constexpr float LOG2E = 1.4426950408889634f;
+    const LoopParams& p = *c.p;
+    const int G = p.G;
+    const int cached = (int)p.cache_len;
+    const int64_t lay = (int64_t)layer * p.Hkv * p.S * D + (int64_t)g * p.S * D;
+    const T* kc = (const T*)p.k_cache + lay;
+    const T* vc = (const T*)p.v_cache + lay;
+    const int lr = c.lane % 16, lq = c.lane / 16;
+    const int nbk = c.wave % NBK, kh = c.wave / NBK;
+    const float sl2 = p.scale * LOG2E;
+    float* alpha_s = s.st;              // [GMAXL] rescale factor of the tile
+    float* fin_a = s.st + GMAXL;        // [GMAXL] final factors
+    float* fin_p = s.st + 2 * GMAXL;
+    float* fin_l = s.st + 3 * GMAXL;
+    // head h's running max and sum (wave h)
+    float m = -__builtin_inff(), l = 0.f;
+    float4_t o = {0.f, 0.f, 0.f, 0.f};  // O[4 lq + i][16 nbk + lr], partial over this wave's position steps
+    short4_t qa[KS];
+#pragma unroll
+    for (int kb = 0; kb < KS; ++kb) {
+      const uint2 v = lr < G ? *(const uint2*)(s.q + lr * D + kb * 16 + 4 * lq) : make_uint2(0, 0);
+      qa[kb] = __builtin_bit_cast(short4_t, v);
+    }
+    for (int p0 = 0; p0 < cached; p0 += TP) {
+      const int np = cached - p0 < TP ? cached - p0 : TP;
+      if (p0 > 0) {
+        bar();  // every wave is done with the previous tile
+        if (c.wave == 0) {
+          tile_load(c, kc, vc, p0, np, s);
+          wait_vm0();
+        }
+        bar();
+      }
+      // ---- scores
+      for (int blk = c.wave; blk * 16 < np; blk += LWAVES) {
+        const int r = blk * 16 + lr;
+        const char* krow = s.kt + r * PPR * 16;
+        float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < KS; ++kb) {
+          const int piece = 2 * kb + (lq >> 1);
+          const uint2 v = r < np ? *(const uint2*)(krow + ((piece ^ (r % PPR)) * 16) + (lq & 1) * 8) : make_uint2(0, 0);
+          acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(qa[kb], __builtin_bit_cast(short4_t, v), acc, 0, 0, 0);
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int hh = 4 * lq + i;
+          if (hh < G && r < np) s.sc[hh * TP + r] = acc[i] * sl2;
+        }
+      }
+      bar();
+      c.mark(trs + LOOP_TR_ATT_SC);
+      // ---- wave h: head h's softmax over the tile (base 2)
+      if (c.wave < G) {
+        float* sh = s.sc + c.wave * TP;
+        float mx = -__builtin_inff();
+        for (int r = c.lane; r < np; r += 64) mx = fmaxf(mx, sh[r]);
+        const float mn = fmaxf(m, wave_max(mx));
+        const float alpha = __builtin_amdgcn_exp2f(m - mn);
+        float ls = 0.f;
+        for (int r = c.lane; r < np; r += 64) {
+          const float pr = __builtin_amdgcn_exp2f(sh[r] - mn);
+          sh[r] = pr;
+          ls += pr;
+        }
+        l = fmaf(l, alpha, wave_sum(ls));
+        m = mn;
+        if (c.lane == 0) alpha_s[c.wave] = alpha;
+      }
+      bar();
+      // ---- O = O * alpha + P V over this wave's position steps
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int hh = 4 * lq + i;
+        o[i] *= hh < G ? alpha_s[hh] : 1.f;
+      }
+      const int dcol = nbk * 16 + lr;  // this lane's output dim
+      const int dpc = dcol / 8, dofs = (dcol % 8) * 2;
+      for (int ks = kh; ks * 16 < np; ks += KH) {
+        const int k0 = ks * 16 + 4 * lq;  // this lane's 4 positions
+        float4 pv = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (lr < G) pv = *(const float4*)(s.sc + lr * TP + k0);
+        const float pp[4] = {pv.x, pv.y, pv.z, pv.w};
+        uint32_t pa[2], vb[2];
+#pragma unroll
+        for (int e = 0; e < 4; e += 2) {
+          const float a0 = k0 + e < np ? pp[e] : 0.f, a1 = k0 + e + 1 < np ? pp[e + 1] : 0.f;
+          pa[e / 2] = (uint32_t)f32_to_bf16(a0) | ((uint32_t)f32_to_bf16(a1) << 16);
+          uint32_t v0 = 0, v1 = 0;
+          const int r0 = k0 + e, r1 = k0 + e + 1;
+          if (r0 < np) v0 = *(const uint16_t*)(s.vt + r0 * PPR * 16 + ((dpc ^ (r0 % PPR)) * 16) + dofs);
+          if (r1 < np) v1 = *(const uint16_t*)(s.vt + r1 * PPR * 16 + ((dpc ^ (r1 % PPR)) * 16) + dofs);
+          vb[e / 2] = v0 | (v1 << 16);
+        }
+        o = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(short4_t, make_uint2(pa[0], pa[1])),
+                                                      __builtin_bit_cast(short4_t, make_uint2(vb[0], vb[1])), o, 0, 0,
+                                                      0);
+      }
+    }
+    c.mark(trs + LOOP_TR_ATT_PV);
+    // ---- the current position (its k and v came through the hand-off)
+    if (c.wave < G) {
+      float sp = 0.f;
+      for (int d = c.lane; d < D; d += 64) sp = fmaf(load_f32<T>(s.q, c.wave * D + d), s.kn[d], sp);
+      const float sv = wave_sum(sp) * sl2;
+      const float mn = fmaxf(m, sv);
+      const float alpha = __builtin_amdgcn_exp2f(m - mn);
+      const float pr = __builtin_amdgcn_exp2f(sv - mn);
+      if (c.lane == 0) {
+        fin_a[c.wave] = alpha;
+        fin_p[c.wave] = pr;
+        fin_l[c.wave] = fmaf(l, alpha, pr);
+      }
+    }
+    // partials of the position steps -> the kh == 0 wave of each dim block
+    float* part = s.sc;  // free now: [KH - 1][NBK][64 lanes][4]
+    if (KH > 1 && kh > 0) *(float4*)(part + (((kh - 1) * NBK + nbk) * 64 + c.lane) * 4) = make_float4(o[0], o[1], o[2], o[3]);
+    bar();
+    if (kh == 0) {
+#pragma unroll
+      for (int k = 1; k < KH; ++k) {
+        const float4 q4 = *(const float4*)(part + (((k - 1) * NBK + nbk) * 64 + c.lane) * 4);
+        o[0] += q4.x;
+        o[1] += q4.y;
+        o[2] += q4.z;
+        o[3] += q4.w;
+      }
+      const int d = nbk * 16 + lr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int hh = 4 * lq + i;
+        if (hh < G) store_f32<T>(xin, hh * D + d, fmaf(fin_p[hh], s.vn[d], o[i] * fin_a[hh]) / fin_l[hh]);
+      }
+    }
+    bar();
+  }
+
   // GQA attention of the block's KV group g for its G query heads over
   // ctx = cache_len + 1 positions: cached rows from K / V tiles in LDS (the
   // first tile was loaded during phase A), the current row from s.kn / s.vn.
@@ -529,7 +705,7 @@ struct Loop {
   // runs head h's online softmax over the tile and its P V (lane = dims).
   // The output, rounded to T, goes to xin (the o_proj input).
   __device__ __forceinline__ static void attention(const Ctx& c, int layer, int g, const AttnLds& s, T* xin,
-                                                   bool tile_loader, int trs) {
+                                                   int trs) {
     const LoopParams& p = *c.p;
     const int G = p.G;
     const int cached = (int)p.cache_len;
@@ -546,13 +722,47 @@ struct Loop {
       const int np = cached - p0 < TP ? cached - p0 : TP;
       if (p0 > 0) {
         bar();  // every wave is done with the previous tile
-        if (tile_loader) {  // the o_proj wave(s)
-          tile_load(c, kc, vc, p0, np, s, p.role[1], p.role[2]);
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (c.wave == 0) {
+          tile_load(c, kc, vc, p0, np, s);
+          wait_vm0();
         }
         bar();
       }
-      // ---- scores of the tile: thread = position, every head
+      // ---- scores of the tile
+      if constexpr (EPW == 2) {
+        // MFMA 16x16x16 (bf16 in, fp32 out): A = the q heads (rows, padded
+        // to 16), B = 16 positions' keys; lane l holds A[l % 16][4 (l / 16) ..
+        // + 3] and B[4 (l / 16) .. + 3][l % 16] of each 16-dim step, and gets
+        // D[4 (l / 16) + i][l % 16]. Wave w scores position blocks w, w + 8, ...
+        typedef short short4_t __attribute__((ext_vector_type(4)));
+        typedef float float4_t __attribute__((ext_vector_type(4)));
+        constexpr int KS = D / 16;
+        const int lr = c.lane % 16, lq = c.lane / 16;
+        short4_t qa[KS];
+#pragma unroll
+        for (int kb = 0; kb < KS; ++kb) {
+          const uint2 v = lr < G ? *(const uint2*)(s.q + lr * D + kb * 16 + 4 * lq) : make_uint2(0, 0);
+          qa[kb] = __builtin_bit_cast(short4_t, v);
+        }
+        for (int blk = c.wave; blk * 16 < np; blk += LWAVES) {
+          const int r = blk * 16 + lr;
+          const char* krow = s.kt + r * PPR * 16;
+          float4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kb = 0; kb < KS; ++kb) {
+            const int piece = 2 * kb + (lq >> 1);
+            const uint2 v =
+                r < np ? *(const uint2*)(krow + ((piece ^ (r % PPR)) * 16) + (lq & 1) * 8) : make_uint2(0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(qa[kb], __builtin_bit_cast(short4_t, v), acc, 0, 0, 0);
+          }
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int hh = 4 * lq + i;
+            if (hh < G && r < np) s.sc[hh * TP + r] = acc[i] * p.scale;
+          }
+        }
+      } else
+      // thread = position, every head
       for (int r = c.tid; r < np; r += LT) {
         float a[GMAXL];
 #pragma unroll
@@ -620,13 +830,108 @@ struct Loop {
       const float mn = fmaxf(m, sv);
       const float alpha = expf(m - mn);
       const float pr = expf(sv - mn);
-      l = fmaf(l, alpha, pr);
+      const float lt = fmaf(l, alpha, pr);
       if (pg == 0) {
+        float o[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int d = dc * 8 + e;
-          store_f32<T>(xin, h * D + d, fmaf(pr, s.vn[d], acc[e] * alpha) / l);
+        for (int e = 0; e < 8; ++e) o[e] = fmaf(pr, s.vn[dc * 8 + e], acc[e] * alpha) / lt;
+        if constexpr (EPW == 2) {
+          *(uint4*)(xin + h * D + dc * 8) =
+              make_uint4(pack_word<T>(o), pack_word<T>(o + 2), pack_word<T>(o + 4), pack_word<T>(o + 6));
+        } else {
+          *(float4*)(xin + h * D + dc * 8) = make_float4(o[0], o[1], o[2], o[3]);
+          *(float4*)(xin + h * D + dc * 8 + 4) = make_float4(o[4], o[5], o[6], o[7]);
         }
+      }
+    }
+    bar();
+  }
+
+  // ---------------------------------------------------------------- block glue
+  // x += add (MODE 0: stage holds dtype words of the previous down; MODE 1:
+  // stage holds the Hkv groups' fp32 o_proj partials, rounded to the dtype
+  // once summed; MODE 2: nothing to add), each sum rounded to the dtype
+  // (layer.py:63-64); then xin = dtype((x * rsqrt(mean(x^2) + eps)) * w) in
+  // fp32 (layer.py:39-42), w being the norm weight in LDS. Thread t owns
+  // elements 4t .. 4t + 3 (H <= 4 * LT, checked on the host).
+  template <int MODE>
+  __device__ __forceinline__ static void x_add_norm(const Ctx& c, float* xs, const uint64_t* stage, const T* w,
+                                                    T* xin, float* red) {
+    const int H = c.p->H;
+    const int gi = c.tid;
+    const bool in = gi < H / 4;
+    float4* xs4 = (float4*)xs;
+    float xv[4] = {0.f, 0.f, 0.f, 0.f};
+    if (in) {
+      const float4 v = xs4[gi];
+      xv[0] = v.x;
+      xv[1] = v.y;
+      xv[2] = v.z;
+      xv[3] = v.w;
+      if constexpr (MODE == 0) {
+        const uint4* st4 = (const uint4*)stage;
+        float ad[4];
+        if constexpr (EPW == 2) {  // words 2 gi, 2 gi + 1
+          const uint4 a = st4[gi];
+          ad[0] = word_elem<T>(a.x, 0);
+          ad[1] = word_elem<T>(a.x, 1);
+          ad[2] = word_elem<T>(a.z, 0);
+          ad[3] = word_elem<T>(a.z, 1);
+        } else {
+          const uint4 a = st4[2 * gi], b = st4[2 * gi + 1];
+          ad[0] = __uint_as_float(a.x);
+          ad[1] = __uint_as_float(a.z);
+          ad[2] = __uint_as_float(b.x);
+          ad[3] = __uint_as_float(b.z);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[e] = round_to<T>(add_rn(xv[e], ad[e]));
+      } else if constexpr (MODE == 1) {
+        float ad[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int g = 0; g < c.p->Hkv; ++g) {
+          const uint4* st4 = (const uint4*)(stage + (int64_t)g * H);
+          const uint4 a = st4[2 * gi], b = st4[2 * gi + 1];
+          ad[0] += __uint_as_float(a.x);
+          ad[1] += __uint_as_float(a.z);
+          ad[2] += __uint_as_float(b.x);
+          ad[3] += __uint_as_float(b.z);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xv[e] = round_to<T>(add_rn(xv[e], round_to<T>(ad[e])));
+      }
+      if constexpr (MODE != 2) xs4[gi] = make_float4(xv[0], xv[1], xv[2], xv[3]);
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) ss = add_rn(ss, mul_rn(xv[e], xv[e]));
+    ss = wave_sum(ss);
+    if (c.lane == 0) red[c.wave] = ss;
+    bar();
+    float tot = 0.f;
+#pragma unroll
+    for (int k = 0; k < LWAVES; ++k) tot = add_rn(tot, red[k]);
+    const float r = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(tot, (float)H), c.p->eps)));
+    if (in) {
+      float wv[4], o[4];
+      if constexpr (EPW == 2) {
+        const uint2 a = ((const uint2*)w)[gi];
+        wv[0] = word_elem<T>(a.x, 0);
+        wv[1] = word_elem<T>(a.x, 1);
+        wv[2] = word_elem<T>(a.y, 0);
+        wv[3] = word_elem<T>(a.y, 1);
+      } else {
+        const float4 a = ((const float4*)w)[gi];
+        wv[0] = a.x;
+        wv[1] = a.y;
+        wv[2] = a.z;
+        wv[3] = a.w;
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = mul_rn(mul_rn(xv[e], r), wv[e]);
+      if constexpr (EPW == 2) {
+        ((uint2*)xin)[gi] = make_uint2(pack_word<T>(o), pack_word<T>(o + 2));
+      } else {
+        ((float4*)xin)[gi] = make_float4(o[0], o[1], o[2], o[3]);
       }
     }
     bar();
@@ -652,9 +957,9 @@ struct Loop {
     uint64_t* stage = (uint64_t*)(lds + p.lds_stage);    // gathered hand-off words
     uint64_t* qstage = (uint64_t*)(lds + p.lds_qstage);  // the group's q / k / v words
     float* rowres = (float*)(lds + p.lds_rowres);
-    T* nws = (T*)(lds + p.lds_norm);          // the current RMSNorm weight
-    float* red = (float*)(lds + p.lds_misc);  // [LWAVES]
-    float* amv = red + LWAVES;                // [LWAVES]
+    T* nws = (T*)(lds + p.lds_norm);  // the current RMSNorm weight
+    float* red = (float*)(lds + p.lds_misc);
+    float* amv = red + LWAVES;
     int64_t* ami = (int64_t*)(lds + p.lds_misc + 64 * 4);
     AttnLds at;  // K / V tiles in their own region; the rest aliases stage (free in phase B)
     at.kt = lds + p.lds_tile;
@@ -663,17 +968,16 @@ struct Loop {
     at.kn = (float*)(at.q + GMAXL * D);
     at.vn = at.kn + D;
     at.sc = at.vn + D;
+    at.st = at.sc + GMAXL * TP;
     const int H = p.H, Hq = p.Hq, Hkv = p.Hkv, G = p.G;
     const uint4* xin4 = (const uint4*)xin;
 
-    // this wave's role: 0 = hand-offs, 1 = QKV, 2 = o_proj (+ K / V tiles),
-    // 3 = gate/up, 4 = down weights
-    const int role = c.wave == 0 ? 0 : c.wave < p.role[1] ? 1 : c.wave < p.role[2] ? 2 : c.wave < p.role[3] ? 3 : 4;
-    const bool w0 = role == 0;
-    const int rw = role == 0 ? 0 : c.wave - p.role[role - 1];     // index within the role
-    const int nr = role == 0 ? 1 : p.role[role] - p.role[role - 1];  // waves in the role
+    const bool w0 = c.wave == 0;  // wave 0 waits on the hand-offs; waves 1.. stream weights
+    const int rw = c.wave - 1, nrw = NCW;
+    float* rw_res = rowres + (w0 ? 0 : rw) * RPW;  // this weight wave's row results (phases A, C)
 
     const int npb = a_pairs_block(c);
+    const int a_my_n = w0 ? 0 : a_my(npb, rw, nrw);
     int bg, br0, br1;
     b_rows_range(c, bg, br0, br1);
     const bool b_work = br1 > br0;
@@ -682,55 +986,79 @@ struct Loop {
     c_range(c, cu0, cu1);
     d_range(c, du0, du1);
     lm_range(c, lr0, lr1);
-    const int c_rows_n = 2 * EPW * (cu1 - cu0);
+    const int c_my = w0 ? 0 : (rw < cu1 - cu0 ? (cu1 - cu0 - 1 - rw) / nrw + 1 : 0);
     const int d_rows_n = EPW * (du1 - du0);
+    const int64_t pos = p.positions[0];
+    const bool pos_ok = pos >= 0 && pos < p.max_pos;
+    // wave 0: the first K / V tile of a layer's attention (rows below
+    // cache_len were written by earlier steps)
+    auto tile_first = [&](int layer) {
+      const int64_t lay_kv = (int64_t)layer * Hkv * p.S * D + (int64_t)bg * p.S * D;
+      const int np0 = (int)(p.cache_len < TP ? p.cache_len : TP);
+      tile_load(c, (const T*)p.k_cache + lay_kv, (const T*)p.v_cache + lay_kv, 0, np0, at);
+    };
 
-    // Issue this wave's weight stream of a layer (roles 1..4).
-    uint4 buf[BUFW];
-    auto issue_a = [&](const LoopLayerW& w) {
-      rows_issue<JA, SA>(buf, a_q(c, w, npb, rw, nr), a_rows(c, rw, nr), 0, 0, c.lane);
-    };
-    auto issue_b = [&](const LoopLayerW& w) {
-      rows_issue<JB, SB>(buf, b_q(c, w, bg, bn, rw, nr), b_rows(c, br0, rw, nr), 0, 0, c.lane);
-    };
-    auto issue_c = [&](const LoopLayerW& w) {
-      rows_issue<JC, SC>(buf, c_q(c, w, c_rows_n, rw, nr), c_rows(c, cu0, rw, nr), 0, 0, c.lane);
-    };
-    auto issue_d = [&](const LoopLayerW& w) {
-      rows_issue<JD, SD>(buf, d_q(c, w, d_rows_n, rw, nr), d_rows(c, du0, rw, nr), 0, 0, c.lane);
-    };
-    // the o_proj wave(s) copy a layer's first K / V tile into LDS one layer
-    // ahead (rows below cache_len were written by earlier steps)
-    auto tile_next = [&](int layer) {
-      if (b_work) {
-        const int64_t lay_kv = (int64_t)layer * Hkv * p.S * D + (int64_t)bg * p.S * D;
-        const int np0 = (int)(p.cache_len < TP ? p.cache_len : TP);
-        tile_load(c, (const T*)p.k_cache + lay_kv, (const T*)p.v_cache + lay_kv, 0, np0, at, p.role[1], p.role[2]);
+    // register batches: the next layer's rows of every phase
+    uint4 bufA[JA * SA], bufB[JB * SB], bufC[JC * SC], bufD[JD * SD];
+    // The gate/up and down batches go out in three parts each, after the
+    // stores of three different phases, so that the loads of a phase's
+    // weights are not one burst.
+    constexpr int NC = JC * SC, ND = JD * SD;
+#define ISSUE_C(K, W, LIVE) \
+  rows_issue_part<JC, SC, NC*(K) / 3, NC*((K) + 1) / 3>(bufC, c_q(c, W, c_my, LIVE), rc, 0, 0, c.lane)
+#define ISSUE_D(K, W, LIVE) \
+  rows_issue_part<JD, SD, ND*(K) / 3, ND*((K) + 1) / 3>(bufD, d_q(c, W, d_rows_n, rw, nrw, LIVE), rd, 0, 0, c.lane)
+    const auto ra = a_rows(c, rw, nrw);
+    const auto rb = b_rows(c, br0, rw, nrw);
+    const auto rc = c_rows(c, cu0, rw, nrw);
+    const auto rd = d_rows(c, du0, rw, nrw);
+    // lane 2 t + k: the k-th bias of the wave's t-th pair (loaded with the
+    // layer's QKV rows) and its RoPE cos / sin (the same for every layer)
+    float biasv = 0.f, cosv = 0.f, sinv = 0.f;
+    const int a_lane_t = c.lane >> 1, a_lane_k = c.lane & 1;
+    auto issue_bias = [&](const LoopLayerW& w, bool live) {
+      if (!w0) {
+        int hd, i;
+        a_pair(c, rw, nrw, a_lane_t, hd, i);
+        const bool in = live && a_lane_t < a_my_n;
+        const int k = in ? hd * D + i + a_lane_k * HALF : 0;
+        if constexpr (EPW == 2) {
+          typedef __attribute__((address_space(1))) const uint16_t gU16;
+          biasv = bf16_to_f32(((const gU16*)w.bqkv)[k]);
+        } else {
+          typedef __attribute__((address_space(1))) const float gF;
+          biasv = ((const gF*)w.bqkv)[k];
+        }
       }
     };
-    if (role == 1) issue_a(p.layers[0]);
-    if (role == 2) {
-      tile_next(0);
-      issue_b(p.layers[0]);
-    }
-    if (role == 3) issue_c(p.layers[0]);
-    if (role == 4) issue_d(p.layers[0]);
-
-    // ---- embedding (embedding.py:44-46): every block gathers the row. Only
-    // wave 0 issues plain global loads: in waves 1..7 they would complete
-    // behind the streamed weights.
-    if (w0) {
+    if (!w0) {
+      int hd, i;
+      a_pair(c, rw, nrw, a_lane_t, hd, i);
+      if (pos_ok && a_lane_t < a_my_n && hd < Hq + Hkv) {
+        typedef __attribute__((address_space(1))) const float gF;
+        cosv = ((const gF*)p.cos_tab)[pos * D + i + a_lane_k * HALF];
+        sinv = ((const gF*)p.sin_tab)[pos * D + i + a_lane_k * HALF];
+      }
+      const LoopLayerW& l0 = p.layers[0];
+      rows_issue<JA, SA>(bufA, a_q(c, l0, a_my_n, true), ra, 0, 0, c.lane);
+      issue_bias(l0, true);
+      rows_issue<JB, SB>(bufB, b_q(c, l0, bg, bn, rw, nrw, true), rb, 0, 0, c.lane);
+      ISSUE_C(0, l0, true);
+      ISSUE_C(1, l0, true);
+      ISSUE_D(0, l0, true);
+    } else {
+      // embedding (embedding.py:44-46): every block gathers the row
       const int64_t id = p.ids[0];
       const bool ok = id >= 0 && id < p.V;
       const T* row = (const T*)p.embed + (ok ? id : 0) * H;
       for (int i = c.lane; i < H; i += 64) xs[i] = ok ? load_f32<T>(row, i) : __builtin_nanf("");
+      if (!pos_ok && c.b == 0 && c.lane == 0)
+        __hip_atomic_fetch_or(&p.ctrl[LOOP_CTRL_ERROR], (uint32_t)LOOP_ERR_POSITION, __ATOMIC_RELAXED,
+                              __HIP_MEMORY_SCOPE_AGENT);
     }
     c.mark(LOOP_TR_START);
-    const int64_t pos = p.positions[0];
-    const bool pos_ok = pos >= 0 && pos < p.max_pos;
-    if (!pos_ok && c.b == 0 && c.tid == 0)
-      __hip_atomic_fetch_or(&p.ctrl[LOOP_CTRL_ERROR], (uint32_t)LOOP_ERR_POSITION, __ATOMIC_RELAXED,
-                            __HIP_MEMORY_SCOPE_AGENT);
+    if (p.trace && c.tid == 0)
+      p.trace[((int64_t)c.b * p.trace_slots + 1 + p.L * LOOP_TR_PER_LAYER + 3) * LWAVES + 1] = clock64();
 
     for (int layer = 0; layer < p.L; ++layer) {
       const LoopLayerW& lw = p.layers[layer];
@@ -743,89 +1071,85 @@ struct Loop {
       uint64_t* ll_act = ll + p.off_act;
       uint64_t* ll_down = ll + p.off_down;
 
-      // ======== A: x += down (previous layer), RMSNorm, QKV + RoPE ========
+      // ======== A: x += down (previous layer), RMSNorm, QKV + bias + RoPE ========
       if (w0) {
         lds_fetch(c, lw.ln1, H * (int)sizeof(T), nws);
+        if (b_work) tile_first(layer);  // this layer's first K / V tile, ahead of phase B
         if (layer > 0)
           ll_gather(c, p.ll + (int64_t)(layer - 1) * p.ll_layer_words + p.off_down, H / EPW, stage);
         else
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the norm weight
+          wait_vm0();
+        c.mark(tr + LOOP_TR_A_ISSUED);  // wave 0: the hand-off arrived
       }
       bar();
-      if (layer > 0) {
-        for (int i = c.tid; i < H; i += LT)
-          xs[i] = round_to<T>(add_rn(xs[i], word_elem<T>(payload(stage[i / EPW]), i % EPW)));
-        bar();
-      }
+      if (layer > 0)
+        x_add_norm<0>(c, xs, stage, nws, xin, red);
+      else
+        x_add_norm<2>(c, xs, stage, nws, xin, red);
       c.mark(tr + LOOP_TR_A_IN);
-      // wave 0: this phase's epilogue inputs (bias, RoPE rows), ahead of use
-      float eb[2] = {0.f, 0.f}, ecs[4] = {0.f, 0.f, 0.f, 0.f};
-      if (w0 && c.lane < npb) {
-        const int pr = c.b + c.nb * c.lane;
-        const int hd = pr / HALF, i = pr % HALF;
-        eb[0] = load_f32<T>((const T*)lw.bqkv, hd * D + i);
-        eb[1] = load_f32<T>((const T*)lw.bqkv, hd * D + i + HALF);
-        if (pos_ok && hd < Hq + Hkv) {
-          ecs[0] = p.cos_tab[pos * D + i];
-          ecs[1] = p.sin_tab[pos * D + i];
-          ecs[2] = p.cos_tab[pos * D + i + HALF];
-          ecs[3] = p.sin_tab[pos * D + i + HALF];
-        }
-      }
-      block_rmsnorm<T>(c, xs, nws, xin, red);
-      if (role == 1) {
-        rows_consume<T, JA, SA>(buf, a_q(c, lw, npb, rw, nr), a_rows(c, rw, nr), xin4, c.lane, [&](int s, float v) {
-          if (c.lane == 0) rowres[2 * (rw + nr * (s >> 1)) + (s & 1)] = v;
+      if (!w0) {
+        rows_consume<T, JA, SA>(bufA, a_q(c, lw, a_my_n, true), ra, xin4, c.lane, [&](int s, float v) {
+          if (c.lane == 0) rw_res[s] = v;
         });
-      }
-      bar();
-      if (w0 && c.lane < npb) {  // npb <= 64
-        const int t = c.lane;
-        const int pr = c.b + c.nb * t;
-        const int hd = pr / HALF, i = pr % HALF;
-        // F.linear output with bias, rounded to the dtype (fused.py:58)
-        const float va = round_to<T>(add_rn(rowres[2 * t], eb[0]));
-        const float vb = round_to<T>(add_rn(rowres[2 * t + 1], eb[1]));
-        float o[2] = {va, vb};
-        if (hd < Hq + Hkv) {
-          // rotate: x * cos + rotate_half(x) * sin, fp32, each op rounded,
-          // then cast (rope.py:57-62)
-          if (pos_ok) {
-            o[0] = round_to<T>(add_rn(mul_rn(va, ecs[0]), -mul_rn(vb, ecs[1])));
-            o[1] = round_to<T>(add_rn(mul_rn(vb, ecs[2]), mul_rn(va, ecs[3])));
+        const float bias_now = biasv;
+        wave_lds_fence();
+        // lane t: the wave's t-th pair
+        const float b0 = __shfl(bias_now, 2 * a_lane_t), b1 = __shfl(bias_now, 2 * a_lane_t + 1);
+        const float cs0 = __shfl(cosv, 2 * a_lane_t), cs1 = __shfl(cosv, 2 * a_lane_t + 1);
+        const float sn0 = __shfl(sinv, 2 * a_lane_t), sn1 = __shfl(sinv, 2 * a_lane_t + 1);
+        if (c.lane < a_my_n) {
+          const int t = c.lane;
+          int hd, i;
+          a_pair(c, rw, nrw, t, hd, i);
+          // F.linear output with bias, rounded to the dtype (fused.py:58)
+          const float va = round_to<T>(add_rn(rw_res[2 * t], b0));
+          const float vb = round_to<T>(add_rn(rw_res[2 * t + 1], b1));
+          float o[2] = {va, vb};
+          if (hd < Hq + Hkv) {
+            // rotate: x * cos + rotate_half(x) * sin, fp32, each op rounded,
+            // then cast (rope.py:57-62)
+            if (pos_ok) {
+              o[0] = round_to<T>(add_rn(mul_rn(va, cs0), -mul_rn(vb, sn0)));
+              o[1] = round_to<T>(add_rn(mul_rn(vb, cs1), mul_rn(va, sn1)));
+            } else {
+              o[0] = o[1] = __builtin_nanf("");
+            }
+          }
+          uint64_t* wq = ll_qkv + qkv_word(c, hd, i);
+          if constexpr (EPW == 2) {
+            ll_store(wq, c.epoch, pack_word<T>(o));
           } else {
-            o[0] = o[1] = __builtin_nanf("");
+            ll_store(wq, c.epoch, pack_word<T>(&o[0]));
+            ll_store(wq + 1, c.epoch, pack_word<T>(&o[1]));
+          }
+          if (hd >= Hq) {  // KV cache row at cache_len (kv_cache.py:53-54)
+            const bool is_k = hd < Hq + Hkv;
+            const int gg = is_k ? hd - Hq : hd - Hq - Hkv;
+            T* cache = (T*)(is_k ? p.k_cache : p.v_cache) +
+                       ((int64_t)layer * Hkv * p.S + (int64_t)gg * p.S + p.cache_len) * D;
+            store_f32<T>(cache, i, o[0]);
+            store_f32<T>(cache, i + HALF, o[1]);
           }
         }
-        uint64_t* wq = ll_qkv + qkv_word(c, hd, i);
-        if constexpr (EPW == 2) {
-          ll_store(wq, c.epoch, pack_word<T>(o));
-        } else {
-          ll_store(wq, c.epoch, pack_word<T>(&o[0]));
-          ll_store(wq + 1, c.epoch, pack_word<T>(&o[1]));
-        }
-        if (hd >= Hq) {  // KV cache row at cache_len (kv_cache.py:53-54)
-          const bool is_k = hd < Hq + Hkv;
-          const int gg = is_k ? hd - Hq : hd - Hq - Hkv;
-          T* cache = (T*)(is_k ? p.k_cache : p.v_cache) +
-                     ((int64_t)layer * Hkv * p.S + (int64_t)gg * p.S + p.cache_len) * D;
-          store_f32<T>(cache, i, o[0]);
-          store_f32<T>(cache, i + HALF, o[1]);
-        }
+        c.mark(tr + LOOP_TR_A_ISSUED);  // weight waves: results stored
+        // the next loads go out once this phase's results are on their way
+        rows_issue<JA, SA>(bufA, a_q(c, nw, a_my_n, more), ra, 0, 0, c.lane);
+        issue_bias(nw, more);
+        ISSUE_C(2, lw, true);
+        ISSUE_D(1, lw, true);
       }
       c.mark(tr + LOOP_TR_A_OUT);
-      if (role == 1 && more) issue_a(nw);  // overlaps the hand-off to phase B
-      c.mark(tr + LOOP_TR_A_ISSUED);
 
       // ======== B: attention of group bg + its o_proj share for rows [br0, br1) ========
       if (b_work) {
         if (w0) {
           const int gw = (G + 2) * HALF * WPP;  // the group's q heads, k head, v head
           ll_gather(c, ll_qkv + (int64_t)bg * gw, gw, qstage);
-        } else if (role == 2) {
-          asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // the K / V tile
+          c.mark(tr + LOOP_TR_B_ISSUED);  // wave 0: the hand-off arrived
         }
         bar();
+      }
+      if (b_work) {
         for (int t = c.tid; t < (G + 2) * HALF; t += LT) {
           const int hh = t / HALF, i = t % HALF;
           float va, vb;
@@ -848,106 +1172,107 @@ struct Loop {
         }
         bar();
         c.mark(tr + LOOP_TR_B_IN);
-        attention(c, layer, bg, at, xin, role == 2, tr);
+      }
+      if (b_work) {
+        if constexpr (EPW == 2)
+          attention_mfma(c, layer, bg, at, xin, tr);
+        else
+          attention(c, layer, bg, at, xin, tr);
         c.mark(tr + LOOP_TR_B_ATTN);
-        if (role == 2)
-          rows_consume<T, JB, SB>(buf, b_q(c, lw, bg, bn, rw, nr), b_rows(c, br0, rw, nr), xin4, c.lane,
-                                  [&](int s, float v) {
-                                    if (c.lane == 0) rowres[rw + nr * s] = v;
-                                  });
-        bar();
-        if (w0)
-          for (int t = c.lane; t < bn; t += 64)
-            ll_store(ll_p + (int64_t)bg * H + br0 + t, c.epoch, __float_as_uint(rowres[t]));
-        c.mark(tr + LOOP_TR_B_OUT);
       }
-      if (role == 2 && more) {  // overlaps the hand-off to phase C
-        tile_next(layer + 1);
-        issue_b(nw);
+      if (!w0) {
+        rows_consume<T, JB, SB>(bufB, b_q(c, lw, bg, bn, rw, nrw, true), rb, xin4, c.lane, [&](int s, float v) {
+          if (c.lane == 0) ll_store(ll_p + (int64_t)bg * H + br0 + rw + nrw * s, c.epoch, __float_as_uint(v));
+        });
+        c.mark(tr + LOOP_TR_B_ISSUED);  // weight waves: results stored
+        rows_issue<JB, SB>(bufB, b_q(c, nw, bg, bn, rw, nrw, more), rb, 0, 0, c.lane);
+        ISSUE_D(2, lw, true);
       }
-      c.mark(tr + LOOP_TR_B_ISSUED);
+      c.mark(tr + LOOP_TR_B_OUT);
 
       // ======== C: x += dtype(o_proj), RMSNorm, gate/up, SwiGLU ========
       if (w0) {
         lds_fetch(c, lw.ln2, H * (int)sizeof(T), nws);
         ll_gather(c, ll_p, Hkv * H, stage);
+        c.mark(tr + LOOP_TR_C_ISSUED);  // wave 0: the hand-off arrived
       }
       bar();
+      x_add_norm<1>(c, xs, stage, nws, xin, red);
       c.mark(tr + LOOP_TR_C_IN);
-      for (int i = c.tid; i < H; i += LT) {
-        float o = 0.f;
-        for (int g = 0; g < Hkv; ++g) o += __uint_as_float(payload(stage[g * H + i]));
-        xs[i] = round_to<T>(add_rn(xs[i], round_to<T>(o)));
+      if (!w0) {
+        rows_consume<T, JC, SC>(bufC, c_q(c, lw, c_my, true), rc, xin4, c.lane, [&](int s, float v) {
+          if (c.lane == 0) rw_res[s] = v;
+        });
+        wave_lds_fence();
+        if (c.lane < c_my) {  // lane t: the wave's t-th unit
+          const int t = c.lane;
+          float a[EPW];
+#pragma unroll
+          for (int e = 0; e < EPW; ++e)
+            a[e] = swiglu<T>(round_to<T>(rw_res[2 * EPW * t + 2 * e]),
+                             round_to<T>(rw_res[2 * EPW * t + 2 * e + 1]));  // mlp.py:38
+          ll_store(ll_act + cu0 + rw + nrw * t, c.epoch, pack_word<T>(a));
+        }
+        c.mark(tr + LOOP_TR_C_ISSUED);  // weight waves: results stored
+        ISSUE_C(0, nw, more);
+      }
+      c.mark(tr + LOOP_TR_C_OUT);
+
+      // ======== D: down projection ========
+      if (w0) {
+        ll_gather(c, ll_act, p.I / EPW, stage);
+        c.mark(tr + LOOP_TR_D_ISSUED);  // wave 0: the hand-off arrived
       }
       bar();
-      block_rmsnorm<T>(c, xs, nws, xin, red);
-      if (role == 3) {
-        rows_consume<T, JC, SC>(buf, c_q(c, lw, c_rows_n, rw, nr), c_rows(c, cu0, rw, nr), xin4, c.lane,
-                                [&](int s, float v) {
-                                  if (c.lane == 0) rowres[rw + nr * s] = v;
-                                });
+      {
+        // payloads of word pairs -> xin (I / EPW is even: I and H are even)
+        const uint4* st4 = (const uint4*)stage;
+        uint2* x2 = (uint2*)xin;
+        for (int i = c.tid; i < p.I / EPW / 2; i += LT) {
+          const uint4 v = st4[i];
+          x2[i] = make_uint2(v.x, v.z);
+        }
+      }
+      bar();
+      c.mark(tr + LOOP_TR_D_IN);
+      if (!w0) {
+        rows_consume<T, JD, SD>(bufD, d_q(c, lw, d_rows_n, rw, nrw, true), rd, xin4, c.lane, [&](int s, float v) {
+          if (c.lane == 0) rowres[rw + nrw * s] = v;
+        });
+        c.mark(tr + LOOP_TR_D_ISSUED);  // weight waves: results in LDS
+        ISSUE_C(1, nw, more);
+        ISSUE_D(0, nw, more);
       }
       bar();
       if (w0) {
-        for (int t = c.lane; t < cu1 - cu0; t += 64) {
-          float a[EPW];
+        for (int t = c.lane; t < du1 - du0; t += 64) {
+          float o[EPW];
 #pragma unroll
-          for (int e = 0; e < EPW; ++e) {
-            const int br = 2 * (t * EPW + e);
-            a[e] = swiglu<T>(round_to<T>(rowres[br]), round_to<T>(rowres[br + 1]));  // mlp.py:38
-          }
-          ll_store(ll_act + cu0 + t, c.epoch, pack_word<T>(a));
+          for (int e = 0; e < EPW; ++e) o[e] = round_to<T>(rowres[t * EPW + e]);
+          ll_store(ll_down + du0 + t, c.epoch, pack_word<T>(o));
         }
       }
-      c.mark(tr + LOOP_TR_C_OUT);
-      if (role == 3 && more) issue_c(nw);  // overlaps the hand-off to phase D
-      c.mark(tr + LOOP_TR_C_ISSUED);
-
-      // ======== D: down projection ========
-      if (d_rows_n > 0) {
-        if (w0) ll_gather(c, ll_act, p.I / EPW, stage);
-        bar();
-        for (int i = c.tid; i < p.I / EPW; i += LT) ((uint32_t*)xin)[i] = payload(stage[i]);
-        bar();
-        c.mark(tr + LOOP_TR_D_IN);
-        if (role == 4)
-          rows_consume<T, JD, SD>(buf, d_q(c, lw, d_rows_n, rw, nr), d_rows(c, du0, rw, nr), xin4, c.lane,
-                                  [&](int s, float v) {
-                                    if (c.lane == 0) rowres[rw + nr * s] = v;
-                                  });
-        bar();
-        if (w0) {
-          for (int t = c.lane; t < du1 - du0; t += 64) {
-            float o[EPW];
-#pragma unroll
-            for (int e = 0; e < EPW; ++e) o[e] = round_to<T>(rowres[t * EPW + e]);
-            ll_store(ll_down + du0 + t, c.epoch, pack_word<T>(o));
-          }
-        }
-        c.mark(tr + LOOP_TR_D_OUT);
-      }
-      if (role == 4 && more) issue_d(nw);
-      c.mark(tr + LOOP_TR_D_ISSUED);
+      c.mark(tr + LOOP_TR_D_OUT);
     }
+
+#undef ISSUE_C
+#undef ISSUE_D
 
     // ======== final norm, LM head, greedy pick ========
     {
       const int tr = 1 + p.L * LOOP_TR_PER_LAYER;
-      // the LM head streams through every weight wave
-      if (!w0) rows_issue<JL, SL>(buf, lm_q(c, lr1 - lr0), lm_rows(c, lr0), 0, 0, c.lane);
+      uint4 bufL[JL * SL];
+      if (!w0) rows_issue<JL, SL>(bufL, lm_q(c, lr1 - lr0), lm_rows(c, lr0), 0, 0, c.lane);
       if (w0) {
         lds_fetch(c, p.final_norm, H * (int)sizeof(T), nws);
         ll_gather(c, p.ll + (int64_t)(p.L - 1) * p.ll_layer_words + p.off_down, H / EPW, stage);
       }
       bar();
       c.mark(tr);
-      for (int i = c.tid; i < H; i += LT)
-        xs[i] = round_to<T>(add_rn(xs[i], word_elem<T>(payload(stage[i / EPW]), i % EPW)));
-      bar();
-      block_rmsnorm<T>(c, xs, nws, xin, red);
+      x_add_norm<0>(c, xs, stage, nws, xin, red);
       if (!w0) {
         const int cw = c.cw;
-        rows_consume<T, JL, SL>(buf, lm_q(c, lr1 - lr0), lm_rows(c, lr0), xin4, c.lane, [&](int s, float v) {
+        rows_consume<T, JL, SL>(bufL, lm_q(c, lr1 - lr0), lm_rows(c, lr0), xin4, c.lane, [&](int s, float v) {
           if (c.lane == 0) rowres[cw + NCW * s] = v;
         });
       }
@@ -970,21 +1295,25 @@ struct Loop {
         ll_store(part + 2 * c.b, c.epoch, __float_as_uint(amv[0]));
         ll_store(part + 2 * c.b + 1, c.epoch, (uint32_t)ami[0]);
       }
-      if (c.b == 0) {
-        if (w0) ll_gather(c, part, 2 * c.nb, stage);
-        bar();
+      if (c.b == 0 && w0) {
+        ll_gather(c, part, 2 * c.nb, stage);
         float v = -__builtin_inff();
         int64_t i = INT64_MAX;
-        if (c.tid < c.nb) {
-          v = __uint_as_float(payload(stage[2 * c.tid]));
-          i = (int64_t)payload(stage[2 * c.tid + 1]);
+        for (int k = c.lane; k < c.nb; k += 64) {
+          const float vk = __uint_as_float(payload(stage[2 * k]));
+          const int64_t ik = (int64_t)payload(stage[2 * k + 1]);
+          if (argmax_better(vk, ik, v, i)) {
+            v = vk;
+            i = ik;
+          }
         }
-        block_argmax(c, v, i, amv, ami);
-        if (c.tid == 0) {
-          if (p.next_tok) p.next_tok[0] = ami[0];
+        wave_argmax(v, i);
+        if (c.lane == 0) {
+          if (p.next_tok) p.next_tok[0] = i;
           p.ctrl[LOOP_CTRL_EPOCH] = c.epoch;
         }
         c.mark(tr + 2);
+        if (p.trace && c.lane == 0) p.trace[((int64_t)c.b * p.trace_slots + tr + 3) * LWAVES + 2] = clock64();
       }
     }
   }
@@ -1097,7 +1426,7 @@ const char* loop_unsupported(const minitp_qwen2_config& c, int nb, LoopLds* out)
   L.xin = take(align_up(xin_elems * es, 16) + 16);
   // attention: K and V tiles (own region), q rows, current k and v, tile scores (in stage)
   L.tile = take(2 * tp * D * es);
-  const int attn_bytes = GMAXL * D * es + 2 * D * 4 + GMAXL * tp * 4;
+  const int attn_bytes = GMAXL * D * es + 2 * D * 4 + GMAXL * tp * 4 + 4 * GMAXL * 4;
   // gathered hand-off words (8 bytes each, whole 128-word copies)
   const int epw_ = es == 4 ? 1 : 2;
   const int gmax = std::max(std::max(c.kv_heads * c.hidden, c.hidden / epw_), std::max(c.intermediate / epw_, 2 * nb));
@@ -1105,19 +1434,21 @@ const char* loop_unsupported(const minitp_qwen2_config& c, int nb, LoopLds* out)
   const int stage_words = align_up(gmax, 128);
   L.stage = take(std::max(attn_bytes, stage_words * 8));
   L.qstage = take(align_up((G + 2) * (D / 2) * (2 / epw_), 128) * 8);
-  // row results: phase A 2 * pairs, B rows, C rows, D NCW * rows, LM rows
+  // row results: per weight wave (phases A and C), the block's down rows,
+  // the block's LM-head rows
   const int npa = (c.heads + 2 * c.kv_heads) * (D / 2);
-  const int rs = nb / c.kv_heads;
-  const int rows_a = 2 * ((npa + nb - 1) / nb);
-  const int rows_b = (c.hidden + rs - 1) / rs;
   const int epw = es == 4 ? 1 : 2;
-  const int rows_c = 2 * epw * ((c.intermediate / epw + nb - 1) / nb);
-  const int rows_d = NCW * epw * ((c.hidden / epw + nb - 1) / nb);
+  const int rows_d = epw * ((c.hidden / epw + nb - 1) / nb);
   const int rows_lm = (c.vocab + nb - 1) / nb;
-  L.rowres = take(std::max(std::max(std::max(rows_a, rows_b), std::max(rows_c, rows_d)), rows_lm) * 4 + 16);
+  L.rowres = take(std::max(std::max(NCW * LOOP_ROWS_PER_WAVE, rows_d), rows_lm) * 4 + 16);
   L.norm = take(align_up(c.hidden * es, 1024));
   L.misc = take(64 * 4 + LWAVES * 8);
   if ((npa + nb - 1) / nb > 64) return "more than 64 QKV pairs per block";
+  if (c.hidden > 4 * LOOP_THREADS) return "hidden size above 2048";
+  {
+    const int upb = (c.intermediate / epw + nb - 1) / nb;  // gate/up units per block
+    if (2 * epw * ((upb + NCW - 1) / NCW) > LOOP_ROWS_PER_WAVE) return "too many gate/up rows per wave";
+  }
   L.bytes = off;
   if (L.bytes > 160 * 1024) return "LDS layout exceeds 160 KiB";
   if (out) *out = L;
