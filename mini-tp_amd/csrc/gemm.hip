@@ -1,15 +1,23 @@
 // Prefill / batched linear layers: y[M, N] = epilogue(x[M, K] W[N, K]^T (+ bias)).
 //
-// MFMA tiling for CDNA (wave64): a 256-thread block owns a 128 x 128 output
-// tile; its 4 waves form a 2 x 2 grid of 64 x 64 wave tiles, each a 2 x 2 set
-// of 32 x 32 MFMA accumulators (16 fp32 registers per lane each). K advances
-// in 64-byte slabs (32 bf16 or 16 fp32) staged in LDS; both operands are
-// K-contiguous in memory (x rows and W rows), which is the layout the MFMA
-// A/B fragments want, so no transpose is needed anywhere.
+// MFMA tiling for CDNA (wave64): a 256-thread block owns a BM x BN output
+// tile (128 x 128 for large M, 64 x 64 when M is small); its 4 waves form a
+// 2 x 2 grid of wave tiles made of 32 x 32 MFMA accumulators (16 fp32
+// registers per lane each). Both operands are K-contiguous in memory (x rows
+// and W rows), the layout the MFMA A/B fragments want, so nothing is
+// transposed. K advances in chunks of 256 bytes per row staged in LDS; the
+// next chunk's global loads are issued before the current chunk's MFMAs, so
+// HBM latency overlaps the math. Rows are padded by 16 bytes in LDS to spread
+// the MFMA fragment reads over the banks.
 //   bf16: v_mfma_f32_32x32x8bf16_1k (A/B: 4 bf16 per lane, k = 4*(lane/32)+i)
 //   fp32: v_mfma_f32_32x32x2f32     (A/B: 1 float per lane, k = lane/32)
 // Accumulator layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4,
 // column l%32.
+//
+// Small M (prefill of one short prompt, batched decode) leaves few output
+// tiles, so K is split over blockIdx.z: each split writes fp32 partial sums
+// to a workspace and gemm_reduce_kernel adds them in split order (a fixed
+// order, so results do not depend on timing) and applies the epilogue.
 #include "common.h"
 #include "kernels.h"
 
@@ -17,10 +25,13 @@ namespace minitp {
 
 namespace {
 
-constexpr int BM = 128, BN = 128;
-constexpr int SLAB = 64;  // bytes of K per LDS stage per row
-constexpr int PADB = 16;  // row padding (bytes) against LDS bank conflicts
-constexpr int ROWB = SLAB + PADB;
+constexpr int OUT_PARTIAL = 100;  // epilogue: fp32 split-K partials
+// bytes of K per row per LDS chunk: 256 for 64 x 64 tiles, 128 for 128 x 128
+// (both operand tiles of a chunk stay under 40 KiB of LDS)
+template <int BM>
+constexpr int chunk_bytes() {
+  return BM >= 128 ? 128 : 256;
+}
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef short s16x4 __attribute__((ext_vector_type(4)));
@@ -50,48 +61,79 @@ struct Mfma<float> {
   }
 };
 
-template <typename T, int EPI>
+// Block (bx, by, z): output tile (by * BM, bx * BN), K range [z kper, (z + 1)
+// kper). kper is a multiple of the chunk (KCB bytes).
+template <typename T, int BM, int BN, int OUT>
 __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ x, int64_t ldx, const T* __restrict__ w,
                                                    const T* __restrict__ bias, T* y, int64_t ldy, const T* aux,
-                                                   int64_t M, int64_t N, int64_t K, const StepState* state) {
+                                                   float* part, int64_t M, int64_t N, int64_t K, int64_t kper,
+                                                   const StepState* state) {
   if (state != nullptr) y = (T*)state->args.logits;
+  constexpr int KCB = chunk_bytes<BM>(), ROWB = KCB + 16;
+  constexpr int V = Vec<T>::N;          // elements per 16 B
+  constexpr int KCE = KCB / sizeof(T);  // elements of K per chunk
+  constexpr int CPR = KCB / 16;         // 16-byte pieces per row per chunk
+  constexpr int LA = BM * CPR / 256, LB = BN * CPR / 256;  // pieces per thread
+  constexpr int FM = BM / 64, FN = BN / 64;                // 32 x 32 fragments per wave
   __shared__ __attribute__((aligned(16))) char As[BM * ROWB];
   __shared__ __attribute__((aligned(16))) char Bs[BN * ROWB];
-  constexpr int V = Vec<T>::N;              // elements per 16 B
-  constexpr int SLAB_K = SLAB / sizeof(T);  // elements of K per stage
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave >> 1, wn = wave & 1;
   const int64_t m0 = (int64_t)blockIdx.y * BM, n0 = (int64_t)blockIdx.x * BN;
+  const int64_t kb = (int64_t)blockIdx.z * kper;
+  const int64_t ke = kb + kper < K ? kb + kper : K;
 
-  f32x16 acc[2][2];
+  f32x16 acc[FM][FN];
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < FN; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  for (int64_t k0 = 0; k0 < K; k0 += SLAB_K) {
-    // stage: 128 rows x 4 chunks of 16 B for each operand = 2 chunks / thread
+  uint4 ra[LA], rb[LB];
+  auto load = [&](int64_t k0) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-      const int c = tid + h * 256, row = c >> 2, kc = c & 3;
-      const int64_t k = k0 + kc * V;
-      uint4 va = make_uint4(0, 0, 0, 0), vb = make_uint4(0, 0, 0, 0);
-      if (m0 + row < M && k < K) va = *reinterpret_cast<const uint4*>(x + (m0 + row) * ldx + k);
-      if (n0 + row < N && k < K) vb = load_stream16(reinterpret_cast<const uint4*>(w + (n0 + row) * K + k));
-      *reinterpret_cast<uint4*>(As + row * ROWB + kc * 16) = va;
-      *reinterpret_cast<uint4*>(Bs + row * ROWB + kc * 16) = vb;
+    for (int i = 0; i < LA; ++i) {
+      const int c = tid + i * 256, row = c / CPR, pc = c % CPR;
+      const int64_t k = k0 + pc * V;
+      ra[i] = (m0 + row < M && k < ke) ? *reinterpret_cast<const uint4*>(x + (m0 + row) * ldx + k)
+                                       : make_uint4(0, 0, 0, 0);
     }
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+      const int c = tid + i * 256, row = c / CPR, pc = c % CPR;
+      const int64_t k = k0 + pc * V;
+      rb[i] = (n0 + row < N && k < ke) ? load_stream16(reinterpret_cast<const uint4*>(w + (n0 + row) * K + k))
+                                       : make_uint4(0, 0, 0, 0);
+    }
+  };
+  auto stash = [&]() {
+#pragma unroll
+    for (int i = 0; i < LA; ++i) {
+      const int c = tid + i * 256, row = c / CPR, pc = c % CPR;
+      *reinterpret_cast<uint4*>(As + row * ROWB + pc * 16) = ra[i];
+    }
+#pragma unroll
+    for (int i = 0; i < LB; ++i) {
+      const int c = tid + i * 256, row = c / CPR, pc = c % CPR;
+      *reinterpret_cast<uint4*>(Bs + row * ROWB + pc * 16) = rb[i];
+    }
+  };
+
+  if (kb < ke) load(kb);
+  for (int64_t k0 = kb; k0 < ke; k0 += KCE) {
+    stash();
     __syncthreads();
+    if (k0 + KCE < ke) load(k0 + KCE);  // in flight during this chunk's MFMAs
 #pragma unroll
-    for (int ks = 0; ks < SLAB_K / Mfma<T>::KSTEP; ++ks) {
+    for (int ks = 0; ks < KCE / Mfma<T>::KSTEP; ++ks) {
 #pragma unroll
-      for (int i = 0; i < 2; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) {
-          const char* a_row = As + (wm * 64 + i * 32 + (lane & 31)) * ROWB;
-          const char* b_row = Bs + (wn * 64 + j * 32 + (lane & 31)) * ROWB;
+        for (int j = 0; j < FN; ++j) {
+          const char* a_row = As + (wm * (BM / 2) + i * 32 + (lane & 31)) * ROWB;
+          const char* b_row = Bs + (wn * (BN / 2) + j * 32 + (lane & 31)) * ROWB;
           acc[i][j] = Mfma<T>::step(a_row, b_row, ks, lane, acc[i][j]);
         }
     }
@@ -99,18 +141,20 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ x, int6
   }
 
 #pragma unroll
-  for (int i = 0; i < 2; ++i)
+  for (int i = 0; i < FM; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int64_t col = n0 + wn * 64 + j * 32 + (lane & 31);
+    for (int j = 0; j < FN; ++j) {
+      const int64_t col = n0 + wn * (BN / 2) + j * 32 + (lane & 31);
       if (col >= N) continue;
-      const float bcol = (EPI == MINITP_EPI_NONE && bias != nullptr) ? load_f32<T>(bias, col) : 0.f;
+      const float bcol = (OUT == MINITP_EPI_NONE && bias != nullptr) ? load_f32<T>(bias, col) : 0.f;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int64_t row = m0 + wm * 64 + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+        const int64_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
         if (row >= M) continue;
         const float v = acc[i][j][r];
-        if constexpr (EPI == MINITP_EPI_RESID)
+        if constexpr (OUT == OUT_PARTIAL)
+          part[((int64_t)blockIdx.z * M + row) * N + col] = v;
+        else if constexpr (OUT == MINITP_EPI_RESID)
           store_f32<T>(y, row * ldy + col, add_rn(load_f32<T>(aux, row * ldy + col), round_to<T>(v)));
         else
           store_f32<T>(y, row * ldy + col, v + bcol);
@@ -118,31 +162,86 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ x, int6
     }
 }
 
-template <typename T>
-int gemm_typed(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy,
-               int64_t M, int64_t N, int64_t K, int epi, const void* aux, const StepState* state) {
-  dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM));
-  if (epi == MINITP_EPI_RESID)
-    hipLaunchKernelGGL((gemm_kernel<T, MINITP_EPI_RESID>), grid, dim3(256), 0, st, (const T*)x, ldx, (const T*)w,
-                       (const T*)bias, (T*)y, ldy, (const T*)aux, M, N, K, state);
-  else
-    hipLaunchKernelGGL((gemm_kernel<T, MINITP_EPI_NONE>), grid, dim3(256), 0, st, (const T*)x, ldx, (const T*)w,
-                       (const T*)bias, (T*)y, ldy, (const T*)aux, M, N, K, state);
+// y = epilogue(sum over the S splits of part[s][M][N]), splits added in order.
+template <typename T, int EPI>
+__global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restrict__ part, int S, const T* bias, T* y,
+                                                          int64_t ldy, const T* aux, int64_t M, int64_t N,
+                                                          const StepState* state) {
+  if (state != nullptr) y = (T*)state->args.logits;
+  const int64_t MN = M * N;
+  for (int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; e < MN; e += (int64_t)gridDim.x * blockDim.x) {
+    float v = part[e];
+    for (int s = 1; s < S; ++s) v += part[s * MN + e];
+    const int64_t row = e / N, col = e % N;
+    if constexpr (EPI == MINITP_EPI_RESID)
+      store_f32<T>(y, row * ldy + col, add_rn(load_f32<T>(aux, row * ldy + col), round_to<T>(v)));
+    else
+      store_f32<T>(y, row * ldy + col, v + (bias != nullptr ? load_f32<T>(bias, col) : 0.f));
+  }
+}
+
+template <typename T, int BM, int BN>
+int gemm_launch(hipStream_t st, const T* x, int64_t ldx, const T* w, const T* bias, T* y, int64_t ldy, int64_t M,
+                int64_t N, int64_t K, int epi, const T* aux, const StepState* state, float* ws, int64_t ws_bytes) {
+  constexpr int64_t KCE = chunk_bytes<BM>() / sizeof(T);
+  const int64_t tiles = cdiv(N, BN) * cdiv(M, BM);
+  const int64_t nchunk = cdiv(K, KCE);
+  // splits: enough blocks to fill the CUs twice, each at least one chunk deep,
+  // and partials that fit the workspace
+  int64_t S = 1;
+  if (ws != nullptr) {
+    S = std::min<int64_t>(cdiv(512, tiles), nchunk);
+    while (S > 1 && S * M * N * (int64_t)sizeof(float) > ws_bytes) --S;
+  }
+  const int64_t kper = cdiv(nchunk, S) * KCE;
+  S = cdiv(K, kper);
+  const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM), (unsigned)S);
+  if (S > 1) {
+    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, OUT_PARTIAL>), grid, dim3(256), 0, st, x, ldx, w, bias, y, ldy, aux,
+                       ws, M, N, K, kper, state);
+    MINITP_LAUNCH_CHECK();
+    const int rgrid = (int)std::min<int64_t>(cdiv(M * N, 256), 2048);
+    if (epi == MINITP_EPI_RESID)
+      hipLaunchKernelGGL((gemm_reduce_kernel<T, MINITP_EPI_RESID>), dim3(rgrid), dim3(256), 0, st, ws, (int)S, bias,
+                         y, ldy, aux, M, N, state);
+    else
+      hipLaunchKernelGGL((gemm_reduce_kernel<T, MINITP_EPI_NONE>), dim3(rgrid), dim3(256), 0, st, ws, (int)S, bias, y,
+                         ldy, aux, M, N, state);
+  } else if (epi == MINITP_EPI_RESID) {
+    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, MINITP_EPI_RESID>), grid, dim3(256), 0, st, x, ldx, w, bias, y, ldy,
+                       aux, ws, M, N, K, kper, state);
+  } else {
+    hipLaunchKernelGGL((gemm_kernel<T, BM, BN, MINITP_EPI_NONE>), grid, dim3(256), 0, st, x, ldx, w, bias, y, ldy,
+                       aux, ws, M, N, K, kper, state);
+  }
   MINITP_LAUNCH_CHECK();
   return MINITP_OK;
+}
+
+template <typename T>
+int gemm_typed(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy,
+               int64_t M, int64_t N, int64_t K, int epi, const void* aux, const StepState* state, void* ws,
+               int64_t ws_bytes) {
+  // large M: 128 x 128 tiles already fill the chip; small M: 64 x 64 tiles and split K
+  if (M >= 512)
+    return gemm_launch<T, 128, 128>(st, (const T*)x, ldx, (const T*)w, (const T*)bias, (T*)y, ldy, M, N, K, epi,
+                                    (const T*)aux, state, (float*)ws, ws_bytes);
+  return gemm_launch<T, 64, 64>(st, (const T*)x, ldx, (const T*)w, (const T*)bias, (T*)y, ldy, M, N, K, epi,
+                                (const T*)aux, state, (float*)ws, ws_bytes);
 }
 
 }  // namespace
 
 int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
-                int64_t ldy, int64_t M, int64_t N, int64_t K, int epi, const void* aux, const StepState* state) {
+                int64_t ldy, int64_t M, int64_t N, int64_t K, int epi, const void* aux, const StepState* state,
+                void* ws, int64_t ws_bytes) {
   if (M == 0 || N == 0) return MINITP_OK;
   if (epi != MINITP_EPI_NONE && epi != MINITP_EPI_RESID) {
     set_error("gemm: epilogue %d not supported (split SwiGLU runs as its own kernel)", epi);
     return MINITP_ERR_UNSUPPORTED;
   }
-  return dtype == MINITP_F32 ? gemm_typed<float>(st, x, ldx, w, bias, y, ldy, M, N, K, epi, aux, state)
-                             : gemm_typed<bf16>(st, x, ldx, w, bias, y, ldy, M, N, K, epi, aux, state);
+  return dtype == MINITP_F32 ? gemm_typed<float>(st, x, ldx, w, bias, y, ldy, M, N, K, epi, aux, state, ws, ws_bytes)
+                             : gemm_typed<bf16>(st, x, ldx, w, bias, y, ldy, M, N, K, epi, aux, state, ws, ws_bytes);
 }
 
 }  // namespace minitp

@@ -77,9 +77,12 @@ bool gemv_supported(int dtype, int64_t M, int64_t K);
 
 // gemm.hip: y[M, N] = epilogue(x[M, K] W[N, K]^T (+ bias)), MFMA tiles.
 // When `state` is non-null the output base is state->logits (graph replays).
+// With a workspace (ws, ws_bytes), small-M products split K over more
+// blocks and reduce the fp32 partials in a second kernel.
+constexpr int64_t GEMM_WS_BYTES = 8LL << 20;
 int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
                 int64_t ldy, int64_t M, int64_t N, int64_t K, int epi, const void* aux,
-                const StepState* state = nullptr);
+                const StepState* state = nullptr, void* ws = nullptr, int64_t ws_bytes = 0);
 
 // elementwise.hip
 int launch_fill_normal(hipStream_t st, int dtype, void* dst, int64_t count, uint64_t seed, uint64_t sid,

@@ -73,6 +73,7 @@ struct Ws {
   int64_t* part_idx;
   void* amax_ws;
   int64_t amax_ws_bytes;
+  void* gemm_ws;  // split-K partials of the prefill / batched GEMMs
   int64_t bytes;
 };
 
@@ -143,6 +144,7 @@ struct Qwen2Program {
     w.part_idx = (int64_t*)take(std::min<int64_t>(B, 4) * np * 8);
     w.amax_ws_bytes = argmax_workspace_bytes(B, c.vocab);
     w.amax_ws = take(w.amax_ws_bytes);
+    w.gemm_ws = take(GEMM_WS_BYTES);
     w.bytes = off;
     return w;
   }
@@ -205,7 +207,7 @@ struct Qwen2Program {
       } else {
         if ((rc = launch_rmsnorm(st, c.dtype, w.x, L(l, MINITP_W_LN1), w.h, M, H, c.eps))) return rc;
         if ((rc = launch_gemm(st, c.dtype, w.h, H, L(l, MINITP_W_QKV), L(l, MINITP_W_QKV_BIAS), w.qkv, qkv_rows(), M,
-                              qkv_rows(), H, MINITP_EPI_NONE, nullptr)))
+                              qkv_rows(), H, MINITP_EPI_NONE, nullptr, nullptr, w.gemm_ws, GEMM_WS_BYTES)))
           return rc;
         if ((rc = launch_rope_kv_write(st, c.dtype, w.qkv, qkv_rows(), w.q, nullptr, nullptr, cos_tab, sin_tab, nullptr,
                                        c.max_pos, B, T, c.heads, c.kv_heads, D, s.max_seq, 0, nullptr, w.st, l)))
@@ -234,7 +236,7 @@ struct Qwen2Program {
         if ((rc = launch_gemv(st, c.dtype, PRO_NONE, EPI_RESID, g))) return rc;
       } else {
         if ((rc = launch_gemm(st, c.dtype, w.attn, q_rows(), L(l, MINITP_W_O), nullptr, w.x, H, M, H, q_rows(),
-                              MINITP_EPI_RESID, w.x)))
+                              MINITP_EPI_RESID, w.x, nullptr, w.gemm_ws, GEMM_WS_BYTES)))
           return rc;
       }
       // ---- MLP block ----------------------------------------------------------
@@ -265,12 +267,12 @@ struct Qwen2Program {
       } else {
         if ((rc = launch_rmsnorm(st, c.dtype, w.x, L(l, MINITP_W_LN2), w.h, M, H, c.eps))) return rc;
         if ((rc = launch_gemm(st, c.dtype, w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.gu, 2 * I, M, 2 * I, H,
-                              MINITP_EPI_NONE, nullptr)))
+                              MINITP_EPI_NONE, nullptr, nullptr, w.gemm_ws, GEMM_WS_BYTES)))
           return rc;
         const char* up = (const char*)w.gu + I * es();
         if ((rc = launch_silu_mul(st, c.dtype, w.gu, up, 2 * I, w.act, I, M, I))) return rc;
         if ((rc = launch_gemm(st, c.dtype, w.act, I, L(l, MINITP_W_DOWN), nullptr, w.x, H, M, H, I, MINITP_EPI_RESID,
-                              w.x)))
+                              w.x, nullptr, w.gemm_ws, GEMM_WS_BYTES)))
           return rc;
       }
     }
