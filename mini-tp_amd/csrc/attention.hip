@@ -414,6 +414,152 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const T* q, const T* 
   }
 }
 
+
+// Prefill on matrix cores (bf16): block = (b * Hq + h, 64-query tile), wave
+// w = the 16-query strip t0 = 64 y + 16 w. Per 64-key tile staged in LDS (K
+// row-major, V transposed so that a P V operand is 4 consecutive keys):
+// S = Q K^T by MFMA 16x16x16 (A = the strip's q rows, B = 16 keys), causal
+// mask, online softmax in base 2 per query row (a row's 16 columns of a
+// key block sit in 16 lanes, reduced with xor shuffles), P rounded to bf16
+// through a per-wave LDS tile into A layout, then O += P V by MFMA (B = 16
+// dims x 4 keys per lane). The row sums stay per lane in fp32 and are added
+// across the 16 lanes at the end; O / l is rounded to bf16 once.
+template <int D>
+__global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, const bf16* kc, const bf16* vc,
+                                                                bf16* out, AttnShape s, int64_t cache_len,
+                                                                float scale) {
+  typedef short short4_t __attribute__((ext_vector_type(4)));
+  typedef float float4_t __attribute__((ext_vector_type(4)));
+  constexpr int KT = 64;            // keys per tile
+  constexpr int KB = KT / 16;       // 16-key blocks per tile
+  constexpr int KS = D / 16;        // 16-dim steps of a score, and 16-dim output blocks
+  constexpr int PPRW = D / 8;       // 16-byte pieces per K / V row
+  constexpr int KROW = D * 2 + 16;  // LDS bytes per K row (padded)
+  constexpr int VROW = KT * 2 + 16; // LDS bytes per transposed V row (one dim)
+  constexpr int PROW = KT * 2 + 16; // LDS bytes per P row
+  __shared__ __attribute__((aligned(16))) char Ks[KT * KROW];
+  __shared__ __attribute__((aligned(16))) char Vt[D * VROW];
+  __shared__ __attribute__((aligned(16))) char Ps[4][16 * PROW];
+  const int G = s.Hq / s.Hkv;
+  const int bh = blockIdx.x, b = bh / s.Hq, h = bh % s.Hq, g = h / G;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane % 16, lq = lane / 16;
+  const int64_t t0 = (int64_t)blockIdx.y * 64 + wave * 16;
+  const bf16* kbase = kc + ((int64_t)b * s.Hkv + g) * s.S * D;
+  const bf16* vbase = vc + ((int64_t)b * s.Hkv + g) * s.S * D;
+  const float sl2 = scale * 1.4426950408889634f;
+  char* pw = Ps[wave];
+
+  short4_t qa[KS];
+  {
+    const int64_t t = t0 + lr;
+#pragma unroll
+    for (int kb = 0; kb < KS; ++kb) {
+      const uint2 v = t < s.T ? *(const uint2*)(q + (((int64_t)b * s.T + t) * s.Hq + h) * D + kb * 16 + 4 * lq)
+                              : make_uint2(0, 0);
+      qa[kb] = __builtin_bit_cast(short4_t, v);
+    }
+  }
+  float4_t o[KS];
+#pragma unroll
+  for (int dn = 0; dn < KS; ++dn) o[dn] = float4_t{0.f, 0.f, 0.f, 0.f};
+  float m[4], lsum[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -__builtin_inff();
+    lsum[i] = 0.f;
+  }
+  const int64_t tb_last = std::min<int64_t>((int64_t)blockIdx.y * 64 + 63, s.T - 1);
+  const int64_t key_end = cache_len + tb_last + 1;  // keys the block's queries may see
+
+  for (int64_t k0 = 0; k0 < key_end; k0 += KT) {
+    __syncthreads();  // the previous tile is consumed
+    for (int c = tid; c < KT * PPRW; c += 256) {
+      const int j = c / PPRW, pc = c % PPRW;
+      const bool ok = k0 + j < key_end;
+      const uint4 kv = ok ? *(const uint4*)(kbase + (k0 + j) * D + pc * 8) : make_uint4(0, 0, 0, 0);
+      const uint4 vv = ok ? *(const uint4*)(vbase + (k0 + j) * D + pc * 8) : make_uint4(0, 0, 0, 0);
+      *(uint4*)(Ks + j * KROW + pc * 16) = kv;
+      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        *(uint16_t*)(Vt + (pc * 8 + e) * VROW + j * 2) = (uint16_t)(e & 1 ? vw[e >> 1] >> 16 : vw[e >> 1]);
+    }
+    __syncthreads();
+    if (t0 >= s.T || k0 > cache_len + t0 + 15) continue;  // this strip sees none of the tile
+    // ---- scores (row 4 lq + i of the strip, key k0 + 16 kbk + lr)
+    float sc[KB][4];
+#pragma unroll
+    for (int kbk = 0; kbk < KB; ++kbk) {
+      float4_t acc = {0.f, 0.f, 0.f, 0.f};
+      const char* krow = Ks + (kbk * 16 + lr) * KROW;
+#pragma unroll
+      for (int kb = 0; kb < KS; ++kb) {
+        const short4_t kv = *(const short4_t*)(krow + (kb * 16 + 4 * lq) * 2);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(qa[kb], kv, acc, 0, 0, 0);
+      }
+      const int64_t key = k0 + kbk * 16 + lr;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int64_t qpos = cache_len + t0 + 4 * lq + i;
+        sc[kbk][i] = key <= qpos ? acc[i] * sl2 : -__builtin_inff();
+      }
+    }
+    // ---- online softmax per row
+    float alpha[4], mn[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float mx = sc[0][i];
+#pragma unroll
+      for (int kbk = 1; kbk < KB; ++kbk) mx = fmaxf(mx, sc[kbk][i]);
+#pragma unroll
+      for (int msk = 1; msk < 16; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
+      mn[i] = fmaxf(m[i], mx);
+      alpha[i] = mn[i] == -__builtin_inff() ? 1.f : __builtin_amdgcn_exp2f(m[i] - mn[i]);
+      m[i] = mn[i];
+      lsum[i] *= alpha[i];
+    }
+#pragma unroll
+    for (int kbk = 0; kbk < KB; ++kbk)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float pr = sc[kbk][i] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(sc[kbk][i] - mn[i]);
+        lsum[i] += pr;
+        *(uint16_t*)(pw + (4 * lq + i) * PROW + (kbk * 16 + lr) * 2) = f32_to_bf16(pr);
+      }
+#pragma unroll
+    for (int dn = 0; dn < KS; ++dn)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) o[dn][i] *= alpha[i];
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    // ---- O += P V
+#pragma unroll
+    for (int kk = 0; kk < KB; ++kk) {
+      const short4_t pa = *(const short4_t*)(pw + lr * PROW + (kk * 16 + 4 * lq) * 2);
+#pragma unroll
+      for (int dn = 0; dn < KS; ++dn) {
+        const short4_t vb = *(const short4_t*)(Vt + (dn * 16 + lr) * VROW + (kk * 16 + 4 * lq) * 2);
+        o[dn] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[dn], 0, 0, 0);
+      }
+    }
+  }
+  if (t0 >= s.T) return;
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int msk = 1; msk < 16; msk <<= 1) lsum[i] += __shfl_xor(lsum[i], msk, 64);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int64_t t = t0 + 4 * lq + i;
+    if (t >= s.T) continue;
+#pragma unroll
+    for (int dn = 0; dn < KS; ++dn)
+      store_f32<bf16>(out, (((int64_t)b * s.T + t) * s.Hq + h) * D + dn * 16 + lr, o[dn][i] / lsum[i]);
+  }
+}
+
 template <typename T, int D, int HP>
 int decode_launch(hipStream_t st, DecodeArgs& a, int nsplit) {
   const int G = a.s.Hq / a.s.Hkv;
@@ -458,8 +604,12 @@ template <typename T, int D>
 int prefill_dispatch(hipStream_t st, const void* q, const void* k, const void* v, void* out, const AttnShape& s,
                      int64_t cache_len) {
   const float scale = 1.0f / sqrtf((float)D);
-  hipLaunchKernelGGL((prefill_attn_kernel<T, D>), dim3(s.B * s.Hq, (unsigned)cdiv(s.T, QT)), dim3(256), 0, st,
-                     (const T*)q, (const T*)k, (const T*)v, (T*)out, s, cache_len, scale);
+  if constexpr (sizeof(T) == 2)
+    hipLaunchKernelGGL((prefill_attn_mfma_kernel<D>), dim3(s.B * s.Hq, (unsigned)cdiv(s.T, 64)), dim3(256), 0, st,
+                       (const bf16*)q, (const bf16*)k, (const bf16*)v, (bf16*)out, s, cache_len, scale);
+  else
+    hipLaunchKernelGGL((prefill_attn_kernel<T, D>), dim3(s.B * s.Hq, (unsigned)cdiv(s.T, QT)), dim3(256), 0, st,
+                       (const T*)q, (const T*)k, (const T*)v, (T*)out, s, cache_len, scale);
   MINITP_LAUNCH_CHECK();
   return MINITP_OK;
 }

@@ -316,6 +316,24 @@ def test_prefill_attention_causal(t, cache_len, hq, hkv, d):
     assert (got.double() - ref).abs().max().item() < 2e-5
 
 
+@pytest.mark.parametrize("t,cache_len", [(2, 0), (16, 0), (65, 0), (128, 0), (6, 5), (70, 33), (300, 17)])
+@pytest.mark.parametrize("hq,hkv,d", [(14, 2, 64), (4, 2, 16), (28, 4, 128), (8, 8, 32)])
+def test_prefill_attention_causal_bf16(t, cache_len, hq, hkv, d):
+    """bf16 prefill runs on matrix cores with P rounded to bf16 as the MFMA
+    operand; against a float64 reference on the same bf16 inputs the output
+    (values of order 1) agrees to a few bf16 steps: atol 3e-2."""
+    b = 2
+    s = cache_len + t + 2
+    g = torch.Generator().manual_seed(t * 11 + cache_len + d)
+    q = torch.randn(b, t, hq, d, generator=g).bfloat16()
+    kc = torch.randn(b, hkv, s, d, generator=g).bfloat16()
+    vc = torch.randn(b, hkv, s, d, generator=g).bfloat16()
+    got = _k().attention(q.to(DEV), kc.to(DEV), vc.to(DEV), cache_len=cache_len).cpu()
+    assert got.dtype == torch.bfloat16
+    ref = _ref_attention(q.double(), kc.double(), vc.double(), cache_len)
+    assert (got.double() - ref).abs().max().item() < 3e-2
+
+
 # ---------------------------------------------------------------------------
 # argmax (torch.argmax order: first maximum, NaN wins)
 
