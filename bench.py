@@ -58,10 +58,78 @@ def parse(argv=None):
     ap.add_argument("--cpu-budget-s", type=float, default=15.0)
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="only run a plain copy of MIB MiB (the --pmc byte-counter calibration) and exit")
+    ap.add_argument("--workload", default="q05b", choices=sorted(WORKLOADS),
+                    help="q05b (default): the headline line; the others measure the remaining workloads "
+                         "(one JSON line each, not the headline metric)")
     ap.add_argument("--dominant-only", action="store_true",
                     help="only launch the dominant kernel, eagerly (no graphs), once per layer 4 times over, and "
                          "exit: the workload of the --pmc byte-counter passes")
     return ap.parse_args(argv)
+
+
+# Other workloads: (shape, batch, prompt length, decode steps after the first token)
+WORKLOADS = {
+    "q05b": None,  # the headline line below
+    "q05b-b32": ("QWEN05B", 32, 2048, 511),
+    "q7b": ("QWEN7B", 1, 512, 255),
+    "q7b-prefill": ("QWEN7B", 4, 4096, 0),
+}
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def prefill_flops(cfg, batch: int, t: int) -> float:
+    """Dense FLOPs of a prefill of `t` tokens per row: the linear layers, causal
+    attention (QK^T and PV over the visible keys) and the LM head of the last
+    position only (what the prefill computes when no full logits are asked)."""
+    L, H, hq, hkv, d, inter, v = (cfg.num_hidden_layers, cfg.hidden_size, cfg.num_attention_heads,
+                                  cfg.num_key_value_heads, cfg.head_dim, cfg.intermediate_size, cfg.vocab_size)
+    m = batch * t
+    linear = 2.0 * m * L * (H * (hq + 2 * hkv) * d + hq * d * H + 3 * inter * H)
+    attn = 2.0 * 2.0 * batch * L * hq * d * (t * (t + 1) / 2)
+    return linear + attn + 2.0 * batch * v * H
+
+
+def secondary(args):
+    """One JSON line for a non-headline workload: decode tok/s with the step
+    roofline, or (prefill-only) TTFT with the dense-FLOP MFMA fraction."""
+    import torch
+
+    from minitp import synthetic
+    from minitp.generation import GenerationState
+
+    shape, batch, plen, steps = WORKLOADS[args.workload]
+    cfg = getattr(synthetic, shape)
+    torch.cuda.set_device(0)
+    out = {"workload": args.workload, "shape": shape, "batch": batch, "prompt": plen, "dtype": "bf16"}
+    with torch.inference_mode():
+        model = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device="cuda", seed=0)
+        prompt = synthetic.synthetic_prompt(cfg.vocab_size, batch, plen, seed=0, device="cuda")
+        torch.cuda.synchronize()
+        if steps:
+            decode_run(model, prompt, steps)  # warmup (graph capture for this batch / length)
+            dt, ttft, _, _ = decode_run(model, prompt, steps)
+            total = sum(step_bytes(cfg, plen + s, batch=batch) for s in range(steps))
+            out.update({"decode_tok_s": round(batch * steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 4),
+                        "step_roofline_frac": round(total / dt / 1e9 / HBM_PEAK_GBS, 4),
+                        "roofline_tok_s": round(batch * HBM_PEAK_GBS * 1e9 / (total / steps), 1),
+                        "ttft_ms": round(ttft * 1e3, 3)})
+        else:
+            ttfts = []
+            for _ in range(4):
+                st = GenerationState(model, prompt, 1)
+                a, b = torch.cuda.Event(True), torch.cuda.Event(True)
+                a.record()
+                st.select_next(st.prefill())
+                b.record()
+                torch.cuda.synchronize()
+                ttfts.append(a.elapsed_time(b) / 1e3)
+                del st
+            ttft = sorted(ttfts)[1]  # p50 of the last three (the first includes one-time setup)
+            fl = prefill_flops(cfg, batch, plen)
+            out.update({"ttft_ms": round(ttft * 1e3, 3), "prefill_tflop": round(fl / 1e12, 2),
+                        "mfma_frac": round(fl / ttft / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                        "ttft_ms_all": [round(t * 1e3, 3) for t in ttfts]})
+    print(json.dumps(out), flush=True)
 
 
 def decode_run(model, prompt, n_steps, record_steps=False):
@@ -237,6 +305,9 @@ def main(argv=None):
     if args.copy_calibration:
         torch.cuda.set_device(0)
         copy_calibration(args.copy_calibration)
+        return
+    if WORKLOADS[args.workload] is not None:
+        secondary(args)
         return
     from minitp.bench.benchmark import _percentiles
     from minitp.synthetic import QWEN05B, build_synthetic_model, synthetic_prompt
