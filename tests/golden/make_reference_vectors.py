@@ -46,6 +46,7 @@ ORACLE_CASES = {
     "q7b2_bf16": ("QWEN7B", 2, torch.bfloat16, 1, 16, 8),
     "q05b2_b32_fp32": ("QWEN05B", 2, torch.float32, 32, 24, 8),  # batch-32 decode (GEMM + batched attention)
     "q05b2_b32_bf16": ("QWEN05B", 2, torch.bfloat16, 32, 24, 8),
+    "q05b2_b3_bf16": ("QWEN05B", 2, torch.bfloat16, 3, 40, 24),  # small-batch decode GEMV path, batch 3
     "q7b1_b2_p256_bf16": ("QWEN7B", 1, torch.bfloat16, 2, 256, 2),  # 7B prefill shape (MFMA GEMM + attention)
 }
 TOPK = 16

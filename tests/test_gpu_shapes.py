@@ -1,7 +1,8 @@
 """Parity at the other workloads' layer shapes, with fewer layers (every
 layer runs the same kernels): the 7B decode shape with its untied LM head,
 batch-32 decode at the 0.5B shape (GEMM + batched attention paths) and the 7B
-prefill shape (MFMA GEMMs and prefill attention at 2 x 256 tokens).
+prefill shape (MFMA GEMMs and prefill attention at 2 x 256 tokens), and
+batch-3 decode at the 0.5B shape (the small-batch GEMV path).
 
 Fixtures: tests/golden/{q7b2,q05b2_b32,q7b1_b2_p256}_*.npz, written by
 tests/golden/make_reference_vectors.py from the oracle (which reproduces the
@@ -28,6 +29,7 @@ CASES = {  # fixture: (shape key, layers, dtype)
     "q7b2_bf16": ("qwen2.5-7b", 2, torch.bfloat16),
     "q05b2_b32_fp32": ("qwen2.5-0.5b", 2, torch.float32),
     "q05b2_b32_bf16": ("qwen2.5-0.5b", 2, torch.bfloat16),
+    "q05b2_b3_bf16": ("qwen2.5-0.5b", 2, torch.bfloat16),
     "q7b1_b2_p256_bf16": ("qwen2.5-7b", 1, torch.bfloat16),
 }
 
@@ -57,7 +59,7 @@ def test_fp32_greedy_ids_exact_and_logits(name):
     print(f"{name}: ids exact; max logit err decode {err:.2e} prefill {err_p:.2e}")
 
 
-@pytest.mark.parametrize("name", ["q7b2_bf16", "q05b2_b32_bf16", "q7b1_b2_p256_bf16"])
+@pytest.mark.parametrize("name", ["q7b2_bf16", "q05b2_b32_bf16", "q05b2_b3_bf16", "q7b1_b2_p256_bf16"])
 def test_bf16_logits_teacher_forced(name):
     fx = np.load(os.path.join(GOLDEN, f"{name}.npz"))
     model = _model(name)
