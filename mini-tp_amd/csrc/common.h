@@ -22,12 +22,16 @@ typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ float bf16_to_f32(uint16_t h) { return __uint_as_float(((uint32_t)h) << 16); }
 
-__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  const uint32_t u = __float_as_uint(f);
-  const uint32_t rne = (u + 0x7fffu + ((u >> 16) & 1u)) >> 16;
-  const uint32_t qnan = (u >> 16) | 0x0040u;
-  return (uint16_t)((u & 0x7fffffffu) > 0x7f800000u ? qnan : rne);  // a select, not a branch
+// gfx950's v_cvt_pk_bf16_f32 rounds to nearest even, which is torch's
+// float -> bfloat16 rounding: checked bit for bit against the integer form
+// ((u + 0x7fff + lsb) >> 16) over every non-NaN fp32 pattern; NaN stays NaN.
+typedef float f32x2_cvt __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_cvt __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  const f32x2_cvt v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, bf16x2_cvt));
 }
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) { return (uint16_t)pack_bf16x2(f, 0.f); }
 
 // Round a float to the model's storage precision and back (identity for f32).
 template <typename T>

@@ -89,10 +89,10 @@ __device__ __forceinline__ float dot_chunk<bf16>(const uint4& w, const float*, c
 
 __device__ __forceinline__ uint4 pack_bf16x8(const float* f) {
   uint4 r;
-  r.x = (uint32_t)f32_to_bf16(f[0]) | ((uint32_t)f32_to_bf16(f[1]) << 16);
-  r.y = (uint32_t)f32_to_bf16(f[2]) | ((uint32_t)f32_to_bf16(f[3]) << 16);
-  r.z = (uint32_t)f32_to_bf16(f[4]) | ((uint32_t)f32_to_bf16(f[5]) << 16);
-  r.w = (uint32_t)f32_to_bf16(f[6]) | ((uint32_t)f32_to_bf16(f[7]) << 16);
+  r.x = pack_bf16x2(f[0], f[1]);
+  r.y = pack_bf16x2(f[2], f[3]);
+  r.z = pack_bf16x2(f[4], f[5]);
+  r.w = pack_bf16x2(f[6], f[7]);
   return r;
 }
 
@@ -295,14 +295,23 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < JMAX; ++j) unpack16(xb[m][j], xf[m][j], (T*)nullptr);
   if constexpr (PRO == PRO_NORM) {
+    // Every wave recomputes the row's norm, so this stays short: for bf16 the
+    // sum of squares runs on packed dot instructions (exact products, fp32
+    // accumulation) and the normed row is rounded two elements per
+    // instruction straight into the packed operand of the dots.
     float tot[MM];
 #pragma unroll
     for (int m = 0; m < MM; ++m) {
       float ss = 0.f;
+      if constexpr (sizeof(T) == 2) {
 #pragma unroll
-      for (int j = 0; j < JMAX; ++j)
+        for (int j = 0; j < JMAX; ++j) ss = dot_chunk<T>(xb[m][j], nullptr, xb[m][j], ss);
+      } else {
 #pragma unroll
-        for (int e = 0; e < V; ++e) ss = add_rn(ss, mul_rn(xf[m][j][e], xf[m][j][e]));
+        for (int j = 0; j < JMAX; ++j)
+#pragma unroll
+          for (int e = 0; e < V; ++e) ss = add_rn(ss, mul_rn(xf[m][j][e], xf[m][j][e]));
+      }
       tot[m] = wave_sum(ss);
     }
     if constexpr (KSPLIT > 1) {
@@ -324,9 +333,15 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
       for (int j = 0; j < JMAX; ++j) {
         float wf[V];
         unpack16(nw[j], wf, (T*)nullptr);
+        if constexpr (sizeof(T) == 2) {  // the dots read the packed row only
+          float o[V];
 #pragma unroll
-        for (int e = 0; e < V; ++e) xf[m][j][e] = m < M ? round_to<T>(mul_rn(mul_rn(xf[m][j][e], r), wf[e])) : 0.f;
-        if constexpr (sizeof(T) == 2) xb[m][j] = pack_bf16x8(xf[m][j]);
+          for (int e = 0; e < V; ++e) o[e] = mul_rn(mul_rn(xf[m][j][e], r), wf[e]);
+          xb[m][j] = pack_bf16x8(o);
+        } else {
+#pragma unroll
+          for (int e = 0; e < V; ++e) xf[m][j][e] = m < M ? mul_rn(mul_rn(xf[m][j][e], r), wf[e]) : 0.f;
+        }
       }
     }
   }
