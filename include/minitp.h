@@ -76,6 +76,11 @@ int minitp_add(void* stream, int dtype, const void* a, const void* b, void* out,
 int minitp_silu_mul(void* stream, int dtype, const void* gate, const void* up, int64_t ld_in,
                     void* out, int64_t ld_out, int64_t rows, int64_t n);
 
+/* Tensor.to(torch.bfloat16) of fp32 values (the casts of layer.py:42,
+ * mlp.py:38, rope.py:62 ...): out[i] = round-to-nearest-even bf16 of in[i],
+ * NaN stays NaN. */
+int minitp_cast_f32_bf16(void* stream, const float* in, void* out, int64_t n);
+
 /* ---- linear layers ------------------------------------------------------ */
 /* F.linear(x, W, bias) with fp32 accumulation (linear.py:57-58, 111-122;
  * fused.py:57-61, 102-104), result rounded to dtype, then the epilogue.

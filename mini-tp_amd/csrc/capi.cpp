@@ -123,6 +123,13 @@ int minitp_silu_mul(void* stream, int dtype, const void* gate, const void* up, i
   return launch_silu_mul(S(stream), dtype, gate, up, ld_in, out, ld_out, rows, n);
 }
 
+int minitp_cast_f32_bf16(void* stream, const float* in, void* out, int64_t n) {
+  MINITP_CHECK_ARG(n >= 0, "cast: n=%lld", (long long)n);
+  if (n == 0) return MINITP_OK;
+  MINITP_CHECK_ARG(in && out, "cast: NULL pointer");
+  return launch_cast_f32_bf16(S(stream), in, out, n);
+}
+
 namespace {
 
 int linear_checks(int dtype, const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy,

@@ -222,4 +222,17 @@ int launch_silu_mul(hipStream_t st, int dtype, const void* gate, const void* up,
   return MINITP_OK;
 }
 
+__global__ void cast_f32_bf16_kernel(const float* in, uint16_t* out, int64_t n) {
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += stride) out[i] = f32_to_bf16(in[i]);
+}
+
+int launch_cast_f32_bf16(hipStream_t st, const float* in, void* out, int64_t n) {
+  if (n == 0) return MINITP_OK;
+  const int grid = (int)std::min<int64_t>(cdiv(n, 256), 65536);
+  cast_f32_bf16_kernel<<<grid, 256, 0, st>>>(in, (uint16_t*)out, n);
+  MINITP_LAUNCH_CHECK();
+  return MINITP_OK;
+}
+
 }  // namespace minitp

@@ -96,6 +96,7 @@ int launch_rmsnorm(hipStream_t st, int dtype, const void* x, const void* w, void
 int launch_add(hipStream_t st, int dtype, const void* a, const void* b, void* out, int64_t n, int64_t b_period);
 int launch_silu_mul(hipStream_t st, int dtype, const void* gate, const void* up, int64_t ld_in, void* out,
                     int64_t ld_out, int64_t rows, int64_t n);
+int launch_cast_f32_bf16(hipStream_t st, const float* in, void* out, int64_t n);
 
 // rope.hip
 int launch_rope(hipStream_t st, int dtype, const void* q, const void* k, void* q_out, void* k_out, const float* cos_tab,

@@ -40,6 +40,7 @@ SIGNATURES = {
     "minitp_rmsnorm": (_int, [_vp, _int, _vp, _vp, _vp, _i64, _i64, _f32]),
     "minitp_add": (_int, [_vp, _int, _vp, _vp, _vp, _i64, _i64]),
     "minitp_silu_mul": (_int, [_vp, _int, _vp, _vp, _i64, _vp, _i64, _i64, _i64]),
+    "minitp_cast_f32_bf16": (_int, [_vp, _vp, _vp, _i64]),
     "minitp_linear": (_int, [_vp, _int, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp]),
     "minitp_rmsnorm_linear": (_int, [_vp, _int, _vp, _i64, _vp, _f32, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int,
                                      _vp]),

@@ -236,3 +236,15 @@ def argmax(logits: torch.Tensor) -> torch.Tensor:
     N.check(_lib().minitp_argmax(N.stream(), N.dtype_code(x.dtype), x.data_ptr(), ld, rows, v, out.data_ptr(), 1,
                                  ws.data_ptr(), ws.numel()), "argmax")
     return out
+
+
+def cast_bf16(x: torch.Tensor) -> torch.Tensor:
+    """x.to(torch.bfloat16) for a contiguous fp32 tensor, on the library's
+    conversion (round to nearest even)."""
+    N.require_gpu(x, what="cast_bf16")
+    if x.dtype != torch.float32:
+        raise TypeError(f"cast_bf16: expected float32, got {x.dtype}")
+    x = x.contiguous()
+    out = torch.empty(x.shape, dtype=torch.bfloat16, device=x.device)
+    N.check(_lib().minitp_cast_f32_bf16(N.stream(), x.data_ptr(), out.data_ptr(), x.numel()), "cast_f32_bf16")
+    return out

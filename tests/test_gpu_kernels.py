@@ -379,3 +379,26 @@ def test_embedding_gathers_rows():
     ids = torch.tensor([[0, 999, 17], [5, 5, 3]])
     got = _k().embedding(ids.to(DEV), table.to(DEV)).cpu()
     assert torch.equal(got, F.embedding(ids, table))
+
+
+# ---------------------------------------------------------------------------
+# fp32 -> bf16 rounding (the conversion every bf16 kernel uses)
+
+
+def test_bf16_rounding_matches_torch_bitwise():
+    """Every exponent, both signs, halfway and odd/even ties, subnormals, inf
+    and NaN: bit-identical to torch's CPU Tensor.to(torch.bfloat16), NaN
+    staying NaN."""
+    g = torch.Generator().manual_seed(3)
+    bits = torch.randint(-(2**31), 2**31, (1 << 24,), generator=g, dtype=torch.int64)
+    halves = (torch.arange(0, 1 << 16, dtype=torch.int64) << 16) | 0x8000  # exact ties
+    odd = halves + 0x10000
+    special = torch.tensor([0, 0x80000000, 0x7F800000, 0xFF800000, 0x00000001, 0x007FFFFF, 0x7F7FFFFF,
+                            0x7F7F8000, 0x3F808000, 0x3F818000, 0x7FC00000, 0x7F800001], dtype=torch.int64)
+    u = torch.cat([bits, halves, odd, special]) & 0xFFFFFFFF
+    f = (u - ((u >> 31) << 32)).to(torch.int32).view(torch.float32)
+    got = _k().cast_bf16(f.to(DEV)).cpu()
+    ref = f.to(torch.bfloat16)
+    nan = torch.isnan(f)
+    assert torch.isnan(got[nan].float()).all()
+    assert torch.equal(got[~nan].view(torch.int16), ref[~nan].view(torch.int16))
