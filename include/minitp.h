@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MINITP_ABI_VERSION 2
+#define MINITP_ABI_VERSION 3
 
 enum {
   MINITP_OK = 0,
@@ -198,7 +198,21 @@ int64_t minitp_qwen2_table_bytes(const minitp_qwen2_config* cfg);
 /* One forward over ids [B, T]. logits: [B, T, V] when logits_all, else the
  * last position only [B, V]. next_tok (optional): argmax of the last
  * position per row, written to next_tok[b * next_tok_ld]. The KV caches are
- * [L, B, Hkv, S, D]; rows cache_len .. cache_len + T - 1 are written. */
+ * [L, B, Hkv, S, D]; rows cache_len .. cache_len + T - 1 are written.
+ *
+ * End-of-sequence early stop kept on the device (generate_greedy's
+ * finished mask, generation.py:150-168), on when eos_state is not NULL
+ * (next_tok required): after the token selection, a row that had finished
+ * gets eos_token, and a row finishes when its token is eos_token. eos_state
+ * is device memory of batch + 2 int64 words, zero before the first forward
+ * of a generation: the finished flags, then a halted word, then the stop
+ * column. When every row has finished, the forward sets halted and the stop
+ * column to cursor + 1 (cursor = the column next_tok points into: the
+ * reference's cursor after the append that ends its loop), and stores the
+ * stop column to *eos_host too when that is not NULL (a device address of
+ * pinned host memory, minitp_host_device_pointer). Forwards run after the
+ * halt write no KV rows, change no token and no flag: a host that checks the
+ * stop column a few steps late loses nothing but time. */
 typedef struct minitp_qwen2_step {
   const int64_t* ids;
   int64_t ids_ld;
@@ -215,7 +229,16 @@ typedef struct minitp_qwen2_step {
   int64_t next_tok_ld;
   void* workspace;
   int64_t workspace_bytes;
+  int64_t* eos_state;
+  int64_t eos_token;
+  int64_t cursor;
+  int64_t* eos_host;
 } minitp_qwen2_step;
+
+/* Device address of pinned host memory (hipHostMalloc / torch pin_memory),
+ * for eos_host. No counterpart in the reference (its host reads a device
+ * flag with a blocking copy each step). */
+int minitp_host_device_pointer(void* host, void** device);
 
 int minitp_qwen2_create(const minitp_qwen2_config* cfg, const minitp_qwen2_weights* w,
                         void** handle);

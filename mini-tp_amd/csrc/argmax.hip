@@ -89,7 +89,42 @@ __global__ __launch_bounds__(256) void argmax_merge_kernel(const float* pv, cons
 
 int64_t nslices(int64_t V) { return std::max<int64_t>(1, cdiv(V, SLICE)); }
 
+// generate_greedy's finished mask (generation.py:153-168) after a token
+// selection: tok = finished ? eos : tok; finished |= tok == eos. Once every
+// row has finished, the halted word and the stop column are set (and the
+// stop column stored to the host word); a forward that starts halted leaves
+// tokens and flags alone.
+__global__ __launch_bounds__(256) void eos_update_kernel(const StepState* state, int64_t B) {
+  const StepArgs& a = state->args;
+  int64_t* es = a.eos_state;
+  if (es == nullptr || es[B] != 0) return;  // the same answer for every thread
+  __shared__ int unfinished;
+  if (threadIdx.x == 0) unfinished = 0;
+  __syncthreads();
+  for (int64_t b = threadIdx.x; b < B; b += blockDim.x) {
+    int64_t* slot = a.next_tok + b * a.next_tok_ld;
+    const bool was = es[b] != 0;
+    if (was) *slot = a.eos_token;
+    const bool fin = was || *slot == a.eos_token;
+    es[b] = fin ? 1 : 0;
+    if (!fin) unfinished = 1;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0 && unfinished == 0) {
+    es[B] = 1;
+    es[B + 1] = a.cursor + 1;
+    if (a.eos_host != nullptr)
+      __hip_atomic_store(a.eos_host, a.cursor + 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_SYSTEM);
+  }
+}
+
 }  // namespace
+
+int launch_eos_update(hipStream_t st, const StepState* state, int64_t B) {
+  eos_update_kernel<<<1, 256, 0, st>>>(state, B);
+  MINITP_LAUNCH_CHECK();
+  return MINITP_OK;
+}
 
 int64_t argmax_workspace_bytes(int64_t B, int64_t V) { return B * nslices(V) * (4 + 8); }
 

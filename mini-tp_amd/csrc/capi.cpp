@@ -123,6 +123,12 @@ int minitp_silu_mul(void* stream, int dtype, const void* gate, const void* up, i
   return launch_silu_mul(S(stream), dtype, gate, up, ld_in, out, ld_out, rows, n);
 }
 
+int minitp_host_device_pointer(void* host, void** device) {
+  MINITP_CHECK_ARG(host != nullptr && device != nullptr, "NULL pointer");
+  MINITP_RETURN_HIP(hipHostGetDevicePointer(device, host, 0));
+  return MINITP_OK;
+}
+
 int minitp_cast_f32_bf16(void* stream, const float* in, void* out, int64_t n) {
   MINITP_CHECK_ARG(n >= 0, "cast: n=%lld", (long long)n);
   if (n == 0) return MINITP_OK;

@@ -168,13 +168,13 @@ __device__ __forceinline__ void finish_pair(const GemvArgs& a, int m, int64_t ro
         const int64_t base = ((int64_t)m * s.Hq + head) * D;
         store_f32<T>(q, base + i, oa);
         store_f32<T>(q, base + i + half, ob);
-      } else {
+      } else if (!st->halted) {
         T* kc = (T*)st->args.k_cache + (int64_t)a.layer * s.B * s.Hkv * s.S * D;
         const int64_t base = (((int64_t)b * s.Hkv + (head - s.Hq)) * s.S + st->args.cache_len + tt) * D;
         store_f32<T>(kc, base + i, oa);
         store_f32<T>(kc, base + i + half, ob);
       }
-    } else {
+    } else if (!st->halted) {
       T* vc = (T*)st->args.v_cache + (int64_t)a.layer * s.B * s.Hkv * s.S * D;
       const int64_t base = (((int64_t)b * s.Hkv + (head - s.Hq - s.Hkv)) * s.S + st->args.cache_len + tt) * D;
       store_f32<T>(vc, base + i, va);
@@ -664,14 +664,14 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvArgs a) {
                     const int64_t base = ((int64_t)m * s.Hq + head) * D;
                     store_f32<T>(q, base + i, oa);
                     store_f32<T>(q, base + i + half, ob);
-                  } else {
+                  } else if (!st->halted) {
                     const int64_t g = head - s.Hq;
                     T* kc = (T*)st->args.k_cache + (int64_t)a.layer * s.B * s.Hkv * s.S * D;
                     const int64_t base = (((int64_t)b * s.Hkv + g) * s.S + st->args.cache_len + tt) * D;
                     store_f32<T>(kc, base + i, oa);
                     store_f32<T>(kc, base + i + half, ob);
                   }
-                } else {
+                } else if (!st->halted) {
                   const int64_t g = head - s.Hq - s.Hkv;
                   T* vc = (T*)st->args.v_cache + (int64_t)a.layer * s.B * s.Hkv * s.S * D;
                   const int64_t base = (((int64_t)b * s.Hkv + g) * s.S + st->args.cache_len + tt) * D;

@@ -21,6 +21,12 @@ struct StepArgs {
   void* logits;  // [B, V] (or [B, T, V]) logits output
   int64_t* next_tok;
   int64_t next_tok_ld;
+  // end-of-sequence early stop (NULL eos_state: off); words of eos_state:
+  // [0, B) finished flags, B halted, B + 1 stop column
+  int64_t* eos_state;
+  int64_t eos_token;
+  int64_t cursor;     // column of the output ids that next_tok points into
+  int64_t* eos_host;  // device address of a pinned host word, or NULL
 };
 
 // What the forward's later kernels read from device memory, so a captured
@@ -28,8 +34,8 @@ struct StepArgs {
 // change, and that node writes this struct.
 struct StepState {
   StepArgs args;
-  int32_t error;  // 1: a position was outside the RoPE table
-  int32_t pad_;
+  int32_t error;   // 1: a position was outside the RoPE table
+  int32_t halted;  // early stop reached before this forward: no KV writes
   // T == 1: the RoPE table rows of positions[0], copied by the first kernel of
   // the forward so the QKV epilogue reads them at a fixed address (NaN when
   // the position is outside the table).
@@ -123,6 +129,8 @@ int launch_prefill_attention(hipStream_t st, int dtype, const void* q, const voi
 int64_t argmax_workspace_bytes(int64_t B, int64_t V);
 // Winner of each of `rows` rows of nb (value, index) partials -> out (or
 // state->next_tok when state is non-null; nothing when that is null).
+// End-of-sequence bookkeeping after a forward's token selection (one block).
+int launch_eos_update(hipStream_t st, const StepState* state, int64_t B);
 int launch_argmax_merge(hipStream_t st, const float* pv, const int64_t* pi, int64_t nb, int64_t rows, int64_t* out,
                         int64_t out_stride, const StepState* state);
 // With `state`: logits = state->logits + row_offset, out = state->next_tok

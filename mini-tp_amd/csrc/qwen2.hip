@@ -38,6 +38,7 @@ __global__ void step_embed_kernel(StepState* dst, StepArgs val, const T* __restr
     if (threadIdx.x == 0) {
       dst->args = val;
       dst->error = 0;
+      dst->halted = val.eos_state != nullptr && val.eos_state[gridDim.x / T_] != 0;
     }
     if (T_ == 1) {
       const int64_t pos = val.positions[0];
@@ -64,6 +65,24 @@ __global__ void step_embed_kernel(StepState* dst, StepArgs val, const T* __restr
 
 constexpr int EMBED_THREADS = 128;
 
+StepArgs step_args(const minitp_qwen2_step& s) {
+  StepArgs val{};
+  val.ids = s.ids;
+  val.ids_ld = s.ids_ld;
+  val.positions = s.positions;
+  val.cache_len = s.cache_len;
+  val.k_cache = s.k_cache;
+  val.v_cache = s.v_cache;
+  val.logits = s.logits;
+  val.next_tok = s.next_tok;
+  val.next_tok_ld = s.next_tok_ld;
+  val.eos_state = s.eos_state;
+  val.eos_token = s.eos_token;
+  val.cursor = s.cursor;
+  val.eos_host = s.eos_host;
+  return val;
+}
+
 struct Ws {
   StepState* st;
   void *x, *h, *qkv, *q, *attn, *gu, *act;
@@ -80,6 +99,7 @@ struct Ws {
 struct GraphEntry {
   int64_t batch, max_seq;
   void* workspace;
+  bool eos;  // records the end-of-sequence update after the token selection
   hipGraph_t graph;
   hipGraphExec_t exec;
   hipGraphNode_t first;
@@ -156,20 +176,17 @@ struct Qwen2Program {
 
   // The launch sequence of one forward (also what a decode graph records).
   int run(hipStream_t st, const minitp_qwen2_step& s, const Ws& w) {
+    const int rc = run_model(st, s, w);
+    if (rc || s.eos_state == nullptr) return rc;
+    return launch_eos_update(st, w.st, s.batch);
+  }
+
+  int run_model(hipStream_t st, const minitp_qwen2_step& s, const Ws& w) {
     const int64_t B = s.batch, T = s.tokens, M = B * T;
     const int64_t H = c.hidden, I = c.intermediate, V = c.vocab;
     const int D = c.head_dim;
     int rc;
-    StepArgs val{};
-    val.ids = s.ids;
-    val.ids_ld = s.ids_ld;
-    val.positions = s.positions;
-    val.cache_len = s.cache_len;
-    val.k_cache = s.k_cache;
-    val.v_cache = s.v_cache;
-    val.logits = s.logits;
-    val.next_tok = s.next_tok;
-    val.next_tok_ld = s.next_tok_ld;
+    const StepArgs val = step_args(s);
     const int64_t max_pos = c.max_pos;
     if (c.dtype == MINITP_F32)
       hipLaunchKernelGGL(step_embed_kernel<float>, dim3((unsigned)M), dim3(EMBED_THREADS), 0, st, w.st, val,
@@ -440,6 +457,9 @@ struct Qwen2Program {
                      "logits buffer required (batch %lld, logits_all %d: the LM head stores logits before the argmax)",
                      (long long)s->batch, (int)s->logits_all);
     MINITP_CHECK_ARG(s->ids_ld >= s->tokens, "ids_ld=%lld < tokens", (long long)s->ids_ld);
+    MINITP_CHECK_ARG(s->eos_state == nullptr || (s->next_tok != nullptr && s->eos_token >= 0 && s->cursor >= 0),
+                     "early stop needs next_tok, eos_token >= 0 and cursor >= 0 (eos_token %lld, cursor %lld)",
+                     (long long)s->eos_token, (long long)s->cursor);
     if (s->cache_len < 0 || s->cache_len + s->tokens > s->max_seq) {
       set_error("KV cache overflow: seq %lld+%lld > max_seq_len=%lld", (long long)s->cache_len, (long long)s->tokens,
                 (long long)s->max_seq);
@@ -466,16 +486,7 @@ struct Qwen2Program {
 };
 
 static int patch_and_launch(Qwen2Program* p, GraphEntry& g, hipStream_t st, const minitp_qwen2_step& s, const Ws& w) {
-  StepArgs val{};
-  val.ids = s.ids;
-  val.ids_ld = s.ids_ld;
-  val.positions = s.positions;
-  val.cache_len = s.cache_len;
-  val.k_cache = s.k_cache;
-  val.v_cache = s.v_cache;
-  val.logits = s.logits;
-  val.next_tok = s.next_tok;
-  val.next_tok_ld = s.next_tok_ld;
+  StepArgs val = step_args(s);
   StepState* dst = w.st;
   const void* table = p->embed;
   void* out = w.x;
@@ -627,17 +638,20 @@ int minitp_qwen2_decode(void* handle, void* stream, const minitp_qwen2_step* ste
   int rc = p->check_step(step, w);
   if (rc) return rc;
   hipStream_t st = (hipStream_t)stream;
-  const bool loop_ok = p->loop_why.empty() && step->batch == 1;
-  if (p->decode_path == MINITP_DECODE_PERSISTENT && !loop_ok) {
-    minitp::set_error("persistent decode unavailable: %s",
-                      step->batch != 1 ? "batch != 1" : p->loop_why.c_str());
-    return MINITP_ERR_UNSUPPORTED;
+  // AUTO takes the graph: it is the faster path at every measured shape. The
+  // persistent kernel has no end-of-sequence update, so early stop replays
+  // the graph whatever path is selected.
+  if (p->decode_path == MINITP_DECODE_PERSISTENT && step->eos_state == nullptr) {
+    if (!p->loop_why.empty() || step->batch != 1) {
+      minitp::set_error("persistent decode unavailable: %s", step->batch != 1 ? "batch != 1" : p->loop_why.c_str());
+      return MINITP_ERR_UNSUPPORTED;
+    }
+    return p->run_loop(st, *step);
   }
-  // AUTO takes the graph: it is the faster path at every measured shape
-  if (loop_ok && p->decode_path == MINITP_DECODE_PERSISTENT) return p->run_loop(st, *step);
   std::lock_guard<std::mutex> lock(p->mu);
   for (auto& g : p->graphs)
-    if (g.batch == step->batch && g.max_seq == step->max_seq && g.workspace == step->workspace)
+    if (g.batch == step->batch && g.max_seq == step->max_seq && g.workspace == step->workspace &&
+        g.eos == (step->eos_state != nullptr))
       return minitp::patch_and_launch(p, g, st, *step, w);
   // First step with this shape: run eagerly, then record the same sequence.
   if ((rc = p->run(st, *step, w))) return rc;
@@ -646,6 +660,7 @@ int minitp_qwen2_decode(void* handle, void* stream, const minitp_qwen2_step* ste
   g.batch = step->batch;
   g.max_seq = step->max_seq;
   g.workspace = step->workspace;
+  g.eos = step->eos_state != nullptr;
   MINITP_RETURN_HIP(hipStreamBeginCapture(p->capture_stream, hipStreamCaptureModeRelaxed));
   rc = p->run(p->capture_stream, *step, w);
   hipError_t e = hipStreamEndCapture(p->capture_stream, &g.graph);

@@ -104,6 +104,7 @@ __global__ void rope_kv_write_kernel(const T* qkv, int64_t ld, T* q_out, T* k_ca
   if (idx >= B * T_ * heads * half) return;
   const int64_t i = idx % half;
   const int64_t head = (idx / half) % heads;
+  if (state != nullptr && state->halted && head >= Hq) return;  // early stop reached: no KV rows
   const int64_t n = idx / (half * heads);  // token row b*T + t
   const int64_t b = n / T_, t = n % T_;
   const T* src = qkv + n * ld + head * D;

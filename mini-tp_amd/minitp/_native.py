@@ -41,6 +41,7 @@ SIGNATURES = {
     "minitp_add": (_int, [_vp, _int, _vp, _vp, _vp, _i64, _i64]),
     "minitp_silu_mul": (_int, [_vp, _int, _vp, _vp, _i64, _vp, _i64, _i64, _i64]),
     "minitp_cast_f32_bf16": (_int, [_vp, _vp, _vp, _i64]),
+    "minitp_host_device_pointer": (_int, [_vp, ctypes.POINTER(_vp)]),
     "minitp_linear": (_int, [_vp, _int, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp]),
     "minitp_rmsnorm_linear": (_int, [_vp, _int, _vp, _i64, _vp, _f32, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int,
                                      _vp]),
@@ -83,7 +84,8 @@ class Qwen2Step(ctypes.Structure):
     _fields_ = [("ids", _vp), ("ids_ld", _i64), ("positions", _vp), ("batch", _i64), ("tokens", _i64),
                 ("cache_len", _i64), ("k_cache", _vp), ("v_cache", _vp), ("max_seq", _i64), ("logits", _vp),
                 ("logits_all", _i32), ("next_tok", _vp), ("next_tok_ld", _i64), ("workspace", _vp),
-                ("workspace_bytes", _i64)]
+                ("workspace_bytes", _i64), ("eos_state", _vp), ("eos_token", _i64), ("cursor", _i64),
+                ("eos_host", _vp)]
 
 
 _lib = None

@@ -9,16 +9,31 @@ produced returns that column and ``append`` has nothing left to copy.
 Fixed-length mode (``early_stop=False``) therefore issues no host sync and
 no extra kernels per token.
 
+Early stop on an EOS token keeps the reference's finished mask on the
+device: one more kernel after each token selection applies
+``tok = where(finished, eos, tok); finished |= tok == eos`` and, once every
+row has finished, records the stop column and writes it to a pinned host
+word. The host reads that word instead of a blocking ``finished.all()``
+copy each step; it keeps at most ``EOS_LAG`` steps queued ahead of the GPU,
+and the steps it queued past the stop write no KV rows, so the result, the
+cursor and ``kv.seq_len`` are the reference's.
+
 The decode logits buffer [B, 1, V] is reused: logits returned by one
 ``decode_step`` are overwritten by the next.
 """
 
 from __future__ import annotations
 
+import collections
+import ctypes
+
 import torch
 
+from minitp import _native as N
 from minitp.kv_cache import KVCache
 from minitp.layer import TPQwen2ForCausalLM
+
+EOS_LAG = 2  # decode steps the host may queue before it reads the stop word
 
 
 def _kv_heads_local(model: TPQwen2ForCausalLM) -> int:
@@ -66,6 +81,28 @@ class GenerationState:
         self._last_logits: torch.Tensor | None = None
         self._last_tok: torch.Tensor | None = None
         self._decode_logits: torch.Tensor | None = None
+        self._eos_dev: torch.Tensor | None = None  # [B + 2] finished flags, halted, stop column
+        self._eos_host: torch.Tensor | None = None  # pinned stop column (0 = running)
+        self._eos_host_dev: int | None = None
+
+    def _enable_device_eos(self, eos: int) -> None:
+        """Keep generate_greedy's finished mask and stop test on the device."""
+        b = self.out_ids.shape[0]
+        self.eos = eos
+        self._eos_dev = torch.zeros(b + 2, dtype=torch.long, device=self.out_ids.device)
+        self._eos_host = torch.zeros(1, dtype=torch.long, pin_memory=True)
+        dev = ctypes.c_void_p()
+        N.check(N.lib().minitp_host_device_pointer(self._eos_host.data_ptr(), ctypes.byref(dev)), "host_device_pointer")
+        self._eos_host_dev = dev.value
+
+    def _eos_args(self) -> tuple | None:
+        if self._eos_dev is None:
+            return None
+        return (self._eos_dev.data_ptr(), self.eos, self.cursor, self._eos_host_dev)
+
+    def _eos_stop(self) -> int:
+        """Stop column the device recorded (0 while some row is running)."""
+        return int(self._eos_host[0])
 
     def _next_column(self) -> torch.Tensor | None:
         return self.out_ids[:, self.cursor] if self.cursor < self.total else None
@@ -83,7 +120,7 @@ class GenerationState:
             return self.model(ids, positions=positions, kv_cache=self.kv)
         self._check_position(self.prompt_len - 1)
         col = self._next_column()
-        logits = self.model._native(ids, positions, self.kv, next_tok=col)
+        logits = self.model._native(ids, positions, self.kv, next_tok=col, eos=self._eos_args())
         self._last_logits, self._last_tok = logits, col
         return logits
 
@@ -113,7 +150,8 @@ class GenerationState:
         if tok.dtype != torch.long:
             tok = tok.long()
         col = self._next_column()
-        logits = self.model.decode_native(tok, pos.reshape(()), self.kv, self._decode_logits, col)
+        logits = self.model.decode_native(tok, pos.reshape(()), self.kv, self._decode_logits, col,
+                                          eos=self._eos_args())
         self._last_logits, self._last_tok = logits, col
         return logits
 
@@ -128,6 +166,8 @@ def generate_greedy(model: TPQwen2ForCausalLM, input_ids: torch.Tensor, max_new_
     state = GenerationState(model, input_ids, max_new_tokens, kv=kv, distributed_argmax=distributed_argmax,
                             kv_init=kv_init)
     b = input_ids.shape[0]
+    if early_stop and eos_token_id is not None and state._native and max_new_tokens > 0:
+        return _generate_device_eos(state, eos_token_id, max_new_tokens)
     if early_stop and eos_token_id is not None:
         state.eos = eos_token_id
         state.finished = torch.zeros(b, dtype=torch.bool, device=input_ids.device)
@@ -144,3 +184,34 @@ def generate_greedy(model: TPQwen2ForCausalLM, input_ids: torch.Tensor, max_new_
         if step + 1 < max_new_tokens:
             logits = state.decode_step(tok, pos)
     return state.out_ids[:, : state.cursor] if early_stop else state.out_ids
+
+
+def _generate_device_eos(state: GenerationState, eos: int, max_new_tokens: int) -> torch.Tensor:
+    """generate_greedy's early-stop loop with the finished mask on the device."""
+    if eos < 0:
+        raise ValueError(f"eos_token_id must be >= 0, got {eos}")
+    state._enable_device_eos(eos)
+    kv_start = state.kv.seq_len
+    logits = state.prefill()
+    inflight: collections.deque = collections.deque()
+    for step in range(max_new_tokens):
+        tok = state.select_next(logits)
+        pos = state.append(tok)
+        if step + 1 >= max_new_tokens:
+            break
+        while len(inflight) >= EOS_LAG:
+            inflight.popleft().synchronize()
+        if state._eos_stop():
+            break
+        logits = state.decode_step(tok, pos)
+        ev = torch.cuda.Event()
+        ev.record()
+        inflight.append(ev)
+    torch.cuda.current_stream().synchronize()
+    stop = state._eos_stop()
+    if stop:
+        # every column after the stop was a step the device ran halted
+        state.cursor = stop
+        state.kv.seq_len = kv_start + stop - 1  # the prompt, then one decode per column before the stop
+    state.finished = state._eos_dev[: state.out_ids.shape[0]].bool()
+    return state.out_ids[:, : state.cursor]

@@ -194,7 +194,7 @@ class TPQwen2ForCausalLM(nn.Module):
         return self._prog
 
     def _native(self, input_ids: torch.Tensor, positions: torch.Tensor, kv_cache: KVCache | None,
-                next_tok: torch.Tensor | None = None) -> torch.Tensor:
+                next_tok: torch.Tensor | None = None, eos: tuple | None = None) -> torch.Tensor:
         prog = self.program()
         b, t = input_ids.shape
         dev = prog.device
@@ -212,16 +212,18 @@ class TPQwen2ForCausalLM(nn.Module):
         step = N.Qwen2Step(ids.data_ptr(), ids.stride(0), pos.data_ptr(), b, t, kv.seq_len, kv.k_buf.data_ptr(),
                            kv.v_buf.data_ptr(), kv.max_seq_len, logits.data_ptr(), 1 if t > 1 else 0,
                            N.ptr(next_tok), next_tok.stride(0) if next_tok is not None else 0, ws.data_ptr(),
-                           ws.numel())
+                           ws.numel(), *(eos or (None, 0, 0, None)))
         N.check(N.lib().minitp_qwen2_forward(prog.handle, N.stream(), ctypes.byref(step)), "qwen2_forward")
         if kv_cache is not None:
             kv_cache.advance(t)
         return logits
 
     def decode_native(self, tok: torch.Tensor, pos: torch.Tensor, kv_cache: KVCache, logits: torch.Tensor,
-                      next_tok: torch.Tensor | None) -> torch.Tensor:
+                      next_tok: torch.Tensor | None, eos: tuple | None = None) -> torch.Tensor:
         """One T == 1 step replayed from the program's decode hipGraph.
-        tok [B] (any stride), pos 0-d long, logits [B, 1, V] written in place."""
+        tok [B] (any stride), pos 0-d long, logits [B, 1, V] written in place.
+        eos: (state pointer, token, cursor, host word pointer) of the
+        on-device early stop, or None."""
         prog = self._prog if self._prog is not None else self.program()
         b = tok.shape[0]
         kv_cache.check_room(1)
@@ -229,7 +231,7 @@ class TPQwen2ForCausalLM(nn.Module):
         step = N.Qwen2Step(tok.data_ptr(), tok.stride(0), pos.data_ptr(), b, 1, kv_cache.seq_len,
                            kv_cache.k_buf.data_ptr(), kv_cache.v_buf.data_ptr(), kv_cache.max_seq_len,
                            logits.data_ptr(), 0, N.ptr(next_tok), next_tok.stride(0) if next_tok is not None else 0,
-                           ws.data_ptr(), ws.numel())
+                           ws.data_ptr(), ws.numel(), *(eos or (None, 0, 0, None)))
         N.check(N.lib().minitp_qwen2_decode(prog.handle, N.stream(), ctypes.byref(step)), "qwen2_decode")
         kv_cache.advance(1)
         return logits

@@ -1,0 +1,145 @@
+"""Early stop on an EOS token with the finished mask on the device.
+
+generate_greedy(early_stop=True, eos_token_id=e) (generation.py:133-171)
+against the oracle's loop, run live on the CPU: the same trimmed ids, the
+same KV fill cursor, and no KV row written past it (the cache is poisoned
+with NaN first, so a row written by a step queued past the stop shows up).
+Batches 1-3 run the fused GEMV program, batch 5 the GEMM one.
+"""
+
+import pytest
+import torch
+
+from tests.test_gpu_model import _model_from_state
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.fixture(scope="module")
+def pair():
+    from oracle import qwen2_ref
+
+    shape = qwen2_ref.TINY
+    state = qwen2_ref.synthetic_state(shape, seed=0, dtype=torch.float32)
+    return _model_from_state(shape, state, torch.float32), qwen2_ref.OracleQwen2(shape, state)
+
+
+def _both(pair, prompt, n, eos, max_seq=None):
+    from oracle import qwen2_ref
+
+    from minitp.generation import generate_greedy, make_kv_cache
+
+    model, oracle = pair
+    b, t = prompt.shape
+    max_seq = max_seq or t + n
+    kv = make_kv_cache(model, b, max_seq)
+    kv.poison(float("nan"))
+    okv = oracle.make_kv_cache(b, max_seq)
+    got = generate_greedy(model, prompt.to(DEV), n, eos_token_id=eos, early_stop=True, kv=kv).cpu()
+    ref = qwen2_ref.generate_greedy(oracle, prompt, n, eos_token_id=eos, early_stop=True, kv=okv)
+    assert got.shape == ref.shape and torch.equal(got, ref), (got, ref)
+    assert kv.seq_len == okv.seq_len, (kv.seq_len, okv.seq_len)
+    for buf in kv.k + kv.v:
+        assert torch.isfinite(buf[:, :, : kv.seq_len]).all()
+        assert torch.isnan(buf[:, :, kv.seq_len :]).all(), "a KV row was written past the stop"
+    return got
+
+
+def _free_run(pair, prompt, n):
+    from oracle import qwen2_ref
+
+    return qwen2_ref.generate_greedy(pair[1], prompt, n, early_stop=False)
+
+
+@pytest.mark.parametrize("batch", [1, 3, 5])
+def test_rows_finishing_at_different_steps(pair, batch):
+    prompt, eos, firsts = _rows_sharing_a_token(pair, batch, 32)
+    out = _both(pair, prompt, 32, eos)
+    print(f"batch {batch}: eos {eos}, first reached per row {firsts}, stopped at {out.shape[1]} of {6 + 32}")
+    assert out.shape[1] == 6 + max(firsts) + 1
+
+
+def _rows_sharing_a_token(pair, batch, n):
+    """Prompts of `batch` rows that all generate one token, each row reaching
+    it at a different step, picked from 256 candidate rows (rows of a batch
+    do not interact, so the subset's runs are the candidates' runs). The
+    tiny model mostly repeats one token per row, so few tokens qualify."""
+    from oracle import qwen2_ref
+
+    cand = qwen2_ref.synthetic_prompt(qwen2_ref.TINY.vocab_size, 256, 6, seed=11)
+    gen = _free_run(pair, cand, n)[:, 6:]
+    best = None
+    for v in torch.unique(gen).tolist():
+        hit = gen == v
+        by_step = {}
+        for r in hit.any(1).nonzero().flatten().tolist():
+            by_step.setdefault(int(hit[r].int().argmax()), r)
+        if len(by_step) < batch:
+            continue
+        steps = sorted(by_step)
+        pick = [steps[round(i * (len(steps) - 1) / max(batch - 1, 1))] for i in range(batch)]
+        if best is None or pick[-1] - pick[0] > best[0]:
+            best = (pick[-1] - pick[0], v, [by_step[k] for k in pick], pick)
+    assert best is not None, "no token reached by enough rows at different steps"
+    return cand[best[2]], best[1], best[3]
+
+
+def test_eos_never_produced_runs_full_length(pair):
+    from oracle import qwen2_ref
+
+    prompt = qwen2_ref.synthetic_prompt(qwen2_ref.TINY.vocab_size, 2, 5, seed=12)
+    free = _free_run(pair, prompt, 10)
+    unused = next(v for v in range(qwen2_ref.TINY.vocab_size) if not (free[:, 5:] == v).any())
+    out = _both(pair, prompt, 10, unused)
+    assert out.shape[1] == 15
+
+
+def test_stop_on_the_prefill_token(pair):
+    """Every row's first pick is EOS: no decode step may leave a trace."""
+    from oracle import qwen2_ref
+
+    prompt = qwen2_ref.synthetic_prompt(qwen2_ref.TINY.vocab_size, 1, 7, seed=13)
+    free = _free_run(pair, prompt, 4)
+    out = _both(pair, prompt, 12, int(free[0, 7]))
+    assert out.shape[1] == 8
+
+
+def test_stop_on_the_last_step_and_single_token(pair):
+    from oracle import qwen2_ref
+
+    prompt = qwen2_ref.synthetic_prompt(qwen2_ref.TINY.vocab_size, 1, 5, seed=14)
+    free = _free_run(pair, prompt, 6)
+    last = int(free[0, -1])
+    if not (free[0, 5:-1] == last).any():
+        assert _both(pair, prompt, 6, last).shape[1] == 11
+    _both(pair, prompt, 1, int(free[0, 5]))
+
+
+def test_resume_with_eos_on_a_filled_cache(pair):
+    """kv= holding an earlier prompt: the stop cursor counts from it."""
+    from oracle import qwen2_ref
+
+    from minitp.generation import generate_greedy, make_kv_cache
+
+    model, oracle = pair
+    first = qwen2_ref.synthetic_prompt(qwen2_ref.TINY.vocab_size, 2, 4, seed=15)
+    second = qwen2_ref.synthetic_prompt(qwen2_ref.TINY.vocab_size, 2, 5, seed=16)
+    kv = make_kv_cache(model, 2, 30)
+    okv = oracle.make_kv_cache(2, 30)
+    model(first.to(DEV), kv_cache=kv)
+    oracle(first, kv_cache=okv)
+    free = qwen2_ref.generate_greedy(oracle, second, 12, early_stop=False,
+                                     kv=_copy_cache(oracle, okv))
+    eos = int(free[1, 5 + 2])
+    got = generate_greedy(model, second.to(DEV), 12, eos_token_id=eos, kv=kv).cpu()
+    ref = qwen2_ref.generate_greedy(oracle, second, 12, eos_token_id=eos, kv=okv)
+    assert torch.equal(got, ref) and kv.seq_len == okv.seq_len
+
+
+def _copy_cache(oracle, okv):
+    c = oracle.make_kv_cache(okv.k[0].shape[0], okv.max_seq_len)
+    for dst, src in zip(c.k + c.v, okv.k + okv.v):
+        dst.copy_(src)
+    c.seq_len = okv.seq_len
+    return c
