@@ -32,13 +32,45 @@ constexpr int U = 2;  // gemv_lds_kernel chunk unroll
 constexpr int MAX_GRID = 2048;
 constexpr int64_t REG_MAX_CHUNKS = 1024;
 
+// EPI_QKV_ROPE of a single-token forward: the RoPE rows come from the
+// StepState, so the epilogue's side inputs need no position load first.
+constexpr int EPI_QKV_ROPE1 = 5;
+template <int EPI>
+constexpr bool is_qkv() {
+  return EPI == EPI_QKV_ROPE || EPI == EPI_QKV_ROPE1;
+}
+
+// Buffer resource over [base, base + bytes): a load at a lane offset past
+// the end returns zeros without touching memory. The register path issues
+// all of its input and weight loads through these, unconditionally: a load
+// behind a branch leaves a value that has to be merged with the branch-free
+// default, and the compiler places that merge (and the wait for the load it
+// implies) before the next loads it issues, which would hold the weight
+// stream back by a full memory round trip. Built from wave-uniform values
+// made explicitly uniform, so the resource lives in scalar registers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  const int n = (int)__builtin_amdgcn_readfirstlane(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
+}
+// Cache-policy bits of the weight loads: nt (read once per step) when
+// MINITP_NT_LOADS is set.
+constexpr int W_AUX = MINITP_NT_LOADS ? 2 : 0;
+template <int AUX>
+__device__ __forceinline__ uint4 span_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 
 template <int EPI>
 __device__ __forceinline__ void tuple_rows(int64_t t, const GemvArgs& a, int64_t& ra, int64_t& rb) {
   if constexpr (EPI == EPI_SWIGLU) {
     ra = t * P;
     rb = a.N + t * P;
-  } else if constexpr (EPI == EPI_QKV_ROPE) {
+  } else if constexpr (is_qkv<EPI>()) {
     const int half = a.a.D / 2;
     const int per_head = half / P;
     const int64_t head = t / per_head;
@@ -53,7 +85,7 @@ __device__ __forceinline__ void tuple_rows(int64_t t, const GemvArgs& a, int64_t
 template <int EPI>
 __host__ __device__ __forceinline__ int64_t num_tuples(const GemvArgs& a) {
   if constexpr (EPI == EPI_SWIGLU) return a.N / P;
-  if constexpr (EPI == EPI_QKV_ROPE) return (int64_t)(a.a.Hq + 2 * a.a.Hkv) * (a.a.D / 2) / P;
+  if constexpr (is_qkv<EPI>()) return (int64_t)(a.a.Hq + 2 * a.a.Hkv) * (a.a.D / 2) / P;
   return cdiv(a.N, R);
 }
 
@@ -98,21 +130,30 @@ __device__ __forceinline__ uint4 pack_bf16x8(const float* f) {
 
 // Epilogue side inputs a lane needs for pair ep of row em of tuple rows[]:
 // RoPE: cos/sin of both rows (single-token forwards read the rows the first
-// kernel copied into the StepState); RESID: both residual values.
+// kernel copied into the StepState) in side[0..3] and the two bias values in
+// side[4..5]; RESID: both residual values. The single-token RoPE and the
+// residual loads are unconditional (clamped to rows that exist), so nothing
+// has to wait for them before the epilogue.
 template <typename T, int EPI>
 __device__ __forceinline__ void load_side(const GemvArgs& a, int em, int ep, const int64_t* rows, const bool* rok,
                                           int64_t pos, float* side) {
-  if constexpr (EPI == EPI_QKV_ROPE) {
+  if constexpr (EPI == EPI_QKV_ROPE1) {
+    const int D = a.a.D;
+    const int i = (int)(rows[ep] % D);
+    side[0] = a.st->rope_cos[i];
+    side[1] = a.st->rope_sin[i];
+    side[2] = a.st->rope_cos[i + D / 2];
+    side[3] = a.st->rope_sin[i + D / 2];
+    side[4] = load_f32<T>((const T*)a.bias, rows[ep]);
+    side[5] = load_f32<T>((const T*)a.bias, rows[P + ep]);
+  } else if constexpr (EPI == EPI_QKV_ROPE) {
     const int D = a.a.D;
     const int64_t head = rows[ep] / D;
+    side[4] = load_f32<T>((const T*)a.bias, rows[ep]);
+    side[5] = load_f32<T>((const T*)a.bias, rows[P + ep]);
     if (head < a.a.Hq + a.a.Hkv) {
       const int i = (int)(rows[ep] % D);
-      if (a.a.T == 1) {
-        side[0] = a.st->rope_cos[i];
-        side[1] = a.st->rope_sin[i];
-        side[2] = a.st->rope_cos[i + D / 2];
-        side[3] = a.st->rope_sin[i + D / 2];
-      } else if (pos >= 0 && pos < a.max_pos) {
+      if (pos >= 0 && pos < a.max_pos) {
         side[0] = a.cos_tab[pos * D + i];
         side[1] = a.sin_tab[pos * D + i];
         side[2] = a.cos_tab[pos * D + i + D / 2];
@@ -121,8 +162,9 @@ __device__ __forceinline__ void load_side(const GemvArgs& a, int em, int ep, con
     }
   } else if constexpr (EPI == EPI_RESID) {
     const T* aux = (const T*)a.aux;
-    if (rok[ep]) side[0] = load_f32<T>(aux, em * a.ldy + rows[ep]);
-    if (rok[P + ep]) side[1] = load_f32<T>(aux, em * a.ldy + rows[P + ep]);
+    const int64_t m = em < a.M ? em : 0;
+    side[0] = load_f32<T>(aux, m * a.ldy + (rok[ep] ? rows[ep] : 0));
+    side[1] = load_f32<T>(aux, m * a.ldy + (rok[P + ep] ? rows[P + ep] : 0));
   }
 }
 
@@ -141,11 +183,10 @@ __device__ __forceinline__ void finish_pair(const GemvArgs& a, int m, int64_t ro
     if (okb) store_f32<T>(y, m * a.ldy + row_b, add_rn(side[1], round_to<T>(vb)));
   } else if constexpr (EPI == EPI_SWIGLU) {
     store_f32<T>((T*)a.y, m * a.ldy + row_a, swiglu<T>(round_to<T>(va), round_to<T>(vb)));
-  } else if constexpr (EPI == EPI_QKV_ROPE) {
-    const T* bias = (const T*)a.bias;
+  } else if constexpr (is_qkv<EPI>()) {
     // F.linear output with bias, rounded to the dtype (fused.py:58)
-    va = round_to<T>(va + load_f32<T>(bias, row_a));
-    vb = round_to<T>(vb + load_f32<T>(bias, row_b));
+    va = round_to<T>(va + side[4]);
+    vb = round_to<T>(vb + side[5]);
     const StepState* st = a.st;
     const AttnShape& s = a.a;
     const int D = s.D, half = D / 2;
@@ -229,11 +270,14 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
   const int64_t ntup = num_tuples<EPI>(a);
   const int64_t tstride = (int64_t)gridDim.x * SLOTS;
   const uint4* W = (const uint4*)a.w;
+  const uint32_t row_bytes = (uint32_t)(a.K * (int64_t)sizeof(T));
 
-  // Load order matters: vector loads retire in issue order, so everything
-  // the prologue consumes (input rows, RMSNorm weight, epilogue side inputs)
-  // is requested before the weights; the norm math then overlaps the weight
-  // loads still in flight.
+  // Load order matters: vector loads retire in issue order, so what the
+  // prologue consumes (input rows, RMSNorm weight) is requested first, then
+  // the weights, then the epilogue's side inputs; the norm math overlaps the
+  // weight loads still in flight. Lane l's 16-byte chunk j of a row sits at
+  // byte offset (kw * 64 + l + j * 64 * KSPLIT) * 16; chunks past the row end
+  // read zeros.
   int64_t t = (int64_t)blockIdx.x * SLOTS + slot;
   int64_t rows[R];
   bool rok[R];
@@ -250,14 +294,17 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < R; ++r) rok[r] = ok && row_valid<EPI>(rows[r], a);
   };
+  uint32_t coff[JMAX];
+#pragma unroll
+  for (int j = 0; j < JMAX; ++j) coff[j] = (uint32_t)((kw * 64 + lane + j * 64 * KSPLIT) * 16);
   auto load_w = [&]() {
+    __amdgpu_buffer_rsrc_t rs[R];
 #pragma unroll
-    for (int j = 0; j < JMAX; ++j) {
-      const int64_t c = (int64_t)kw * 64 + lane + (int64_t)j * 64 * KSPLIT;
+    for (int r = 0; r < R; ++r) rs[r] = span_rsrc(W + (rok[r] ? rows[r] : 0) * nchunk, rok[r] ? row_bytes : 0u);
 #pragma unroll
-      for (int r = 0; r < R; ++r)
-        wv[j][r] = (rok[r] && c < nchunk) ? load_stream16(W + rows[r] * nchunk + c) : make_uint4(0, 0, 0, 0);
-    }
+    for (int j = 0; j < JMAX; ++j)
+#pragma unroll
+      for (int r = 0; r < R; ++r) wv[j][r] = span_load16<W_AUX>(rs[r], coff[j]);
   };
   set_rows(t);
 
@@ -266,28 +313,34 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
   float xf[MM][JMAX][V];
   uint4 xb[MM][JMAX];
   uint4 nw[JMAX];
+  {
+    __amdgpu_buffer_rsrc_t nr = span_rsrc(a.norm_w, PRO == PRO_NORM ? row_bytes : 0u);
 #pragma unroll
-  for (int j = 0; j < JMAX; ++j) {
-    const int64_t c = (int64_t)kw * 64 + lane + (int64_t)j * 64 * KSPLIT;
-    nw[j] = (PRO == PRO_NORM && c < nchunk) ? *reinterpret_cast<const uint4*>((const T*)a.norm_w + c * V)
-                                            : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < JMAX; ++j) nw[j] = PRO == PRO_NORM ? span_load16<0>(nr, coff[j]) : make_uint4(0, 0, 0, 0);
 #pragma unroll
-    for (int m = 0; m < MM; ++m)
-      xb[m][j] = (m < M && c < nchunk) ? *reinterpret_cast<const uint4*>(x + m * a.ldx + c * V)
-                                       : make_uint4(0, 0, 0, 0);
+    for (int m = 0; m < MM; ++m) {
+      __amdgpu_buffer_rsrc_t xr = span_rsrc(x + (m < M ? m : 0) * a.ldx, m < M ? row_bytes : 0u);
+#pragma unroll
+      for (int j = 0; j < JMAX; ++j) xb[m][j] = span_load16<0>(xr, coff[j]);
+    }
   }
 
-  // ---- 2. the epilogue's side inputs for the first tuple -----------------------
+  // ---- 2. the first tuple's weights -----------------------------------------
+  load_w();
+  // Keep the scheduler from sinking the weight loads below the prologue math
+  // (and the waits for the input rows that math needs).
+  __builtin_amdgcn_sched_barrier(0);
+
+  // ---- 3. the epilogue's side inputs for the first tuple -----------------------
   const int em = lane / P, ep = lane % P;  // this lane finishes pair ep of row em
-  float side[4] = {0.f, 0.f, 0.f, 0.f};
+  float side[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
   int64_t pos = 0;
   if constexpr (EPI == EPI_QKV_ROPE) {
     if (em < M && a.a.T > 1) pos = a.st->args.positions[em % a.a.T];
+    if (em < M && t < ntup) load_side<T, EPI>(a, em, ep, rows, rok, pos, side);
+  } else {
+    load_side<T, EPI>(a, em, ep, rows, rok, pos, side);
   }
-  if (em < M && t < ntup) load_side<T, EPI>(a, em, ep, rows, rok, pos, side);
-
-  // ---- 3. the first tuple's weights -----------------------------------------
-  load_w();
 
   // ---- 4. input rows in registers (normed and rounded like layer.py:39-42) --
 #pragma unroll
@@ -723,7 +776,7 @@ int pick_k(hipStream_t st, const GemvArgs& a) {
     if (nchunk <= 512) return launch_reg<T, MM, 2, 4, PRO, EPI>(st, a);
     if (nchunk <= REG_MAX_CHUNKS) return launch_reg<T, MM, 4, 4, PRO, EPI>(st, a);
   }
-  if constexpr (MM == 1) return launch_lds<T, MM, PRO, EPI>(st, a);
+  if constexpr (MM == 1) return launch_lds<T, MM, PRO, EPI == EPI_QKV_ROPE1 ? EPI_QKV_ROPE : EPI>(st, a);
   set_error("gemv: M=%lld with K=%lld is served by the GEMM path", (long long)a.M, (long long)a.K);
   return MINITP_ERR_UNSUPPORTED;
 }
@@ -745,7 +798,7 @@ int pick_epi(hipStream_t st, int epi, const GemvArgs& a) {
     case EPI_SWIGLU:
       return pick_m<T, PRO, EPI_SWIGLU>(st, a);
     case EPI_QKV_ROPE:
-      return pick_m<T, PRO, EPI_QKV_ROPE>(st, a);
+      return a.a.T == 1 ? pick_m<T, PRO, EPI_QKV_ROPE1>(st, a) : pick_m<T, PRO, EPI_QKV_ROPE>(st, a);
     case EPI_ARGMAX:
       return pick_m<T, PRO, EPI_ARGMAX>(st, a);
   }
