@@ -277,16 +277,22 @@ def test_decode_attention_fp32(ctx, hq, hkv, d):
     assert (got.double() - ref).abs().max().item() < 2e-5
 
 
-@pytest.mark.parametrize("ctx", [5, 384, 2304])
-def test_decode_attention_bf16(ctx):
-    b, hq, hkv, d = 3, 14, 2, 64
-    g = torch.Generator().manual_seed(ctx)
+@pytest.mark.parametrize("ctx", [1, 5, 16, 17, 130, 384, 513, 767, 2304])
+@pytest.mark.parametrize("b,hq,hkv,d", [(3, 14, 2, 64), (1, 28, 4, 128), (2, 8, 8, 64), (1, 4, 2, 16)])
+def test_decode_attention_bf16(ctx, b, hq, hkv, d):
+    """bf16 decode (fp32 scores, softmax and P V; the output rounded to bf16
+    once): within one bf16 rounding of a float64 reference on the same bf16
+    inputs, at short and split contexts, with the cache rows past the
+    context poisoned."""
+    g = torch.Generator().manual_seed(ctx * 31 + d)
     q = torch.randn(b, 1, hq, d, generator=g).bfloat16()
-    kc = torch.randn(b, hkv, ctx, d, generator=g).bfloat16()
-    vc = torch.randn(b, hkv, ctx, d, generator=g).bfloat16()
+    kc = torch.randn(b, hkv, ctx + 2, d, generator=g).bfloat16()
+    kc[:, :, ctx:] = float("nan")  # rows past the context must not be read
+    vc = torch.randn(b, hkv, ctx + 2, d, generator=g).bfloat16()
+    vc[:, :, ctx:] = float("nan")
     got = _k().attention(q.to(DEV), kc.to(DEV), vc.to(DEV), cache_len=ctx - 1).cpu().double()
     ref = _ref_attention(q, kc, vc, ctx - 1)
-    assert ((got - ref).abs() <= ref.abs() * 2 ** -8 + 1e-6).all()
+    assert ((got - ref).abs() <= ref.abs() * 2 ** -8 + 1e-6).all(), (got - ref).abs().max().item()
 
 
 def test_decode_attention_single_key_returns_v_and_zero_q_averages():
