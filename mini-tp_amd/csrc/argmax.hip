@@ -63,13 +63,25 @@ __global__ __launch_bounds__(256) void argmax_merge_kernel(const float* pv, cons
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float v = -__builtin_inff();
   int64_t i = INT64_MAX;
-  for (int64_t j = tid; j < nb; j += 256) {
-    const float x = pv[row * nb + j];
-    const int64_t xi = pi[row * nb + j];
-    if (argmax_better(x, xi, v, i)) {
-      v = x;
-      i = xi;
+  // partials in batches of four per thread, every load of a batch issued
+  // before the first comparison (a loop that compares as it loads waits one
+  // memory round trip per partial)
+  for (int64_t j0 = tid; j0 < nb; j0 += 4 * 256) {
+    float x[4];
+    int64_t xi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int64_t j = j0 + 256 * k;
+      const int64_t jj = j < nb ? j : j0;  // in bounds; dropped below
+      x[k] = pv[row * nb + jj];
+      xi[k] = pi[row * nb + jj];
     }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+      if (j0 + 256 * k < nb && argmax_better(x[k], xi[k], v, i)) {
+        v = x[k];
+        i = xi[k];
+      }
   }
   wave_argmax(v, i);
   if (lane == 0) {

@@ -175,6 +175,46 @@ int launch_rmsnorm(hipStream_t st, int dtype, const void* x, const void* w, void
   return MINITP_OK;
 }
 
+// Residual add then RMSNorm of the sum, one block per row (layer.py:61-64
+// then 39-42): x = dtype(x + delta) in place, out = RMSNorm(x). Each thread
+// reads and writes only its own elements, so out may alias delta.
+template <typename T>
+__global__ __launch_bounds__(256) void add_rmsnorm_kernel(T* x, const T* delta, const T* __restrict__ w, T* out,
+                                                          int64_t hidden, float eps) {
+  __shared__ float red[4];
+  T* xr = x + blockIdx.x * hidden;
+  const T* dr = delta + blockIdx.x * hidden;
+  T* orow = out + blockIdx.x * hidden;
+  float ss = 0.f;
+  for (int64_t i = threadIdx.x; i < hidden; i += 256) {
+    const float v = round_to<T>(add_rn(load_f32<T>(xr, i), load_f32<T>(dr, i)));
+    store_f32<T>(xr, i, v);
+    ss += mul_rn(v, v);
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  float r = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(tot, (float)hidden), eps)));
+  for (int64_t i = threadIdx.x; i < hidden; i += 256) {
+    float v = load_f32<T>(xr, i);
+    store_f32<T>(orow, i, mul_rn(mul_rn(v, r), load_f32<T>(w, i)));
+  }
+}
+
+int launch_add_rmsnorm(hipStream_t st, int dtype, void* x, const void* delta, const void* w, void* out, int64_t rows,
+                       int64_t hidden, float eps) {
+  if (rows == 0) return MINITP_OK;
+  if (dtype == MINITP_F32)
+    add_rmsnorm_kernel<float><<<(unsigned)rows, 256, 0, st>>>((float*)x, (const float*)delta, (const float*)w,
+                                                              (float*)out, hidden, eps);
+  else
+    add_rmsnorm_kernel<bf16><<<(unsigned)rows, 256, 0, st>>>((bf16*)x, (const bf16*)delta, (const bf16*)w, (bf16*)out,
+                                                             hidden, eps);
+  MINITP_LAUNCH_CHECK();
+  return MINITP_OK;
+}
+
 // ---------------------------------------------------------------------------
 template <typename T>
 __global__ void add_kernel(const T* a, const T* b, T* out, int64_t n, int64_t period) {

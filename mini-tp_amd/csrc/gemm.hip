@@ -6,9 +6,13 @@
 // registers per lane each). Both operands are K-contiguous in memory (x rows
 // and W rows), the layout the MFMA A/B fragments want, so nothing is
 // transposed. K advances in chunks of 256 bytes per row staged in LDS; the
-// next chunk's global loads are issued before the current chunk's MFMAs, so
-// HBM latency overlaps the math. Rows are padded by 16 bytes in LDS to spread
-// the MFMA fragment reads over the banks.
+// global loads of the next DEPTH chunks are in flight (in registers) while a
+// chunk's MFMAs run, so one memory round trip covers DEPTH chunks. The loads
+// are buffer loads whose lanes past the matrix (rows beyond M or N, K beyond
+// the split) get an out-of-range offset and read zeros: no load sits behind
+// a branch, so the compiler can count them precisely instead of waiting for
+// all of them before the next ones issue. Rows are padded by 16 bytes in LDS
+// to spread the MFMA fragment reads over the banks.
 //   bf16: v_mfma_f32_32x32x8bf16_1k (A/B: 4 bf16 per lane, k = 4*(lane/32)+i)
 //   fp32: v_mfma_f32_32x32x2f32     (A/B: 1 float per lane, k = lane/32)
 // Accumulator layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4,
@@ -26,6 +30,40 @@ namespace minitp {
 namespace {
 
 constexpr int OUT_PARTIAL = 100;  // epilogue: fp32 split-K partials
+constexpr uint32_t OOB = 0xffffffffu;  // lane offset that reads zeros
+
+// Buffer resource over [base, base + bytes), wave-uniform (scalar registers).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  const int n = (int)__builtin_amdgcn_readfirstlane(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
+}
+template <int AUX>
+__device__ __forceinline__ uint4 gemm_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+constexpr int GEMM_W_AUX = MINITP_NT_LOADS ? 2 : 0;
+// chunks in flight: register budget of the prefetch (LA + LB uint4 each)
+#ifndef MINITP_GEMM_DEPTH_LARGE
+#define MINITP_GEMM_DEPTH_LARGE 2
+#endif
+#ifndef MINITP_GEMM_DEPTH_SMALL
+#define MINITP_GEMM_DEPTH_SMALL 3
+#endif
+// output tile of the small-M GEMMs (M < 512)
+#ifndef MINITP_GEMM_SMALL_BM
+#define MINITP_GEMM_SMALL_BM 64
+#endif
+#ifndef MINITP_GEMM_SMALL_BN
+#define MINITP_GEMM_SMALL_BN 64
+#endif
+template <int BM>
+constexpr int depth() {
+  return BM >= 128 ? MINITP_GEMM_DEPTH_LARGE : MINITP_GEMM_DEPTH_SMALL;
+}
 // bytes of K per row per LDS chunk: 256 for 64 x 64 tiles, 128 for 128 x 128
 // (both operand tiles of a chunk stay under 40 KiB of LDS)
 template <int BM>
@@ -91,53 +129,67 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ x, int6
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
 
-  uint4 ra[LA], rb[LB];
-  auto load = [&](int64_t k0) {
+  constexpr int DEPTH = depth<BM>();
+  constexpr int ES = (int)sizeof(T);
+  // x rows [0, M) and W rows [0, N) as buffers; a lane's piece is read only
+  // when its row exists and its K lies inside this block's split
+  const __amdgpu_buffer_rsrc_t xr = gemm_rsrc(x, (uint32_t)(((M - 1) * ldx + K) * ES));
+  const __amdgpu_buffer_rsrc_t wr = gemm_rsrc(w, (uint32_t)(N * K * ES));
+  uint4 ra[DEPTH][LA], rb[DEPTH][LB];
+  auto load = [&](int64_t k0, uint4(&a)[LA], uint4(&bb)[LB]) {
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
       const int c = tid + i * 256, row = c / CPR, pc = c % CPR;
       const int64_t k = k0 + pc * V;
-      ra[i] = (m0 + row < M && k < ke) ? *reinterpret_cast<const uint4*>(x + (m0 + row) * ldx + k)
-                                       : make_uint4(0, 0, 0, 0);
+      const bool ok = m0 + row < M && k < ke;
+      a[i] = gemm_load16<0>(xr, ok ? (uint32_t)(((m0 + row) * ldx + k) * ES) : OOB);
     }
 #pragma unroll
     for (int i = 0; i < LB; ++i) {
       const int c = tid + i * 256, row = c / CPR, pc = c % CPR;
       const int64_t k = k0 + pc * V;
-      rb[i] = (n0 + row < N && k < ke) ? load_stream16(reinterpret_cast<const uint4*>(w + (n0 + row) * K + k))
-                                       : make_uint4(0, 0, 0, 0);
+      const bool ok = n0 + row < N && k < ke;
+      bb[i] = gemm_load16<GEMM_W_AUX>(wr, ok ? (uint32_t)(((n0 + row) * K + k) * ES) : OOB);
     }
   };
-  auto stash = [&]() {
+  auto stash = [&](const uint4(&a)[LA], const uint4(&bb)[LB]) {
 #pragma unroll
     for (int i = 0; i < LA; ++i) {
       const int c = tid + i * 256, row = c / CPR, pc = c % CPR;
-      *reinterpret_cast<uint4*>(As + row * ROWB + pc * 16) = ra[i];
+      *reinterpret_cast<uint4*>(As + row * ROWB + pc * 16) = a[i];
     }
 #pragma unroll
     for (int i = 0; i < LB; ++i) {
       const int c = tid + i * 256, row = c / CPR, pc = c % CPR;
-      *reinterpret_cast<uint4*>(Bs + row * ROWB + pc * 16) = rb[i];
+      *reinterpret_cast<uint4*>(Bs + row * ROWB + pc * 16) = bb[i];
     }
   };
 
-  if (kb < ke) load(kb);
-  for (int64_t k0 = kb; k0 < ke; k0 += KCE) {
-    stash();
-    __syncthreads();
-    if (k0 + KCE < ke) load(k0 + KCE);  // in flight during this chunk's MFMAs
+  // chunk c of the split lives in register slot c % DEPTH (loads past the
+  // split read zeros and are never stashed)
 #pragma unroll
-    for (int ks = 0; ks < KCE / Mfma<T>::KSTEP; ++ks) {
+  for (int d = 0; d < DEPTH; ++d) load(kb + (int64_t)d * KCE, ra[d], rb[d]);
+  for (int64_t k0 = kb; k0 < ke; k0 += (int64_t)DEPTH * KCE) {
 #pragma unroll
-      for (int i = 0; i < FM; ++i)
+    for (int d = 0; d < DEPTH; ++d) {
+      const int64_t kc = k0 + (int64_t)d * KCE;
+      if (kc >= ke) break;
+      stash(ra[d], rb[d]);
+      __syncthreads();
+      if (kc + DEPTH * KCE < ke) load(kc + (int64_t)DEPTH * KCE, ra[d], rb[d]);  // in flight for later chunks
 #pragma unroll
-        for (int j = 0; j < FN; ++j) {
-          const char* a_row = As + (wm * (BM / 2) + i * 32 + (lane & 31)) * ROWB;
-          const char* b_row = Bs + (wn * (BN / 2) + j * 32 + (lane & 31)) * ROWB;
-          acc[i][j] = Mfma<T>::step(a_row, b_row, ks, lane, acc[i][j]);
-        }
+      for (int ks = 0; ks < KCE / Mfma<T>::KSTEP; ++ks) {
+#pragma unroll
+        for (int i = 0; i < FM; ++i)
+#pragma unroll
+          for (int j = 0; j < FN; ++j) {
+            const char* a_row = As + (wm * (BM / 2) + i * 32 + (lane & 31)) * ROWB;
+            const char* b_row = Bs + (wn * (BN / 2) + j * 32 + (lane & 31)) * ROWB;
+            acc[i][j] = Mfma<T>::step(a_row, b_row, ks, lane, acc[i][j]);
+          }
+      }
+      __syncthreads();
     }
-    __syncthreads();
   }
 
 #pragma unroll
@@ -184,6 +236,10 @@ template <typename T, int BM, int BN>
 int gemm_launch(hipStream_t st, const T* x, int64_t ldx, const T* w, const T* bias, T* y, int64_t ldy, int64_t M,
                 int64_t N, int64_t K, int epi, const T* aux, const StepState* state, float* ws, int64_t ws_bytes) {
   constexpr int64_t KCE = chunk_bytes<BM>() / sizeof(T);
+  if (N * K * (int64_t)sizeof(T) > 0xffffffffLL || ((M - 1) * ldx + K) * (int64_t)sizeof(T) > 0xffffffffLL) {
+    set_error("gemm: operands over 4 GiB (M=%lld N=%lld K=%lld)", (long long)M, (long long)N, (long long)K);
+    return MINITP_ERR_UNSUPPORTED;
+  }
   const int64_t tiles = cdiv(N, BN) * cdiv(M, BM);
   const int64_t nchunk = cdiv(K, KCE);
   // splits: enough blocks to fill the CUs twice, each at least one chunk deep,
@@ -226,8 +282,9 @@ int gemm_typed(hipStream_t st, const void* x, int64_t ldx, const void* w, const 
   if (M >= 512)
     return gemm_launch<T, 128, 128>(st, (const T*)x, ldx, (const T*)w, (const T*)bias, (T*)y, ldy, M, N, K, epi,
                                     (const T*)aux, state, (float*)ws, ws_bytes);
-  return gemm_launch<T, 64, 64>(st, (const T*)x, ldx, (const T*)w, (const T*)bias, (T*)y, ldy, M, N, K, epi,
-                                (const T*)aux, state, (float*)ws, ws_bytes);
+  return gemm_launch<T, MINITP_GEMM_SMALL_BM, MINITP_GEMM_SMALL_BN>(st, (const T*)x, ldx, (const T*)w,
+                                                                    (const T*)bias, (T*)y, ldy, M, N, K, epi,
+                                                                    (const T*)aux, state, (float*)ws, ws_bytes);
 }
 
 }  // namespace

@@ -85,7 +85,10 @@ bool gemv_supported(int dtype, int64_t M, int64_t K);
 // When `state` is non-null the output base is state->logits (graph replays).
 // With a workspace (ws, ws_bytes), small-M products split K over more
 // blocks and reduce the fp32 partials in a second kernel.
-constexpr int64_t GEMM_WS_BYTES = 8LL << 20;
+#ifndef MINITP_GEMM_WS_MB
+#define MINITP_GEMM_WS_MB 8
+#endif
+constexpr int64_t GEMM_WS_BYTES = (int64_t)MINITP_GEMM_WS_MB << 20;
 int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
                 int64_t ldy, int64_t M, int64_t N, int64_t K, int epi, const void* aux,
                 const StepState* state = nullptr, void* ws = nullptr, int64_t ws_bytes = 0);
@@ -103,6 +106,12 @@ int launch_add(hipStream_t st, int dtype, const void* a, const void* b, void* ou
 int launch_silu_mul(hipStream_t st, int dtype, const void* gate, const void* up, int64_t ld_in, void* out,
                     int64_t ld_out, int64_t rows, int64_t n);
 int launch_cast_f32_bf16(hipStream_t st, const float* in, void* out, int64_t n);
+int launch_add_rmsnorm(hipStream_t st, int dtype, void* x, const void* delta, const void* w, void* out, int64_t rows,
+                       int64_t hidden, float eps);
+// hipBLASLt bf16 y = x W^T (+ bias) for prompt-sized M outside stream capture;
+// MINITP_ERR_UNSUPPORTED when it does not apply (the caller then runs launch_gemm)
+int blaslt_linear_bf16(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
+                       int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws, int64_t ws_bytes);
 
 // rope.hip
 int launch_rope(hipStream_t st, int dtype, const void* q, const void* k, void* q_out, void* k_out, const float* cos_tab,
