@@ -7,7 +7,7 @@
 // and W rows), the layout the MFMA A/B fragments want, so nothing is
 // transposed. K advances in chunks of 256 bytes per row staged in LDS; the
 // global loads of the next DEPTH chunks are in flight (in registers) while a
-// chunk's MFMAs run, so one memory round trip covers DEPTH chunks. The loads
+// chunk's MFMAs run. The loads
 // are buffer loads whose lanes past the matrix (rows beyond M or N, K beyond
 // the split) get an out-of-range offset and read zeros: no load sits behind
 // a branch, so the compiler can count them precisely instead of waiting for
@@ -47,11 +47,13 @@ __device__ __forceinline__ uint4 gemm_load16(__amdgpu_buffer_rsrc_t r, uint32_t 
 }
 constexpr int GEMM_W_AUX = MINITP_NT_LOADS ? 2 : 0;
 // chunks in flight: register budget of the prefetch (LA + LB uint4 each)
+// (one chunk ahead measured best at the 0.5B prompt and 7B prefill shapes;
+// deeper prefetch costs occupancy)
 #ifndef MINITP_GEMM_DEPTH_LARGE
-#define MINITP_GEMM_DEPTH_LARGE 2
+#define MINITP_GEMM_DEPTH_LARGE 1
 #endif
 #ifndef MINITP_GEMM_DEPTH_SMALL
-#define MINITP_GEMM_DEPTH_SMALL 3
+#define MINITP_GEMM_DEPTH_SMALL 1
 #endif
 // output tile of the small-M GEMMs (M < 512)
 #ifndef MINITP_GEMM_SMALL_BM
