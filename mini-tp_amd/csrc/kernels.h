@@ -85,10 +85,11 @@ bool gemv_supported(int dtype, int64_t M, int64_t K);
 // When `state` is non-null the output base is state->logits (graph replays).
 // With a workspace (ws, ws_bytes), small-M products split K over more
 // blocks and reduce the fp32 partials in a second kernel.
-#ifndef MINITP_GEMM_WS_MB
-#define MINITP_GEMM_WS_MB 8
-#endif
-constexpr int64_t GEMM_WS_BYTES = (int64_t)MINITP_GEMM_WS_MB << 20;
+// GEMM workspace of a forward: hipBLASLt's (its heuristics find solutions
+// for the 7B prefill shapes only with tens of MiB), of which the split-K
+// partials of launch_gemm use the first GEMM_SPLIT_BYTES.
+constexpr int64_t GEMM_WS_BYTES = 64LL << 20;
+constexpr int64_t GEMM_SPLIT_BYTES = 8LL << 20;
 int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
                 int64_t ldy, int64_t M, int64_t N, int64_t K, int epi, const void* aux,
                 const StepState* state = nullptr, void* ws = nullptr, int64_t ws_bytes = 0);

@@ -211,7 +211,7 @@ struct Qwen2Program {
       int r = blaslt_linear_bf16(st, xin, ldx, wt, b, y, ldy, M, n, k, w.gemm_ws, GEMM_WS_BYTES);
       if (r == MINITP_ERR_UNSUPPORTED)
         r = launch_gemm(st, c.dtype, xin, ldx, wt, b, y, ldy, M, n, k, MINITP_EPI_NONE, nullptr, nullptr, w.gemm_ws,
-                        GEMM_WS_BYTES);
+                        GEMM_SPLIT_BYTES);
       return r;
     };
     if (blas && (rc = launch_rmsnorm(st, c.dtype, w.x, L(0, MINITP_W_LN1), w.h, M, H, c.eps))) return rc;
@@ -260,7 +260,7 @@ struct Qwen2Program {
       } else {
         if ((rc = launch_rmsnorm(st, c.dtype, w.x, L(l, MINITP_W_LN1), w.h, M, H, c.eps))) return rc;
         if ((rc = launch_gemm(st, c.dtype, w.h, H, L(l, MINITP_W_QKV), L(l, MINITP_W_QKV_BIAS), w.qkv, qkv_rows(), M,
-                              qkv_rows(), H, MINITP_EPI_NONE, nullptr, nullptr, w.gemm_ws, GEMM_WS_BYTES)))
+                              qkv_rows(), H, MINITP_EPI_NONE, nullptr, nullptr, w.gemm_ws, GEMM_SPLIT_BYTES)))
           return rc;
         if ((rc = launch_rope_kv_write(st, c.dtype, w.qkv, qkv_rows(), w.q, nullptr, nullptr, cos_tab, sin_tab, nullptr,
                                        c.max_pos, B, T, c.heads, c.kv_heads, D, s.max_seq, 0, nullptr, w.st, l)))
@@ -289,7 +289,7 @@ struct Qwen2Program {
         if ((rc = launch_gemv(st, c.dtype, PRO_NONE, EPI_RESID, g))) return rc;
       } else {
         if ((rc = launch_gemm(st, c.dtype, w.attn, q_rows(), L(l, MINITP_W_O), nullptr, w.x, H, M, H, q_rows(),
-                              MINITP_EPI_RESID, w.x, nullptr, w.gemm_ws, GEMM_WS_BYTES)))
+                              MINITP_EPI_RESID, w.x, nullptr, w.gemm_ws, GEMM_SPLIT_BYTES)))
           return rc;
       }
       // ---- MLP block ----------------------------------------------------------
@@ -320,12 +320,12 @@ struct Qwen2Program {
       } else {
         if ((rc = launch_rmsnorm(st, c.dtype, w.x, L(l, MINITP_W_LN2), w.h, M, H, c.eps))) return rc;
         if ((rc = launch_gemm(st, c.dtype, w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.gu, 2 * I, M, 2 * I, H,
-                              MINITP_EPI_NONE, nullptr, nullptr, w.gemm_ws, GEMM_WS_BYTES)))
+                              MINITP_EPI_NONE, nullptr, nullptr, w.gemm_ws, GEMM_SPLIT_BYTES)))
           return rc;
         const char* up = (const char*)w.gu + I * es();
         if ((rc = launch_silu_mul(st, c.dtype, w.gu, up, 2 * I, w.act, I, M, I))) return rc;
         if ((rc = launch_gemm(st, c.dtype, w.act, I, L(l, MINITP_W_DOWN), nullptr, w.x, H, M, H, I, MINITP_EPI_RESID,
-                              w.x, nullptr, w.gemm_ws, GEMM_WS_BYTES)))
+                              w.x, nullptr, w.gemm_ws, GEMM_SPLIT_BYTES)))
           return rc;
       }
     }
