@@ -14,6 +14,20 @@ namespace {
 constexpr int GMAX = 8;  // max q heads per KV head served
 constexpr int NW = 8;    // waves per decode block
 
+// Buffer resource over [base, base + bytes), wave-uniform (scalar registers);
+// loads at lane offsets past the end return zeros.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t attn_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  const int n = (int)__builtin_amdgcn_readfirstlane(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
+}
+__device__ __forceinline__ uint4 attn_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
 // Decode geometry: a lane owns 8 consecutive elements of a key row, so LPR
 // lanes cover a row and one load instruction of a wave covers PPI rows. A
 // wave chunk is NI such loads (CP key positions).
@@ -472,20 +486,57 @@ __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, c
   const int64_t tb_last = std::min<int64_t>((int64_t)blockIdx.y * 64 + 63, s.T - 1);
   const int64_t key_end = cache_len + tb_last + 1;  // keys the block's queries may see
 
+  // Tile staging: thread t owns KQ consecutive keys of one 16-byte column pc
+  // (t = kq * PPRW + pc). Its K pieces go to LDS as they are; its V pieces are
+  // transposed on the way, KQ keys of one dim packed into one LDS write. The
+  // next tile's pieces are loaded into registers while the current tile is
+  // computed. Buffer loads past key_end read zeros (no branch, no wait).
+  constexpr int NPC = KT * PPRW;                // 16-byte pieces per matrix per tile
+  constexpr int KQ = NPC >= 256 ? NPC / 256 : 1;
+  const int kq = tid / PPRW, pc = tid % PPRW;
+  const bool stager = tid < NPC / KQ;
+  const uint32_t kv_bytes = (uint32_t)(key_end * D * 2);
+  const __amdgpu_buffer_rsrc_t krs = attn_rsrc(kbase, kv_bytes), vrs = attn_rsrc(vbase, kv_bytes);
+  uint4 kr[KQ], vr[KQ];
+  auto load_tile = [&](int64_t k0) {
+#pragma unroll
+    for (int u = 0; u < KQ; ++u) {
+      const int64_t key = k0 + kq * KQ + u;
+      const uint32_t off = stager && key < key_end ? (uint32_t)((key * D + pc * 8) * 2) : kv_bytes;
+      kr[u] = attn_load16(krs, off);
+      vr[u] = attn_load16(vrs, off);
+    }
+  };
+  auto store_tile = [&]() {
+    if (!stager) return;
+#pragma unroll
+    for (int u = 0; u < KQ; ++u) *(uint4*)(Ks + (kq * KQ + u) * KROW + pc * 16) = kr[u];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint16_t hv[KQ];
+#pragma unroll
+      for (int u = 0; u < KQ; ++u) {
+        const uint32_t wv = e < 2 ? vr[u].x : e < 4 ? vr[u].y : e < 6 ? vr[u].z : vr[u].w;
+        hv[u] = (uint16_t)(e & 1 ? wv >> 16 : wv);
+      }
+      char* dst = Vt + (pc * 8 + e) * VROW + kq * KQ * 2;
+      if constexpr (KQ == 4) {
+        *(uint2*)dst = make_uint2(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
+      } else if constexpr (KQ == 2) {
+        *(uint32_t*)dst = hv[0] | ((uint32_t)hv[1] << 16);
+      } else {
+#pragma unroll
+        for (int u = 0; u < KQ; ++u) *(uint16_t*)(dst + 2 * u) = hv[u];
+      }
+    }
+  };
+
+  load_tile(0);
   for (int64_t k0 = 0; k0 < key_end; k0 += KT) {
     __syncthreads();  // the previous tile is consumed
-    for (int c = tid; c < KT * PPRW; c += 256) {
-      const int j = c / PPRW, pc = c % PPRW;
-      const bool ok = k0 + j < key_end;
-      const uint4 kv = ok ? *(const uint4*)(kbase + (k0 + j) * D + pc * 8) : make_uint4(0, 0, 0, 0);
-      const uint4 vv = ok ? *(const uint4*)(vbase + (k0 + j) * D + pc * 8) : make_uint4(0, 0, 0, 0);
-      *(uint4*)(Ks + j * KROW + pc * 16) = kv;
-      const uint32_t vw[4] = {vv.x, vv.y, vv.z, vv.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        *(uint16_t*)(Vt + (pc * 8 + e) * VROW + j * 2) = (uint16_t)(e & 1 ? vw[e >> 1] >> 16 : vw[e >> 1]);
-    }
+    store_tile();
     __syncthreads();
+    if (k0 + KT < key_end) load_tile(k0 + KT);  // in flight during this tile's math
     if (t0 >= s.T || k0 > cache_len + t0 + 15) continue;  // this strip sees none of the tile
     // ---- scores (row 4 lq + i of the strip, key k0 + 16 kbk + lr)
     float sc[KB][4];
