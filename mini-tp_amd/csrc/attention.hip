@@ -431,13 +431,14 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const T* q, const T* 
 
 // Prefill on matrix cores (bf16): block = (b * Hq + h, 64-query tile), wave
 // w = the 16-query strip t0 = 64 y + 16 w. Per 64-key tile staged in LDS (K
-// row-major, V transposed so that a P V operand is 4 consecutive keys):
-// S = Q K^T by MFMA 16x16x16 (A = the strip's q rows, B = 16 keys), causal
-// mask, online softmax in base 2 per query row (a row's 16 columns of a
-// key block sit in 16 lanes, reduced with xor shuffles), P rounded to bf16
-// through a per-wave LDS tile into A layout, then O += P V by MFMA (B = 16
-// dims x 4 keys per lane). The row sums stay per lane in fp32 and are added
-// across the 16 lanes at the end; O / l is rounded to bf16 once.
+// row-major, V transposed so that a V operand is 4 consecutive keys), the
+// products run transposed: S^T = K Q^T by MFMA 16x16x16 leaves lane
+// (q, r) holding keys 4q .. 4q + 3 of query r, which is exactly its B operand
+// of O^T = V^T P^T, so the probabilities (rounded to bf16) never leave the
+// registers and each lane's softmax state (max, sum; base 2) and O^T column
+// belong to its own query: a tile's max needs two xor shuffles and the
+// rescale none. The row sums stay per lane in fp32 and are added across the
+// four lanes of a query at the end; O / l is rounded to bf16 once.
 template <int D>
 __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, const bf16* kc, const bf16* vc,
                                                                 bf16* out, AttnShape s, int64_t cache_len,
@@ -450,10 +451,8 @@ __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, c
   constexpr int PPRW = D / 8;       // 16-byte pieces per K / V row
   constexpr int KROW = D * 2 + 16;  // LDS bytes per K row (padded)
   constexpr int VROW = KT * 2 + 16; // LDS bytes per transposed V row (one dim)
-  constexpr int PROW = KT * 2 + 16; // LDS bytes per P row
   __shared__ __attribute__((aligned(16))) char Ks[KT * KROW];
   __shared__ __attribute__((aligned(16))) char Vt[D * VROW];
-  __shared__ __attribute__((aligned(16))) char Ps[4][16 * PROW];
   const int G = s.Hq / s.Hkv;
   const int bh = blockIdx.x, b = bh / s.Hq, h = bh % s.Hq, g = h / G;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -462,7 +461,6 @@ __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, c
   const bf16* kbase = kc + ((int64_t)b * s.Hkv + g) * s.S * D;
   const bf16* vbase = vc + ((int64_t)b * s.Hkv + g) * s.S * D;
   const float sl2 = scale * 1.4426950408889634f;
-  char* pw = Ps[wave];
 
   short4_t qa[KS];
   {
@@ -477,12 +475,7 @@ __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, c
   float4_t o[KS];
 #pragma unroll
   for (int dn = 0; dn < KS; ++dn) o[dn] = float4_t{0.f, 0.f, 0.f, 0.f};
-  float m[4], lsum[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    m[i] = -__builtin_inff();
-    lsum[i] = 0.f;
-  }
+  float m[1] = {-__builtin_inff()}, lsum[1] = {0.f};  // of this lane's query (t0 + lr), base 2
   const int64_t tb_last = std::min<int64_t>((int64_t)blockIdx.y * 64 + 63, s.T - 1);
   const int64_t key_end = cache_len + tb_last + 1;  // keys the block's queries may see
 
@@ -538,8 +531,11 @@ __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, c
     __syncthreads();
     if (k0 + KT < key_end) load_tile(k0 + KT);  // in flight during this tile's math
     if (t0 >= s.T || k0 > cache_len + t0 + 15) continue;  // this strip sees none of the tile
-    // ---- scores (row 4 lq + i of the strip, key k0 + 16 kbk + lr)
+    // ---- scores, transposed: S^T[key k0 + 16 kbk + 4 lq + i][query t0 + lr]
+    // (A = the K rows, B = Q^T: the query operand registers as they are)
+    const int64_t qpos = cache_len + t0 + lr;  // this lane's query position
     float sc[KB][4];
+    float mx = -__builtin_inff();
 #pragma unroll
     for (int kbk = 0; kbk < KB; ++kbk) {
       float4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -547,68 +543,56 @@ __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, c
 #pragma unroll
       for (int kb = 0; kb < KS; ++kb) {
         const short4_t kv = *(const short4_t*)(krow + (kb * 16 + 4 * lq) * 2);
-        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(qa[kb], kv, acc, 0, 0, 0);
+        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(kv, qa[kb], acc, 0, 0, 0);
       }
-      const int64_t key = k0 + kbk * 16 + lr;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int64_t qpos = cache_len + t0 + 4 * lq + i;
+        const int64_t key = k0 + kbk * 16 + 4 * lq + i;
         sc[kbk][i] = key <= qpos ? acc[i] * sl2 : -__builtin_inff();
+        mx = fmaxf(mx, sc[kbk][i]);
       }
     }
-    // ---- online softmax per row
-    float alpha[4], mn[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float mx = sc[0][i];
-#pragma unroll
-      for (int kbk = 1; kbk < KB; ++kbk) mx = fmaxf(mx, sc[kbk][i]);
-#pragma unroll
-      for (int msk = 1; msk < 16; msk <<= 1) mx = fmaxf(mx, __shfl_xor(mx, msk, 64));
-      mn[i] = fmaxf(m[i], mx);
-      alpha[i] = mn[i] == -__builtin_inff() ? 1.f : __builtin_amdgcn_exp2f(m[i] - mn[i]);
-      m[i] = mn[i];
-      lsum[i] *= alpha[i];
-    }
-#pragma unroll
-    for (int kbk = 0; kbk < KB; ++kbk)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float pr = sc[kbk][i] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(sc[kbk][i] - mn[i]);
-        lsum[i] += pr;
-        *(uint16_t*)(pw + (4 * lq + i) * PROW + (kbk * 16 + lr) * 2) = f32_to_bf16(pr);
-      }
+    // ---- online softmax of this lane's query (its keys sit in lanes lr, lr + 16, + 32, + 48)
+    mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float mn = fmaxf(m[0], mx);
+    const float alpha = mn == -__builtin_inff() ? 1.f : __builtin_amdgcn_exp2f(m[0] - mn);
+    m[0] = mn;
+    lsum[0] *= alpha;
 #pragma unroll
     for (int dn = 0; dn < KS; ++dn)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) o[dn][i] *= alpha[i];
-    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-    __builtin_amdgcn_wave_barrier();
-    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-    // ---- O += P V
+      for (int i = 0; i < 4; ++i) o[dn][i] *= alpha;
+    // ---- O^T += V^T P^T: P^T[key 4 lq + e][query lr] is this lane's scores, as they are
 #pragma unroll
     for (int kk = 0; kk < KB; ++kk) {
-      const short4_t pa = *(const short4_t*)(pw + lr * PROW + (kk * 16 + 4 * lq) * 2);
+      float pr[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        pr[i] = sc[kk][i] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(sc[kk][i] - mn);
+        lsum[0] += pr[i];
+      }
+      const short4_t pb =
+          __builtin_bit_cast(short4_t, make_uint2(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3])));
 #pragma unroll
       for (int dn = 0; dn < KS; ++dn) {
-        const short4_t vb = *(const short4_t*)(Vt + (dn * 16 + lr) * VROW + (kk * 16 + 4 * lq) * 2);
-        o[dn] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb, o[dn], 0, 0, 0);
+        const short4_t va = *(const short4_t*)(Vt + (dn * 16 + lr) * VROW + (kk * 16 + 4 * lq) * 2);
+        o[dn] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[dn], 0, 0, 0);
       }
     }
   }
   if (t0 >= s.T) return;
+  // row sum of this lane's query over the four lanes holding its keys
+  float l = lsum[0];
+  l += __shfl_xor(l, 16, 64);
+  l += __shfl_xor(l, 32, 64);
+  const int64_t t = t0 + lr;
+  if (t >= s.T) return;
+  bf16* orow = out + (((int64_t)b * s.T + t) * s.Hq + h) * D;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
-#pragma unroll
-    for (int msk = 1; msk < 16; msk <<= 1) lsum[i] += __shfl_xor(lsum[i], msk, 64);
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const int64_t t = t0 + 4 * lq + i;
-    if (t >= s.T) continue;
-#pragma unroll
-    for (int dn = 0; dn < KS; ++dn)
-      store_f32<bf16>(out, (((int64_t)b * s.T + t) * s.Hq + h) * D + dn * 16 + lr, o[dn][i] / lsum[i]);
-  }
+  for (int dn = 0; dn < KS; ++dn)  // O^T[dim 16 dn + 4 lq + i][query lr]: four consecutive dims
+    *(uint2*)(orow + dn * 16 + 4 * lq) =
+        make_uint2(pack_bf16x2(o[dn][0] / l, o[dn][1] / l), pack_bf16x2(o[dn][2] / l, o[dn][3] / l));
 }
 
 template <typename T, int D, int HP>
