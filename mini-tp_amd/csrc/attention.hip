@@ -462,14 +462,27 @@ __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, c
   const bf16* vbase = vc + ((int64_t)b * s.Hkv + g) * s.S * D;
   const float sl2 = scale * 1.4426950408889634f;
 
+  // head dims that are a multiple of 32 run gfx950's 16x16x32 MFMA (8 bf16 per
+  // lane per operand: k = 8 (lane / 16) + e), 16 keeps 16x16x16 (k = 4 (lane / 16) + e)
+  constexpr bool W32 = D % 32 == 0;
+  typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
   short4_t qa[KS];
+  bf16x8_t qa8[W32 ? D / 32 : 1];
   {
     const int64_t t = t0 + lr;
+    const bf16* qrow = q + (((int64_t)b * s.T + (t < s.T ? t : 0)) * s.Hq + h) * D;
+    if constexpr (W32) {
 #pragma unroll
-    for (int kb = 0; kb < KS; ++kb) {
-      const uint2 v = t < s.T ? *(const uint2*)(q + (((int64_t)b * s.T + t) * s.Hq + h) * D + kb * 16 + 4 * lq)
-                              : make_uint2(0, 0);
-      qa[kb] = __builtin_bit_cast(short4_t, v);
+      for (int kb = 0; kb < D / 32; ++kb) {
+        const uint4 v = t < s.T ? *(const uint4*)(qrow + kb * 32 + 8 * lq) : make_uint4(0, 0, 0, 0);
+        qa8[kb] = __builtin_bit_cast(bf16x8_t, v);
+      }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < KS; ++kb) {
+        const uint2 v = t < s.T ? *(const uint2*)(qrow + kb * 16 + 4 * lq) : make_uint2(0, 0);
+        qa[kb] = __builtin_bit_cast(short4_t, v);
+      }
     }
   }
   float4_t o[KS];
@@ -540,10 +553,18 @@ __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, c
     for (int kbk = 0; kbk < KB; ++kbk) {
       float4_t acc = {0.f, 0.f, 0.f, 0.f};
       const char* krow = Ks + (kbk * 16 + lr) * KROW;
+      if constexpr (W32) {
 #pragma unroll
-      for (int kb = 0; kb < KS; ++kb) {
-        const short4_t kv = *(const short4_t*)(krow + (kb * 16 + 4 * lq) * 2);
-        acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(kv, qa[kb], acc, 0, 0, 0);
+        for (int kb = 0; kb < D / 32; ++kb) {
+          const bf16x8_t kv = __builtin_bit_cast(bf16x8_t, *(const uint4*)(krow + (kb * 32 + 8 * lq) * 2));
+          acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qa8[kb], acc, 0, 0, 0);
+        }
+      } else {
+#pragma unroll
+        for (int kb = 0; kb < KS; ++kb) {
+          const short4_t kv = *(const short4_t*)(krow + (kb * 16 + 4 * lq) * 2);
+          acc = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(kv, qa[kb], acc, 0, 0, 0);
+        }
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
@@ -564,6 +585,7 @@ __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, c
 #pragma unroll
       for (int i = 0; i < 4; ++i) o[dn][i] *= alpha;
     // ---- O^T += V^T P^T: P^T[key 4 lq + e][query lr] is this lane's scores, as they are
+    uint2 pk[KB];  // this lane's probabilities of key block kk, bf16
 #pragma unroll
     for (int kk = 0; kk < KB; ++kk) {
       float pr[4];
@@ -572,12 +594,33 @@ __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, c
         pr[i] = sc[kk][i] == -__builtin_inff() ? 0.f : __builtin_amdgcn_exp2f(sc[kk][i] - mn);
         lsum[0] += pr[i];
       }
-      const short4_t pb =
-          __builtin_bit_cast(short4_t, make_uint2(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3])));
+      pk[kk] = make_uint2(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]));
+    }
+    if constexpr (W32) {
+      // one MFMA per 32 keys: k-index 8 lq + e is key 32 j + 4 lq + e (e < 4) or
+      // 32 j + 16 + 4 lq + (e - 4), the same permutation in both operands
 #pragma unroll
-      for (int dn = 0; dn < KS; ++dn) {
-        const short4_t va = *(const short4_t*)(Vt + (dn * 16 + lr) * VROW + (kk * 16 + 4 * lq) * 2);
-        o[dn] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[dn], 0, 0, 0);
+      for (int j = 0; j < KB / 2; ++j) {
+        const bf16x8_t pb = __builtin_bit_cast(bf16x8_t, make_uint4(pk[2 * j].x, pk[2 * j].y, pk[2 * j + 1].x,
+                                                                    pk[2 * j + 1].y));
+#pragma unroll
+        for (int dn = 0; dn < KS; ++dn) {
+          const char* vrow = Vt + (dn * 16 + lr) * VROW;
+          const uint2 v0 = *(const uint2*)(vrow + (32 * j + 4 * lq) * 2);
+          const uint2 v1 = *(const uint2*)(vrow + (32 * j + 16 + 4 * lq) * 2);
+          const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(v0.x, v0.y, v1.x, v1.y));
+          o[dn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb, o[dn], 0, 0, 0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int kk = 0; kk < KB; ++kk) {
+        const short4_t pb = __builtin_bit_cast(short4_t, pk[kk]);
+#pragma unroll
+        for (int dn = 0; dn < KS; ++dn) {
+          const short4_t va = *(const short4_t*)(Vt + (dn * 16 + lr) * VROW + (kk * 16 + 4 * lq) * 2);
+          o[dn] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(va, pb, o[dn], 0, 0, 0);
+        }
       }
     }
   }
