@@ -429,8 +429,8 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const T* q, const T* 
 }
 
 
-// Prefill on matrix cores (bf16): block = (b * Hq + h, 64-query tile), wave
-// w = the 16-query strip t0 = 64 y + 16 w. Per 64-key tile staged in LDS (K
+// Prefill on matrix cores (bf16): block = (b * Hq + h, PQ-query tile), wave
+// w = the 16-query strip t0 = PQ y + 16 w (all strips share each staged tile). Per 64-key tile staged in LDS (K
 // row-major, V transposed so that a V operand is 4 consecutive keys), the
 // products run transposed: S^T = K Q^T by MFMA 16x16x16 leaves lane
 // (q, r) holding keys 4q .. 4q + 3 of query r, which is exactly its B operand
@@ -439,10 +439,12 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const T* q, const T* 
 // belong to its own query: a tile's max needs two xor shuffles and the
 // rescale none. The row sums stay per lane in fp32 and are added across the
 // four lanes of a query at the end; O / l is rounded to bf16 once.
-template <int D>
-__global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, const bf16* kc, const bf16* vc,
-                                                                bf16* out, AttnShape s, int64_t cache_len,
-                                                                float scale) {
+// PW waves (16-query strips) per block, PQ = 16 PW queries.
+template <int D, int PW>
+__global__ __launch_bounds__(PW * 64) void prefill_attn_mfma_kernel(const bf16* q, const bf16* kc, const bf16* vc,
+                                                                    bf16* out, AttnShape s, int64_t cache_len,
+                                                                    float scale) {
+  constexpr int PQ = 16 * PW;
   typedef short short4_t __attribute__((ext_vector_type(4)));
   typedef float float4_t __attribute__((ext_vector_type(4)));
   constexpr int KT = 64;            // keys per tile
@@ -457,7 +459,7 @@ __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, c
   const int bh = blockIdx.x, b = bh / s.Hq, h = bh % s.Hq, g = h / G;
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int lr = lane % 16, lq = lane / 16;
-  const int64_t t0 = (int64_t)blockIdx.y * 64 + wave * 16;
+  const int64_t t0 = (int64_t)blockIdx.y * PQ + wave * 16;
   const bf16* kbase = kc + ((int64_t)b * s.Hkv + g) * s.S * D;
   const bf16* vbase = vc + ((int64_t)b * s.Hkv + g) * s.S * D;
   const float sl2 = scale * 1.4426950408889634f;
@@ -489,7 +491,7 @@ __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, c
 #pragma unroll
   for (int dn = 0; dn < KS; ++dn) o[dn] = float4_t{0.f, 0.f, 0.f, 0.f};
   float m[1] = {-__builtin_inff()}, lsum[1] = {0.f};  // of this lane's query (t0 + lr), base 2
-  const int64_t tb_last = std::min<int64_t>((int64_t)blockIdx.y * 64 + 63, s.T - 1);
+  const int64_t tb_last = std::min<int64_t>((int64_t)blockIdx.y * PQ + PQ - 1, s.T - 1);
   const int64_t key_end = cache_len + tb_last + 1;  // keys the block's queries may see
 
   // Tile staging: thread t owns KQ consecutive keys of one 16-byte column pc
@@ -498,7 +500,7 @@ __global__ __launch_bounds__(256) void prefill_attn_mfma_kernel(const bf16* q, c
   // next tile's pieces are loaded into registers while the current tile is
   // computed. Buffer loads past key_end read zeros (no branch, no wait).
   constexpr int NPC = KT * PPRW;                // 16-byte pieces per matrix per tile
-  constexpr int KQ = NPC >= 256 ? NPC / 256 : 1;
+  constexpr int KQ = NPC >= PW * 64 ? NPC / (PW * 64) : 1;
   const int kq = tid / PPRW, pc = tid % PPRW;
   const bool stager = tid < NPC / KQ;
   const uint32_t kv_bytes = (uint32_t)(key_end * D * 2);
@@ -682,10 +684,16 @@ template <typename T, int D>
 int prefill_dispatch(hipStream_t st, const void* q, const void* k, const void* v, void* out, const AttnShape& s,
                      int64_t cache_len) {
   const float scale = 1.0f / sqrtf((float)D);
-  if constexpr (sizeof(T) == 2)
-    hipLaunchKernelGGL((prefill_attn_mfma_kernel<D>), dim3(s.B * s.Hq, (unsigned)cdiv(s.T, 64)), dim3(256), 0, st,
-                       (const bf16*)q, (const bf16*)k, (const bf16*)v, (bf16*)out, s, cache_len, scale);
-  else
+  if constexpr (sizeof(T) == 2) {
+    // 128-query blocks (eight strips share each staged K / V tile) once they
+    // fill the chip; 64-query blocks for short prompts
+    if ((int64_t)s.B * s.Hq * cdiv(s.T, 128) >= 512)
+      hipLaunchKernelGGL((prefill_attn_mfma_kernel<D, 8>), dim3(s.B * s.Hq, (unsigned)cdiv(s.T, 128)), dim3(512), 0,
+                         st, (const bf16*)q, (const bf16*)k, (const bf16*)v, (bf16*)out, s, cache_len, scale);
+    else
+      hipLaunchKernelGGL((prefill_attn_mfma_kernel<D, 4>), dim3(s.B * s.Hq, (unsigned)cdiv(s.T, 64)), dim3(256), 0,
+                         st, (const bf16*)q, (const bf16*)k, (const bf16*)v, (bf16*)out, s, cache_len, scale);
+  } else
     hipLaunchKernelGGL((prefill_attn_kernel<T, D>), dim3(s.B * s.Hq, (unsigned)cdiv(s.T, QT)), dim3(256), 0, st,
                        (const T*)q, (const T*)k, (const T*)v, (T*)out, s, cache_len, scale);
   MINITP_LAUNCH_CHECK();

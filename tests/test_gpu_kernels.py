@@ -340,6 +340,23 @@ def test_prefill_attention_causal_bf16(t, cache_len, hq, hkv, d):
     assert (got.double() - ref).abs().max().item() < 3e-2
 
 
+@pytest.mark.parametrize("b,t,cache_len,hq,hkv,d", [(2, 1200, 37, 28, 4, 128), (4, 1200, 100, 14, 2, 64)])
+def test_prefill_attention_causal_bf16_long(b, t, cache_len, hq, hkv, d):
+    """Prompts long enough for the 128-query blocks (eight strips sharing each
+    staged K / V tile), with a key offset and the rows past the keys
+    poisoned; same bar as the short cases."""
+    s = cache_len + t + 3
+    g = torch.Generator().manual_seed(t + d)
+    q = torch.randn(b, t, hq, d, generator=g).bfloat16()
+    kc = torch.randn(b, hkv, s, d, generator=g).bfloat16()
+    vc = torch.randn(b, hkv, s, d, generator=g).bfloat16()
+    kc[:, :, cache_len + t:] = float("nan")
+    vc[:, :, cache_len + t:] = float("nan")
+    got = _k().attention(q.to(DEV), kc.to(DEV), vc.to(DEV), cache_len=cache_len).cpu().double()
+    ref = _ref_attention(q.double(), kc.double(), vc.double(), cache_len)
+    assert (got - ref).abs().max().item() < 3e-2
+
+
 # ---------------------------------------------------------------------------
 # argmax (torch.argmax order: first maximum, NaN wins)
 
