@@ -202,9 +202,54 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(T* x, const T* delta, 
   }
 }
 
+// bf16 rows of hidden % 8 == 0: the same math in 16-byte pieces (8 elements per
+// load and store; a thread's elements are whole pieces).
+__global__ __launch_bounds__(256) void add_rmsnorm8_kernel(bf16* x, const bf16* delta, const bf16* __restrict__ w,
+                                                           bf16* out, int64_t hidden, float eps) {
+  __shared__ float red[4];
+  uint4* xr = reinterpret_cast<uint4*>(x + blockIdx.x * hidden);
+  const uint4* dr = reinterpret_cast<const uint4*>(delta + blockIdx.x * hidden);
+  uint4* orow = reinterpret_cast<uint4*>(out + blockIdx.x * hidden);
+  const uint4* wr = reinterpret_cast<const uint4*>(w);
+  const int64_t n8 = hidden / 8;
+  float ss = 0.f;
+  for (int64_t c = threadIdx.x; c < n8; c += 256) {
+    float a[8], d[8];
+    unpack16(xr[c], a, (bf16*)nullptr);
+    unpack16(dr[c], d, (bf16*)nullptr);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      a[e] = round_to<bf16>(add_rn(a[e], d[e]));
+      ss += mul_rn(a[e], a[e]);
+    }
+    xr[c] = make_uint4(pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3]), pack_bf16x2(a[4], a[5]),
+                       pack_bf16x2(a[6], a[7]));
+  }
+  ss = wave_sum(ss);
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = ss;
+  __syncthreads();
+  float tot = (red[0] + red[1]) + (red[2] + red[3]);
+  float r = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(tot, (float)hidden), eps)));
+  for (int64_t c = threadIdx.x; c < n8; c += 256) {
+    float a[8], wf[8], o[8];
+    unpack16(xr[c], a, (bf16*)nullptr);
+    unpack16(wr[c], wf, (bf16*)nullptr);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = mul_rn(mul_rn(a[e], r), wf[e]);
+    orow[c] = make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]),
+                         pack_bf16x2(o[6], o[7]));
+  }
+}
+
 int launch_add_rmsnorm(hipStream_t st, int dtype, void* x, const void* delta, const void* w, void* out, int64_t rows,
                        int64_t hidden, float eps) {
   if (rows == 0) return MINITP_OK;
+  if (dtype == MINITP_BF16 && hidden % 8 == 0 && aligned16(x) && aligned16(delta) && aligned16(w) && aligned16(out)) {
+    add_rmsnorm8_kernel<<<(unsigned)rows, 256, 0, st>>>((bf16*)x, (const bf16*)delta, (const bf16*)w, (bf16*)out,
+                                                        hidden, eps);
+    MINITP_LAUNCH_CHECK();
+    return MINITP_OK;
+  }
   if (dtype == MINITP_F32)
     add_rmsnorm_kernel<float><<<(unsigned)rows, 256, 0, st>>>((float*)x, (const float*)delta, (const float*)w,
                                                               (float*)out, hidden, eps);
@@ -248,9 +293,37 @@ __global__ void silu_mul_kernel(const T* gate, const T* up, int64_t ld_in, T* ou
   }
 }
 
+// bf16, 8 elements per thread through 16-byte loads and stores (rows of n % 8
+// == 0 elements, 16-byte aligned row starts); same math as silu_mul_kernel.
+__global__ void silu_mul8_kernel(const bf16* gate, const bf16* up, int64_t ld_in, bf16* out, int64_t ld_out,
+                                 int64_t rows, int64_t n) {
+  const int64_t n8 = n / 8, total = rows * n8;
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += stride) {
+    const int64_t r = i / n8, c = (i % n8) * 8;
+    const uint4 gv = *reinterpret_cast<const uint4*>(gate + r * ld_in + c);
+    const uint4 uv = *reinterpret_cast<const uint4*>(up + r * ld_in + c);
+    float g[8], u[8], o[8];
+    unpack16(gv, g, (bf16*)nullptr);
+    unpack16(uv, u, (bf16*)nullptr);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = swiglu<bf16>(g[e], u[e]);
+    *reinterpret_cast<uint4*>(out + r * ld_out + c) =
+        make_uint4(pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3]), pack_bf16x2(o[4], o[5]), pack_bf16x2(o[6], o[7]));
+  }
+}
+
 int launch_silu_mul(hipStream_t st, int dtype, const void* gate, const void* up, int64_t ld_in, void* out,
                     int64_t ld_out, int64_t rows, int64_t n) {
   if (rows * n == 0) return MINITP_OK;
+  const bool vec = dtype == MINITP_BF16 && n % 8 == 0 && ld_in % 8 == 0 && ld_out % 8 == 0 && aligned16(gate) &&
+                   aligned16(up) && aligned16(out);
+  if (vec) {
+    const int grid8 = (int)std::min<int64_t>(cdiv(rows * (n / 8), 256), 65536);
+    silu_mul8_kernel<<<grid8, 256, 0, st>>>((const bf16*)gate, (const bf16*)up, ld_in, (bf16*)out, ld_out, rows, n);
+    MINITP_LAUNCH_CHECK();
+    return MINITP_OK;
+  }
   int grid = (int)std::min<int64_t>(cdiv(rows * n, 256), 65536);
   if (dtype == MINITP_F32)
     silu_mul_kernel<float><<<grid, 256, 0, st>>>((const float*)gate, (const float*)up, ld_in, (float*)out, ld_out,

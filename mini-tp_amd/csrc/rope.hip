@@ -129,12 +129,93 @@ __global__ void rope_kv_write_kernel(const T* qkv, int64_t ld, T* q_out, T* k_ca
   }
 }
 
+__device__ __forceinline__ void store8_bf16(bf16* dst, const float* v) {
+  if (((uintptr_t)dst & 15u) == 0) {
+    *reinterpret_cast<uint4*>(dst) = make_uint4(pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]),
+                                                pack_bf16x2(v[4], v[5]), pack_bf16x2(v[6], v[7]));
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) store_f32<bf16>(dst, e, v[e]);
+  }
+}
+
+// The same as rope_kv_write_kernel<bf16> for D / 2 % 8 == 0, eight pairs per
+// thread: 16-byte loads of the qkv row (the caller checks its alignment) and
+// of the fp32 tables, 16-byte stores wherever the destination allows them.
+__global__ void rope_kv_write8_kernel(const bf16* qkv, int64_t ld, bf16* q_out, bf16* k_cache, bf16* v_cache,
+                                      const float* cos_tab, const float* sin_tab, const int64_t* positions,
+                                      int64_t max_pos, int64_t B, int64_t T_, int64_t Hq, int64_t Hkv, int64_t D,
+                                      int64_t S, int64_t cache_len, int32_t* error_flag, const StepState* state,
+                                      int layer) {
+  if (state != nullptr) {
+    const int64_t layer_off = (int64_t)layer * B * Hkv * S * D;
+    positions = state->args.positions;
+    cache_len = state->args.cache_len;
+    k_cache = (bf16*)state->args.k_cache + layer_off;
+    v_cache = (bf16*)state->args.v_cache + layer_off;
+    error_flag = (int32_t*)&state->error;
+  }
+  const int64_t half = D / 2, groups = half / 8, heads = Hq + 2 * Hkv;
+  int64_t idx = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  if (idx >= B * T_ * heads * groups) return;
+  const int64_t i = (idx % groups) * 8;
+  const int64_t head = (idx / groups) % heads;
+  if (state != nullptr && state->halted && head >= Hq) return;
+  const int64_t n = idx / (groups * heads);
+  const int64_t b = n / T_, t = n % T_;
+  const bf16* src = qkv + n * ld + head * D;
+  float xa[8], xb[8], oa[8], ob[8];
+  unpack16(*reinterpret_cast<const uint4*>(src + i), xa, (bf16*)nullptr);
+  unpack16(*reinterpret_cast<const uint4*>(src + i + half), xb, (bf16*)nullptr);
+  bf16* dst;
+  if (head < Hq + Hkv) {
+    const int64_t pos = positions[t];
+    if (pos < 0 || pos >= max_pos) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) oa[e] = ob[e] = __builtin_nanf("");
+      if (error_flag) *error_flag = 1;
+    } else {
+      const float4* cr = reinterpret_cast<const float4*>(cos_tab + pos * D + i);
+      const float4* sr = reinterpret_cast<const float4*>(sin_tab + pos * D + i);
+      const float4 c0 = cr[0], c1 = cr[1], s0 = sr[0], s1 = sr[1];
+      const float4 c2 = cr[half / 4], c3 = cr[half / 4 + 1], s2 = sr[half / 4], s3 = sr[half / 4 + 1];
+      const float ca[8] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w};
+      const float sa[8] = {s0.x, s0.y, s0.z, s0.w, s1.x, s1.y, s1.z, s1.w};
+      const float cb[8] = {c2.x, c2.y, c2.z, c2.w, c3.x, c3.y, c3.z, c3.w};
+      const float sb[8] = {s2.x, s2.y, s2.z, s2.w, s3.x, s3.y, s3.z, s3.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        oa[e] = add_rn(mul_rn(xa[e], ca[e]), -mul_rn(xb[e], sa[e]));
+        ob[e] = add_rn(mul_rn(xb[e], cb[e]), mul_rn(xa[e], sb[e]));
+      }
+    }
+    dst = head < Hq ? q_out + (n * Hq + head) * D : k_cache + ((b * Hkv + (head - Hq)) * S + cache_len + t) * D;
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      oa[e] = xa[e];
+      ob[e] = xb[e];
+    }
+    dst = v_cache + ((b * Hkv + (head - Hq - Hkv)) * S + cache_len + t) * D;
+  }
+  store8_bf16(dst + i, oa);
+  store8_bf16(dst + i + half, ob);
+}
+
 int launch_rope_kv_write(hipStream_t st, int dtype, const void* qkv, int64_t ld_qkv, void* q_out, void* k_cache,
                          void* v_cache, const float* cos_tab, const float* sin_tab, const int64_t* positions,
                          int64_t max_pos, int64_t B, int64_t T_, int64_t Hq, int64_t Hkv, int64_t D, int64_t S,
                          int64_t cache_len, int32_t* error_flag, const StepState* state, int layer) {
   const int64_t n = B * T_ * (Hq + 2 * Hkv) * (D / 2);
   if (n == 0) return MINITP_OK;
+  if (dtype == MINITP_BF16 && D % 16 == 0 && ld_qkv % 8 == 0 && aligned16(qkv) && aligned16(cos_tab) &&
+      aligned16(sin_tab)) {
+    rope_kv_write8_kernel<<<(unsigned)cdiv(n / 8, 256), 256, 0, st>>>(
+        (const bf16*)qkv, ld_qkv, (bf16*)q_out, (bf16*)k_cache, (bf16*)v_cache, cos_tab, sin_tab, positions, max_pos,
+        B, T_, Hq, Hkv, D, S, cache_len, error_flag, state, layer);
+    MINITP_LAUNCH_CHECK();
+    return MINITP_OK;
+  }
   const unsigned grid = (unsigned)cdiv(n, 256);
   if (dtype == MINITP_F32)
     rope_kv_write_kernel<float><<<grid, 256, 0, st>>>((const float*)qkv, ld_qkv, (float*)q_out, (float*)k_cache,
