@@ -15,6 +15,7 @@ Reported beside the headline tok/s:
     launch time, and its measured HBM traffic per launch when the committed
     rocprofv3 counter summary is present;
   * TTFT (prefill start -> first token selected) p50 / mean, TPOT percentiles;
+    the prefill is generate_greedy's: the LM head on the last position only;
   * the CPU baseline: the oracle restatement of the reference's TP=1 path on
     the host cores, bf16, over a bounded sample of the same workload.
 """
@@ -116,7 +117,7 @@ def secondary(args):
         else:
             ttfts = []
             for _ in range(4):
-                st = GenerationState(model, prompt, 1)
+                st = GenerationState(model, prompt, 1, prefill_logits="last")
                 a, b = torch.cuda.Event(True), torch.cuda.Event(True)
                 a.record()
                 st.select_next(st.prefill())
@@ -139,7 +140,7 @@ def decode_run(model, prompt, n_steps, record_steps=False):
 
     from minitp.generation import GenerationState
 
-    st = GenerationState(model, prompt, n_steps + 1)
+    st = GenerationState(model, prompt, n_steps + 1, prefill_logits="last")
     e_t0, e_t1 = torch.cuda.Event(True), torch.cuda.Event(True)
     e_t0.record()
     logits = st.prefill()
@@ -337,7 +338,7 @@ def main(argv=None):
         for _ in range(args.ttft_iters):
             from minitp.generation import GenerationState
 
-            st = GenerationState(model, prompt, 1)
+            st = GenerationState(model, prompt, 1, prefill_logits="last")
             a, b = torch.cuda.Event(True), torch.cuda.Event(True)
             a.record()
             st.select_next(st.prefill())

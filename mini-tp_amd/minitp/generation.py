@@ -20,6 +20,12 @@ cursor and ``kv.seq_len`` are the reference's.
 
 The decode logits buffer [B, 1, V] is reused: logits returned by one
 ``decode_step`` are overwritten by the next.
+
+``prefill`` returns every prompt position's logits [B, T, V], as the
+reference does, unless the state was made with ``prefill_logits="last"``:
+then [B, 1, V] of the last position, the only row a token is picked from.
+``generate_greedy`` uses that form, which skips T - 1 of the T LM-head rows
+of the prompt (the greedy ids are the same).
 """
 
 from __future__ import annotations
@@ -62,8 +68,12 @@ class GenerationState:
     """KV cache + positions buffer + output buffer (generation.py:70-130)."""
 
     def __init__(self, model: TPQwen2ForCausalLM, input_ids: torch.Tensor, max_new_tokens: int,
-                 kv: KVCache | None = None, distributed_argmax: bool = True, kv_init: str = "empty") -> None:
+                 kv: KVCache | None = None, distributed_argmax: bool = True, kv_init: str = "empty",
+                 prefill_logits: str = "all") -> None:
+        if prefill_logits not in ("all", "last"):
+            raise ValueError(f"prefill_logits must be 'all' or 'last', got {prefill_logits!r}")
         self.model = model
+        self.prefill_logits = prefill_logits
         self.distributed_argmax = distributed_argmax
         b, t = input_ids.shape
         self.prompt_len = t
@@ -120,7 +130,8 @@ class GenerationState:
             return self.model(ids, positions=positions, kv_cache=self.kv)
         self._check_position(self.prompt_len - 1)
         col = self._next_column()
-        logits = self.model._native(ids, positions, self.kv, next_tok=col, eos=self._eos_args())
+        logits = self.model._native(ids, positions, self.kv, next_tok=col, eos=self._eos_args(),
+                                    last_only=self.prefill_logits == "last")
         self._last_logits, self._last_tok = logits, col
         return logits
 
@@ -164,7 +175,7 @@ def generate_greedy(model: TPQwen2ForCausalLM, input_ids: torch.Tensor, max_new_
     the first step where every row has produced EOS when ``early_stop``;
     exactly prompt + max_new_tokens columns otherwise."""
     state = GenerationState(model, input_ids, max_new_tokens, kv=kv, distributed_argmax=distributed_argmax,
-                            kv_init=kv_init)
+                            kv_init=kv_init, prefill_logits="last")
     b = input_ids.shape[0]
     if early_stop and eos_token_id is not None and state._native and max_new_tokens > 0:
         return _generate_device_eos(state, eos_token_id, max_new_tokens)

@@ -194,7 +194,11 @@ class TPQwen2ForCausalLM(nn.Module):
         return self._prog
 
     def _native(self, input_ids: torch.Tensor, positions: torch.Tensor, kv_cache: KVCache | None,
-                next_tok: torch.Tensor | None = None, eos: tuple | None = None) -> torch.Tensor:
+                next_tok: torch.Tensor | None = None, eos: tuple | None = None,
+                last_only: bool = False) -> torch.Tensor:
+        """Whole-model forward on the native program. Logits [B, T, V], or
+        [B, 1, V] of the last position when ``last_only`` (one LM-head row per
+        sequence instead of T)."""
         prog = self.program()
         b, t = input_ids.shape
         dev = prog.device
@@ -207,10 +211,11 @@ class TPQwen2ForCausalLM(nn.Module):
             a = self.model.layers[0].self_attn
             kv = KVCache(self.cfg.num_hidden_layers, b, a.kv_heads_local, self.cfg.head_dim, t, prog.dtype, dev)
         kv.check_room(t)
-        logits = torch.empty(b, t, self.cfg.vocab_size, dtype=prog.dtype, device=dev)
+        all_rows = t > 1 and not last_only
+        logits = torch.empty(b, t if all_rows else 1, self.cfg.vocab_size, dtype=prog.dtype, device=dev)
         ws = prog.forward_ws(b * t, b, kv.max_seq_len)
         step = N.Qwen2Step(ids.data_ptr(), ids.stride(0), pos.data_ptr(), b, t, kv.seq_len, kv.k_buf.data_ptr(),
-                           kv.v_buf.data_ptr(), kv.max_seq_len, logits.data_ptr(), 1 if t > 1 else 0,
+                           kv.v_buf.data_ptr(), kv.max_seq_len, logits.data_ptr(), 1 if all_rows else 0,
                            N.ptr(next_tok), next_tok.stride(0) if next_tok is not None else 0, ws.data_ptr(),
                            ws.numel(), *(eos or (None, 0, 0, None)))
         N.check(N.lib().minitp_qwen2_forward(prog.handle, N.stream(), ctypes.byref(step)), "qwen2_forward")
