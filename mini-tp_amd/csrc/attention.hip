@@ -640,6 +640,215 @@ __global__ __launch_bounds__(PW * 64) void prefill_attn_mfma_kernel(const bf16* 
         make_uint2(pack_bf16x2(o[dn][0] / l, o[dn][1] / l), pack_bf16x2(o[dn][2] / l, o[dn][3] / l));
 }
 
+// Long-prompt prefill on matrix cores (bf16, D % 32 == 0). Block = one
+// 128-query tile of one head; its four waves own 32 queries each, as two
+// 16-query strips that share every K and V operand read from LDS (half the
+// LDS traffic of one strip per wave). Products transposed as in
+// prefill_attn_mfma_kernel (S^T = K Q^T, O^T = V^T P^T, 16x16x32 MFMA), with
+//  * K / V tiles of 64 keys double-buffered in LDS: one barrier per tile, the
+//    next tile's global loads in flight during the current tile's math;
+//  * the causal mask applied only on tiles that cross a query of the wave,
+//    the 1/sqrt(D) scale folded into the exponent (exp2(s * c - m)), and the
+//    running-sum / output rescale skipped when no lane's maximum moved;
+//  * query tiles dispatched last (longest) first, and the heads of one KV
+//    group kept on one XCD when the head count allows (blocks go to the
+//    eight XCDs round-robin by linear id, and each XCD has its own L2).
+template <int D>
+__global__ __launch_bounds__(256, 2) void prefill_attn_fa_kernel(const bf16* q, const bf16* kc, const bf16* vc, bf16* out,
+                                                              AttnShape s, int64_t cache_len, float scale) {
+  typedef float float4_t __attribute__((ext_vector_type(4)));
+  typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+  constexpr int NS = 2;              // 16-query strips per wave
+  constexpr int PQ = 4 * 16 * NS;    // queries per block
+  constexpr int KT = 64, KB = KT / 16, KS = D / 16, D32 = D / 32, PPRW = D / 8;
+  constexpr int KROW = D * 2 + 16, VROW = KT * 2 + 16;
+  constexpr int KBYTES = KT * KROW, STAGE = KBYTES + D * VROW;
+  __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
+  const int G = s.Hq / s.Hkv;
+  int bh = blockIdx.x;
+  if (gridDim.x % 8 == 0) bh = (blockIdx.x % 8) * (gridDim.x / 8) + blockIdx.x / 8;  // XCD c: a run of heads
+  const int b = bh / s.Hq, h = bh % s.Hq, g = h / G;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int lr = lane % 16, lq = lane / 16;
+  const int64_t qt = (int64_t)gridDim.y - 1 - blockIdx.y;
+  const int64_t tw = qt * PQ + wave * 16 * NS;  // first query of this wave
+  const bf16* kbase = kc + ((int64_t)b * s.Hkv + g) * s.S * D;
+  const bf16* vbase = vc + ((int64_t)b * s.Hkv + g) * s.S * D;
+  const float sl2 = scale * 1.4426950408889634f;
+
+  bf16x8_t qa[NS][D32];
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    const int64_t t = tw + 16 * st + lr;
+    const bf16* qrow = q + (((int64_t)b * s.T + (t < s.T ? t : 0)) * s.Hq + h) * D;
+#pragma unroll
+    for (int kb = 0; kb < D32; ++kb) {
+      const uint4 v = t < s.T ? *(const uint4*)(qrow + kb * 32 + 8 * lq) : make_uint4(0, 0, 0, 0);
+      qa[st][kb] = __builtin_bit_cast(bf16x8_t, v);
+    }
+  }
+  float4_t o[NS][KS];
+  float m[NS], lsum[NS];
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    m[st] = -__builtin_inff();
+    lsum[st] = 0.f;
+#pragma unroll
+    for (int dn = 0; dn < KS; ++dn) o[st][dn] = float4_t{0.f, 0.f, 0.f, 0.f};
+  }
+  const int64_t tb_last = std::min<int64_t>(qt * PQ + PQ - 1, s.T - 1);
+  const int64_t key_end = cache_len + tb_last + 1;
+  const int64_t ntiles = cdiv(key_end, (int64_t)KT);
+
+  // staging as in prefill_attn_mfma_kernel: thread = (KQ keys, one 16-byte column)
+  constexpr int NPC = KT * PPRW;
+  constexpr int KQ = NPC >= 256 ? NPC / 256 : 1;
+  const int kq = tid / PPRW, pc = tid % PPRW;
+  const bool stager = tid < NPC / KQ;
+  const uint32_t kv_bytes = (uint32_t)(key_end * D * 2);
+  const __amdgpu_buffer_rsrc_t krs = attn_rsrc(kbase, kv_bytes), vrs = attn_rsrc(vbase, kv_bytes);
+  uint4 kr[KQ], vr[KQ];
+  auto load_tile = [&](int64_t k0) {
+#pragma unroll
+    for (int u = 0; u < KQ; ++u) {
+      const int64_t key = k0 + kq * KQ + u;
+      const uint32_t off = stager && key < key_end ? (uint32_t)((key * D + pc * 8) * 2) : kv_bytes;
+      kr[u] = attn_load16(krs, off);
+      vr[u] = attn_load16(vrs, off);
+    }
+  };
+  auto store_tile = [&](char* Ks) {
+    if (!stager) return;
+    char* Vt = Ks + KBYTES;
+#pragma unroll
+    for (int u = 0; u < KQ; ++u) *(uint4*)(Ks + (kq * KQ + u) * KROW + pc * 16) = kr[u];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      uint16_t hv[KQ];
+#pragma unroll
+      for (int u = 0; u < KQ; ++u) {
+        const uint32_t wv = e < 2 ? vr[u].x : e < 4 ? vr[u].y : e < 6 ? vr[u].z : vr[u].w;
+        hv[u] = (uint16_t)(e & 1 ? wv >> 16 : wv);
+      }
+      char* dst = Vt + (pc * 8 + e) * VROW + kq * KQ * 2;
+      if constexpr (KQ == 4) {
+        *(uint2*)dst = make_uint2(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
+      } else if constexpr (KQ == 2) {
+        *(uint32_t*)dst = hv[0] | ((uint32_t)hv[1] << 16);
+      } else {
+#pragma unroll
+        for (int u = 0; u < KQ; ++u) *(uint16_t*)(dst + 2 * u) = hv[u];
+      }
+    }
+  };
+
+  load_tile(0);
+  store_tile(lds);
+  if (ntiles > 1) load_tile(KT);
+  __syncthreads();
+  for (int64_t it = 0; it < ntiles; ++it) {
+    const int64_t k0 = it * KT;
+    const char* Ks = lds + (it & 1) * STAGE;
+    const char* Vt = Ks + KBYTES;
+    if (tw < s.T && k0 <= cache_len + tw + 16 * NS - 1) {  // the wave sees part of the tile
+      float4_t acc[NS][KB];
+#pragma unroll
+      for (int kbk = 0; kbk < KB; ++kbk) {
+#pragma unroll
+        for (int st = 0; st < NS; ++st) acc[st][kbk] = float4_t{0.f, 0.f, 0.f, 0.f};
+        const char* krow = Ks + (kbk * 16 + lr) * KROW;
+#pragma unroll
+        for (int kb = 0; kb < D32; ++kb) {
+          const bf16x8_t kv = __builtin_bit_cast(bf16x8_t, *(const uint4*)(krow + (kb * 32 + 8 * lq) * 2));
+#pragma unroll
+          for (int st = 0; st < NS; ++st)
+            acc[st][kbk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qa[st][kb], acc[st][kbk], 0, 0, 0);
+        }
+      }
+      if (k0 + KT - 1 > cache_len + tw) {  // some key of the tile lies past some query of the wave
+#pragma unroll
+        for (int st = 0; st < NS; ++st) {
+          const int64_t qpos = cache_len + tw + 16 * st + lr;
+#pragma unroll
+          for (int kbk = 0; kbk < KB; ++kbk)
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+              if (k0 + kbk * 16 + 4 * lq + i > qpos) acc[st][kbk][i] = -__builtin_inff();
+        }
+      }
+      uint2 pk[NS][KB];
+#pragma unroll
+      for (int st = 0; st < NS; ++st) {
+        // this lane's query: its 64 keys sit in lanes lr, lr + 16, + 32, + 48. Every
+        // query sees key 0 of tile 0, so the running maximum is finite from there on.
+        float mx = acc[st][0][0];
+#pragma unroll
+        for (int kbk = 0; kbk < KB; ++kbk)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) mx = fmaxf(mx, acc[st][kbk][i]);
+        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
+        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+        const float mn = fmaxf(m[st], mx * sl2);
+        const float alpha = __builtin_amdgcn_exp2f(m[st] - mn);
+        m[st] = mn;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+          lsum[st] *= alpha;
+#pragma unroll
+          for (int dn = 0; dn < KS; ++dn)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) o[st][dn][i] *= alpha;
+        }
+#pragma unroll
+        for (int kbk = 0; kbk < KB; ++kbk) {
+          float pr[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            pr[i] = __builtin_amdgcn_exp2f(fmaf(acc[st][kbk][i], sl2, -mn));
+            lsum[st] += pr[i];
+          }
+          pk[st][kbk] = make_uint2(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]));
+        }
+      }
+      // O^T += V^T P^T, one MFMA per 32 keys (k-index 8 lq + e = key 32 j + 4 lq + e,
+      // e < 4, or 32 j + 16 + 4 lq + e - 4: the same permutation in both operands)
+#pragma unroll
+      for (int j = 0; j < KB / 2; ++j) {
+        bf16x8_t pb[NS];
+#pragma unroll
+        for (int st = 0; st < NS; ++st)
+          pb[st] = __builtin_bit_cast(bf16x8_t, make_uint4(pk[st][2 * j].x, pk[st][2 * j].y, pk[st][2 * j + 1].x,
+                                                           pk[st][2 * j + 1].y));
+#pragma unroll
+        for (int dn = 0; dn < KS; ++dn) {
+          const char* vrow = Vt + (dn * 16 + lr) * VROW;
+          const uint2 v0 = *(const uint2*)(vrow + (32 * j + 4 * lq) * 2);
+          const uint2 v1 = *(const uint2*)(vrow + (32 * j + 16 + 4 * lq) * 2);
+          const bf16x8_t va = __builtin_bit_cast(bf16x8_t, make_uint4(v0.x, v0.y, v1.x, v1.y));
+#pragma unroll
+          for (int st = 0; st < NS; ++st)
+            o[st][dn] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va, pb[st], o[st][dn], 0, 0, 0);
+        }
+      }
+    }
+    if (it + 1 < ntiles) store_tile(lds + ((it + 1) & 1) * STAGE);  // that buffer was last read before the previous barrier
+    __syncthreads();
+    if (it + 2 < ntiles) load_tile((it + 2) * KT);
+  }
+#pragma unroll
+  for (int st = 0; st < NS; ++st) {
+    float l = lsum[st];
+    l += __shfl_xor(l, 16, 64);
+    l += __shfl_xor(l, 32, 64);
+    const int64_t t = tw + 16 * st + lr;
+    if (t >= s.T) continue;
+    bf16* orow = out + (((int64_t)b * s.T + t) * s.Hq + h) * D;
+#pragma unroll
+    for (int dn = 0; dn < KS; ++dn)
+      *(uint2*)(orow + dn * 16 + 4 * lq) = make_uint2(pack_bf16x2(o[st][dn][0] / l, o[st][dn][1] / l),
+                                                      pack_bf16x2(o[st][dn][2] / l, o[st][dn][3] / l));
+  }
+}
+
 template <typename T, int D, int HP>
 int decode_launch(hipStream_t st, DecodeArgs& a, int nsplit) {
   const int G = a.s.Hq / a.s.Hkv;
@@ -687,7 +896,11 @@ int prefill_dispatch(hipStream_t st, const void* q, const void* k, const void* v
   if constexpr (sizeof(T) == 2) {
     // 128-query blocks (eight strips share each staged K / V tile) once they
     // fill the chip; 64-query blocks for short prompts
-    if ((int64_t)s.B * s.Hq * cdiv(s.T, 128) >= 512)
+    if (D % 32 == 0 && (int64_t)s.B * s.Hq * cdiv(s.T, 128) >= 512)
+      hipLaunchKernelGGL((prefill_attn_fa_kernel<D % 32 == 0 ? D : 32>), dim3(s.B * s.Hq, (unsigned)cdiv(s.T, 128)),
+                         dim3(256), 0, st, (const bf16*)q, (const bf16*)k, (const bf16*)v, (bf16*)out, s, cache_len,
+                         scale);
+    else if ((int64_t)s.B * s.Hq * cdiv(s.T, 128) >= 512)
       hipLaunchKernelGGL((prefill_attn_mfma_kernel<D, 8>), dim3(s.B * s.Hq, (unsigned)cdiv(s.T, 128)), dim3(512), 0,
                          st, (const bf16*)q, (const bf16*)k, (const bf16*)v, (bf16*)out, s, cache_len, scale);
     else

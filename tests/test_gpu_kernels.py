@@ -340,11 +340,14 @@ def test_prefill_attention_causal_bf16(t, cache_len, hq, hkv, d):
     assert (got.double() - ref).abs().max().item() < 3e-2
 
 
-@pytest.mark.parametrize("b,t,cache_len,hq,hkv,d", [(2, 1200, 37, 28, 4, 128), (4, 1200, 100, 14, 2, 64)])
+@pytest.mark.parametrize("b,t,cache_len,hq,hkv,d", [(2, 1200, 37, 28, 4, 128), (4, 1200, 100, 14, 2, 64),
+                                                    (5, 1100, 0, 12, 3, 128), (4, 1100, 64, 16, 16, 32)])
 def test_prefill_attention_causal_bf16_long(b, t, cache_len, hq, hkv, d):
-    """Prompts long enough for the 128-query blocks (eight strips sharing each
-    staged K / V tile), with a key offset and the rows past the keys
-    poisoned; same bar as the short cases."""
+    """Prompts long enough for the long-prompt kernel (128-query blocks of
+    two-strip waves, double-buffered K / V tiles), with key offsets that do
+    and do not fall on a strip boundary, head counts with and without the
+    per-XCD head grouping (B * Hq a multiple of 8 or not), and the rows past
+    the keys poisoned; same bar as the short cases."""
     s = cache_len + t + 3
     g = torch.Generator().manual_seed(t + d)
     q = torch.randn(b, t, hq, d, generator=g).bfloat16()
