@@ -640,6 +640,23 @@ __global__ __launch_bounds__(PW * 64) void prefill_attn_mfma_kernel(const bf16* 
         make_uint2(pack_bf16x2(o[dn][0] / l, o[dn][1] / l), pack_bf16x2(o[dn][2] / l, o[dn][3] / l));
 }
 
+// Maximum / sum over lanes l, l ^ 16, l ^ 32, l ^ 48 on gfx950's permlane
+// swaps (VALU, no LDS round trip): with both operands equal, a 16-swap leaves
+// lane l's value in one result and lane l ^ 16's in the other, a 32-swap
+// likewise for l ^ 32.
+__device__ __forceinline__ float quad_rows_max(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float quad_rows_sum(float v) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Long-prompt prefill on matrix cores (bf16, D % 32 == 0). Block = one
 // 128-query tile of one head; its four waves own 32 queries each, as two
 // 16-query strips that share every K and V operand read from LDS (half the
@@ -659,9 +676,10 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_fa_kernel(const bf16* q, 
   typedef float float4_t __attribute__((ext_vector_type(4)));
   typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
   constexpr int NS = 2;              // 16-query strips per wave
+  constexpr float RESCALE_SLACK = 8.f;
   constexpr int PQ = 4 * 16 * NS;    // queries per block
   constexpr int KT = 64, KB = KT / 16, KS = D / 16, D32 = D / 32, PPRW = D / 8;
-  constexpr int KROW = D * 2 + 16, VROW = KT * 2 + 16;
+  constexpr int KROW = D * 2 + 16, VROW = KT * 2 + 8;
   constexpr int KBYTES = KT * KROW, STAGE = KBYTES + D * VROW;
   __shared__ __attribute__((aligned(16))) char lds[2 * STAGE];
   const int G = s.Hq / s.Hkv;
@@ -700,25 +718,30 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_fa_kernel(const bf16* q, 
   const int64_t key_end = cache_len + tb_last + 1;
   const int64_t ntiles = cdiv(key_end, (int64_t)KT);
 
-  // staging as in prefill_attn_mfma_kernel: thread = (KQ keys, one 16-byte column)
+  // Staging: a thread loads KQ keys of one 16-byte column of K and of V. K
+  // columns go to consecutive lanes (whole rows per load instruction, stored
+  // as they are); V keys go to consecutive lanes, so that the transposed
+  // writes of one dim by 16 lanes fill one contiguous 128-byte run of a Vt row
+  // (no bank conflicts), at the price of 64-byte row segments per load.
   constexpr int NPC = KT * PPRW;
   constexpr int KQ = NPC >= 256 ? NPC / 256 : 1;
   const int kq = tid / PPRW, pc = tid % PPRW;
-  const bool stager = tid < NPC / KQ;
+  const int kqv = tid % (KT / KQ), pcv = tid / (KT / KQ);
+  static_assert(NPC / KQ == 256, "every thread stages");
+  // pieces of keys past key_end lie past the buffer's size and read as zeros
   const uint32_t kv_bytes = (uint32_t)(key_end * D * 2);
   const __amdgpu_buffer_rsrc_t krs = attn_rsrc(kbase, kv_bytes), vrs = attn_rsrc(vbase, kv_bytes);
+  const uint32_t koff = (uint32_t)((kq * KQ * D + pc * 8) * 2), voff = (uint32_t)((kqv * KQ * D + pcv * 8) * 2);
   uint4 kr[KQ], vr[KQ];
   auto load_tile = [&](int64_t k0) {
+    const uint32_t base = (uint32_t)(k0 * D * 2);
 #pragma unroll
     for (int u = 0; u < KQ; ++u) {
-      const int64_t key = k0 + kq * KQ + u;
-      const uint32_t off = stager && key < key_end ? (uint32_t)((key * D + pc * 8) * 2) : kv_bytes;
-      kr[u] = attn_load16(krs, off);
-      vr[u] = attn_load16(vrs, off);
+      kr[u] = attn_load16(krs, base + koff + u * D * 2);
+      vr[u] = attn_load16(vrs, base + voff + u * D * 2);
     }
   };
   auto store_tile = [&](char* Ks) {
-    if (!stager) return;
     char* Vt = Ks + KBYTES;
 #pragma unroll
     for (int u = 0; u < KQ; ++u) *(uint4*)(Ks + (kq * KQ + u) * KROW + pc * 16) = kr[u];
@@ -730,7 +753,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_fa_kernel(const bf16* q, 
         const uint32_t wv = e < 2 ? vr[u].x : e < 4 ? vr[u].y : e < 6 ? vr[u].z : vr[u].w;
         hv[u] = (uint16_t)(e & 1 ? wv >> 16 : wv);
       }
-      char* dst = Vt + (pc * 8 + e) * VROW + kq * KQ * 2;
+      char* dst = Vt + (pcv * 8 + e) * VROW + kqv * KQ * 2;
       if constexpr (KQ == 4) {
         *(uint2*)dst = make_uint2(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
       } else if constexpr (KQ == 2) {
@@ -754,27 +777,28 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_fa_kernel(const bf16* q, 
       float4_t acc[NS][KB];
 #pragma unroll
       for (int kbk = 0; kbk < KB; ++kbk) {
-#pragma unroll
-        for (int st = 0; st < NS; ++st) acc[st][kbk] = float4_t{0.f, 0.f, 0.f, 0.f};
         const char* krow = Ks + (kbk * 16 + lr) * KROW;
 #pragma unroll
         for (int kb = 0; kb < D32; ++kb) {
           const bf16x8_t kv = __builtin_bit_cast(bf16x8_t, *(const uint4*)(krow + (kb * 32 + 8 * lq) * 2));
 #pragma unroll
           for (int st = 0; st < NS; ++st)
-            acc[st][kbk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kv, qa[st][kb], acc[st][kbk], 0, 0, 0);
+            acc[st][kbk] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+                kv, qa[st][kb], kb == 0 ? float4_t{0.f, 0.f, 0.f, 0.f} : acc[st][kbk], 0, 0, 0);
         }
       }
       if (k0 + KT - 1 > cache_len + tw) {  // some key of the tile lies past some query of the wave
+        __asm__ volatile("");                // (a branch, not selects on every tile)
+        // key k0 + 16 kbk + 4 lq + i is visible to query tw + 16 st + lr when
+        // 16 kbk + i <= cache_len + tw - k0 + 16 st + lr - 4 lq
+        const int rel = (int)(cache_len + tw - k0) + lr - 4 * lq;
 #pragma unroll
-        for (int st = 0; st < NS; ++st) {
-          const int64_t qpos = cache_len + tw + 16 * st + lr;
+        for (int st = 0; st < NS; ++st)
 #pragma unroll
           for (int kbk = 0; kbk < KB; ++kbk)
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-              if (k0 + kbk * 16 + 4 * lq + i > qpos) acc[st][kbk][i] = -__builtin_inff();
-        }
+              if (16 * kbk + i > rel + 16 * st) acc[st][kbk][i] = -__builtin_inff();
       }
       uint2 pk[NS][KB];
 #pragma unroll
@@ -786,12 +810,15 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_fa_kernel(const bf16* q, 
         for (int kbk = 0; kbk < KB; ++kbk)
 #pragma unroll
           for (int i = 0; i < 4; ++i) mx = fmaxf(mx, acc[st][kbk][i]);
-        mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-        mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-        const float mn = fmaxf(m[st], mx * sl2);
-        const float alpha = __builtin_amdgcn_exp2f(m[st] - mn);
-        m[st] = mn;
-        if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+        mx = quad_rows_max(mx) * sl2;
+        // The reference point m moves only when some lane's maximum passes it
+        // by more than RESCALE_SLACK (base 2): until then the probabilities
+        // exp2(s - m) stay below 2^RESCALE_SLACK, and O and the sum keep their
+        // scale (the result is the same up to rounding, fewer rescales).
+        if (__builtin_amdgcn_ballot_w64(mx > m[st] + RESCALE_SLACK)) {
+          const float mn = fmaxf(m[st], mx);
+          const float alpha = __builtin_amdgcn_exp2f(m[st] - mn);
+          m[st] = mn;
           lsum[st] *= alpha;
 #pragma unroll
           for (int dn = 0; dn < KS; ++dn)
@@ -803,7 +830,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_fa_kernel(const bf16* q, 
           float pr[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            pr[i] = __builtin_amdgcn_exp2f(fmaf(acc[st][kbk][i], sl2, -mn));
+            pr[i] = __builtin_amdgcn_exp2f(fmaf(acc[st][kbk][i], sl2, -m[st]));
             lsum[st] += pr[i];
           }
           pk[st][kbk] = make_uint2(pack_bf16x2(pr[0], pr[1]), pack_bf16x2(pr[2], pr[3]));
@@ -836,9 +863,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_fa_kernel(const bf16* q, 
   }
 #pragma unroll
   for (int st = 0; st < NS; ++st) {
-    float l = lsum[st];
-    l += __shfl_xor(l, 16, 64);
-    l += __shfl_xor(l, 32, 64);
+    const float l = quad_rows_sum(lsum[st]);
     const int64_t t = tw + 16 * st + lr;
     if (t >= s.T) continue;
     bf16* orow = out + (((int64_t)b * s.T + t) * s.Hq + h) * D;
