@@ -452,7 +452,7 @@ __global__ __launch_bounds__(PW * 64) void prefill_attn_mfma_kernel(const bf16* 
   constexpr int KS = D / 16;        // 16-dim steps of a score, and 16-dim output blocks
   constexpr int PPRW = D / 8;       // 16-byte pieces per K / V row
   constexpr int KROW = D * 2 + 16;  // LDS bytes per K row (padded)
-  constexpr int VROW = KT * 2 + 16; // LDS bytes per transposed V row (one dim)
+  constexpr int VROW = KT * 2 + 8;  // LDS bytes per transposed V row (one dim)
   __shared__ __attribute__((aligned(16))) char Ks[KT * KROW];
   __shared__ __attribute__((aligned(16))) char Vt[D * VROW];
   const int G = s.Hq / s.Hkv;
@@ -502,6 +502,9 @@ __global__ __launch_bounds__(PW * 64) void prefill_attn_mfma_kernel(const bf16* 
   constexpr int NPC = KT * PPRW;                // 16-byte pieces per matrix per tile
   constexpr int KQ = NPC >= PW * 64 ? NPC / (PW * 64) : 1;
   const int kq = tid / PPRW, pc = tid % PPRW;
+  // V by key-consecutive lanes: the transposed writes of one dim by 16 lanes
+  // fill one contiguous run of a Vt row (no bank conflicts)
+  const int kqv = tid % (KT / KQ), pcv = tid / (KT / KQ);
   const bool stager = tid < NPC / KQ;
   const uint32_t kv_bytes = (uint32_t)(key_end * D * 2);
   const __amdgpu_buffer_rsrc_t krs = attn_rsrc(kbase, kv_bytes), vrs = attn_rsrc(vbase, kv_bytes);
@@ -509,10 +512,9 @@ __global__ __launch_bounds__(PW * 64) void prefill_attn_mfma_kernel(const bf16* 
   auto load_tile = [&](int64_t k0) {
 #pragma unroll
     for (int u = 0; u < KQ; ++u) {
-      const int64_t key = k0 + kq * KQ + u;
-      const uint32_t off = stager && key < key_end ? (uint32_t)((key * D + pc * 8) * 2) : kv_bytes;
-      kr[u] = attn_load16(krs, off);
-      vr[u] = attn_load16(vrs, off);
+      const int64_t key = k0 + kq * KQ + u, keyv = k0 + kqv * KQ + u;
+      kr[u] = attn_load16(krs, stager && key < key_end ? (uint32_t)((key * D + pc * 8) * 2) : kv_bytes);
+      vr[u] = attn_load16(vrs, stager && keyv < key_end ? (uint32_t)((keyv * D + pcv * 8) * 2) : kv_bytes);
     }
   };
   auto store_tile = [&]() {
@@ -527,7 +529,7 @@ __global__ __launch_bounds__(PW * 64) void prefill_attn_mfma_kernel(const bf16* 
         const uint32_t wv = e < 2 ? vr[u].x : e < 4 ? vr[u].y : e < 6 ? vr[u].z : vr[u].w;
         hv[u] = (uint16_t)(e & 1 ? wv >> 16 : wv);
       }
-      char* dst = Vt + (pc * 8 + e) * VROW + kq * KQ * 2;
+      char* dst = Vt + (pcv * 8 + e) * VROW + kqv * KQ * 2;
       if constexpr (KQ == 4) {
         *(uint2*)dst = make_uint2(hv[0] | ((uint32_t)hv[1] << 16), hv[2] | ((uint32_t)hv[3] << 16));
       } else if constexpr (KQ == 2) {
