@@ -68,6 +68,27 @@ def test_cpu_forward_refuses_instead_of_falling_back():
         m(torch.zeros(1, 3, dtype=torch.long))
 
 
+def test_generation_state_prefill_logits_option():
+    """prefill_logits is checked before anything is allocated; 'last' is the
+    form generate_greedy uses, 'all' the reference's default."""
+    from minitp.config import ModelConfig
+    from minitp.distributed.context import ParallelContext
+    from minitp.generation import GenerationState
+    from minitp.layer import TPQwen2ForCausalLM
+
+    cfg = ModelConfig(64, 128, 1, 4, 2, 16, 100, 1e-6, 1e4, 64, True)
+    m = TPQwen2ForCausalLM(cfg, ParallelContext(0, 0, 1, 0, 1, torch.device("cpu"), None))
+    ids = torch.zeros(1, 3, dtype=torch.long)
+    for bad in ("none", "LAST", None):
+        with pytest.raises(ValueError, match="prefill_logits"):
+            GenerationState(m, ids, 2, prefill_logits=bad)
+    assert GenerationState(m, ids, 2).prefill_logits == "all"
+    st = GenerationState(m, ids, 2, prefill_logits="last")
+    assert st.prefill_logits == "last"
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        st.prefill()
+
+
 def test_kv_cache_host_validation():
     from minitp.kv_cache import KVCache
 
