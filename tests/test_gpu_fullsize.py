@@ -1,0 +1,97 @@
+"""The 7B prefill workload at its full size (4 x 4096 tokens, bf16), checked
+through properties that do not need the oracle to run at that size.
+
+The model is the Qwen2.5-7B layer shape with 2 layers and the untied
+152,064-row head (the oracle covers the same shapes at small sizes). At 4 x
+4096 the prompt runs the long-prompt attention kernel, hipBLASLt GEMMs at
+M = 16,384 and the 16-byte elementwise kernels, so these properties exercise
+exactly the full-size path:
+
+* the whole-prompt prefill's last-position logits equal those of a prefill of
+  the first 4,095 tokens followed by one decode step of the last token (the
+  decode attention and GEMV path over the 4,095 cached rows);
+* a prefill in two chunks of 2,048 (the second attending over the first
+  through the cache offset, positions 2,048 .. 4,095 given explicitly) gives
+  the same last-position logits and the same cache rows as the whole prompt.
+
+Bars: the bf16 logit bar of the model tests (0.5 abs); for layer 0's cache
+rows a few bf16 steps (3e-2 + |value| / 32: the two prompts run the QKV GEMM
+at different M, whose algorithms round differently in the last bit), for
+layer 1's 0.125 abs (its inputs carry layer 0's rounding differences; values
+reach about 6). Every logit and cache row must be finite.
+"""
+
+import dataclasses
+
+import pytest
+import torch
+
+from tests.test_gpu_model import BF16_LOGIT_ATOL
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+B, T = 4, 4096
+
+
+@pytest.fixture(scope="module")
+def model_prompt():
+    from minitp import synthetic
+
+    cfg = dataclasses.replace(synthetic.QWEN7B, num_hidden_layers=2)
+    model = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device=DEV, seed=0)
+    prompt = synthetic.synthetic_prompt(cfg.vocab_size, B, T, seed=3, device=DEV)
+    yield model, prompt
+    del model
+    torch.cuda.empty_cache()
+
+
+def _whole(model, prompt):
+    from minitp.generation import GenerationState
+
+    st = GenerationState(model, prompt, 1, prefill_logits="last")
+    logits = st.prefill()[:, 0].float()
+    return logits, st.kv
+
+
+def test_full_prompt_last_row_equals_prefill_then_decode(model_prompt):
+    from minitp.generation import GenerationState
+
+    model, prompt = model_prompt
+    whole, _ = _whole(model, prompt)
+    st = GenerationState(model, prompt[:, :-1], 2, prefill_logits="last")
+    st.prefill()
+    tok = prompt[:, -1].contiguous()
+    pos = st.append(tok)
+    step = st.decode_step(tok, pos)[:, 0].float()
+    assert torch.isfinite(whole).all() and torch.isfinite(step).all()
+    err = (whole - step).abs().max().item()
+    print(f"4 x 4096: whole-prompt vs prefill(4095) + decode: max |logit diff| {err:.4f}")
+    assert err <= BF16_LOGIT_ATOL
+
+
+def test_two_chunk_prefill_equals_whole_prompt(model_prompt):
+    """Chunks through the model's forward with explicit positions (a T > 1
+    forward without them starts at position 0, as the reference's does)."""
+    from minitp.generation import make_kv_cache
+
+    model, prompt = model_prompt
+    whole, kv_whole = _whole(model, prompt)
+    kv = make_kv_cache(model, B, T + 1)
+    h = T // 2
+    with torch.inference_mode():
+        model(prompt[:, :h], positions=torch.arange(0, h, device=DEV), kv_cache=kv)
+        chunked = model(prompt[:, h:], positions=torch.arange(h, T, device=DEV), kv_cache=kv)[:, -1].float()
+    assert kv.seq_len == T
+    err = (whole - chunked).abs().max().item()
+    print(f"4 x 4096: whole vs 2 x 2048 chunks: max |logit diff| {err:.4f}")
+    assert torch.isfinite(chunked).all() and err <= BF16_LOGIT_ATOL
+    for i, (a, b) in enumerate(zip(kv_whole.k + kv_whole.v, kv.k + kv.v)):
+        ra, rb = a[:, :, :T].float(), b[:, :, :T].float()
+        assert torch.isfinite(rb).all()
+        d = (ra - rb).abs()
+        print(f"cache buffer {i}: max |row| {ra.abs().max().item():.3f}, max |diff| {d.max().item():.4f}, "
+              f"rows differing {(d > 0).float().mean().item():.5f}")
+        if i % len(kv.k) == 0:  # layer 0: its inputs are the same; GEMM rounding only
+            assert (d <= 3e-2 + ra.abs() / 32).all()
+        else:  # later layers also carry the earlier layers' rounding differences
+            assert d.max().item() <= 0.125
