@@ -2,7 +2,8 @@
 through properties that do not need the oracle to run at that size.
 
 The model is the Qwen2.5-7B layer shape with 2 layers and the untied
-152,064-row head (the oracle covers the same shapes at small sizes). At 4 x
+152,064-row head (the oracle covers the same shapes at small sizes); the last
+test does the same for the batch-32 decode workload's shapes. At 4 x
 4096 the prompt runs the long-prompt attention kernel, hipBLASLt GEMMs at
 M = 16,384 and the 16-byte elementwise kernels, so these properties exercise
 exactly the full-size path:
@@ -95,3 +96,24 @@ def test_two_chunk_prefill_equals_whole_prompt(model_prompt):
             assert (d <= 3e-2 + ra.abs() / 32).all()
         else:  # later layers also carry the earlier layers' rounding differences
             assert d.max().item() <= 0.125
+
+
+def test_batch32_long_prompt_last_row_equals_prefill_then_decode():
+    """The batch-32 decode workload's shapes (0.5B layers, 2 of them, 32 x 2048
+    bf16): the long-prompt attention at head dim 64 against the batched decode
+    path (GEMM path, decode attention split over the 2,047 cached rows)."""
+    from minitp import synthetic
+    from minitp.generation import GenerationState
+
+    cfg = dataclasses.replace(synthetic.QWEN05B, num_hidden_layers=2)
+    model = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device=DEV, seed=1)
+    prompt = synthetic.synthetic_prompt(cfg.vocab_size, 32, 2048, seed=5, device=DEV)
+    whole = GenerationState(model, prompt, 1, prefill_logits="last").prefill()[:, 0].float()
+    st = GenerationState(model, prompt[:, :-1], 2, prefill_logits="last")
+    st.prefill()
+    tok = prompt[:, -1].contiguous()
+    step = st.decode_step(tok, st.append(tok))[:, 0].float()
+    err = (whole - step).abs().max().item()
+    print(f"32 x 2048: whole-prompt vs prefill(2047) + decode: max |logit diff| {err:.4f}")
+    assert torch.isfinite(whole).all() and torch.isfinite(step).all() and err <= BF16_LOGIT_ATOL
+
