@@ -62,6 +62,9 @@ def parse(argv=None):
     ap.add_argument("--workload", default="q05b", choices=sorted(WORKLOADS),
                     help="q05b (default): the headline line; the others measure the remaining workloads "
                          "(one JSON line each, not the headline metric)")
+    ap.add_argument("--prefill-attention", type=int, default=0, metavar="ITERS",
+                    help="only time the causal prefill attention of the 7B 4 x 4096 prefill (q [4, 4096, 28, 128], "
+                         "4 KV heads, bf16) ITERS times after 3 warm-up calls, print one JSON line and exit")
     ap.add_argument("--dominant-only", action="store_true",
                     help="only launch the dominant kernel, eagerly (no graphs), once per layer 4 times over, and "
                          "exit: the workload of the --pmc byte-counter passes")
@@ -235,6 +238,32 @@ def measured_traffic():
         return None
 
 
+def prefill_attention(iters: int) -> None:
+    """The 7B 4 x 4096 prefill's attention alone (one layer's call), timed with
+    HIP events on the launch stream: the workload of the attention counter runs."""
+    import torch
+
+    from minitp import kernels as K
+
+    b, t, hq, hkv, d = 4, 4096, 28, 4, 128
+    g = torch.Generator(device="cuda").manual_seed(0)
+    q = torch.randn(b, t, hq, d, device="cuda", dtype=torch.bfloat16, generator=g)
+    kc = torch.randn(b, hkv, t, d, device="cuda", dtype=torch.bfloat16, generator=g)
+    vc = torch.randn(b, hkv, t, d, device="cuda", dtype=torch.bfloat16, generator=g)
+    for _ in range(3):
+        K.attention(q, kc, vc, 0)
+    e0, e1 = torch.cuda.Event(True), torch.cuda.Event(True)
+    e0.record()
+    for _ in range(iters):
+        K.attention(q, kc, vc, 0)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / iters
+    flop = 4.0 * b * hq * d * t * (t + 1) / 2
+    print(json.dumps({"kernel": "prefill_attn_fa_kernel<128>", "us_per_call": round(us, 1),
+                      "tflop_s": round(flop / us / 1e6, 1), "calls": iters + 3}), flush=True)
+
+
 def copy_calibration(mib: int) -> None:
     """A plain device copy of `mib` MiB (bf16 tensor copy_), three times: the
     known-size kernel that --pmc FETCH_SIZE / WRITE_SIZE are scaled by."""
@@ -306,6 +335,10 @@ def main(argv=None):
     if args.copy_calibration:
         torch.cuda.set_device(0)
         copy_calibration(args.copy_calibration)
+        return
+    if args.prefill_attention:
+        torch.cuda.set_device(0)
+        prefill_attention(args.prefill_attention)
         return
     if WORKLOADS[args.workload] is not None:
         secondary(args)
