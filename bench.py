@@ -1,30 +1,36 @@
-"""Decode benchmark: Qwen2.5-0.5B-shape bf16, batch 1, 128-token prompt, greedy decode.
+"""Decode benchmark: Qwen2.5-0.5B-shape bf16, batch 1, 128-token prompt + 256 greedy tokens.
 
-A step is one decode token (append + decode_step + select_next, the
-reference's TPOT window, minitp/bench/benchmark.py:138-157), replayed from the
-decode hipGraph. W untimed warmup steps, then exactly K timed steps in one
-region bracketed by torch.cuda.synchronize(). The default K = 255 is the
-workload's 256 greedy tokens (the first comes from the prefill).
+The workload is one generation of 256 greedy tokens after a 128-token
+prompt, KV cache of 384 positions: the prefill picks token 1, then 255
+decode steps (contexts 128 .. 382) pick tokens 2 .. 256. A *step* is one
+decode token: append + decode_step + select_next, the reference's TPOT window
+(minitp/bench/benchmark.py:138-157), replayed from the decode hipGraph.
+
+Generations of this workload run back to back. The first W decode steps are
+warm-up (the first of them captures the decode graph); the next K steps are
+timed. When a generation's 255 steps run out, the next generation's prefill
+runs with the clock stopped, so the timed region holds exactly K decode
+steps, each at the context it has in the workload, bracketed by
+torch.cuda.synchronize() on both sides of every timed stretch.
 
 Reported beside the headline tok/s:
-  * HBM roofline of the whole step: algorithmic bytes per token (weights once,
-    LM head once, norms, QKV bias, KV read of ctx + 1 positions) / time,
-    against MI355X's 8 TB/s;
-  * the dominant kernel (the fused RMSNorm + gate/up GEMV + SwiGLU) timed
-    with HIP events on its stream: algorithmic bytes per launch / mean
-    launch time, and its measured HBM traffic per launch when the committed
-    rocprofv3 counter summary is present;
-  * TTFT (prefill start -> first token selected) p50 / mean, TPOT percentiles;
-    the prefill is generate_greedy's: the LM head on the last position only;
-  * the CPU baseline: the oracle restatement of the reference's TP=1 path on
-    the host cores, bf16, over a bounded sample of the same workload.
+  * the HBM roofline of the timed steps (algorithmic bytes per token:
+    weights once, LM head once, norms, QKV bias, KV read of ctx + 1
+    positions) and of the dominant kernel (the fused RMSNorm + gate/up GEMV
+    + SwiGLU, timed with HIP events on its stream; its HBM traffic from the
+    committed rocprofv3 counter summary);
+  * one whole generation timed with the reference's windows: TTFT, prefill
+    tok/s, TPOT percentiles, peak device memory;
+  * the other workloads (7B decode, 0.5B batch-32 decode, 7B 4 x 4096
+    prefill), each with its roofline fraction;
+  * the CPU baseline: the oracle restatement of the reference TP=1 loop on
+    the host cores, per workload and dtype, over bounded samples.
 """
 
 from __future__ import annotations
 
 import argparse
 import json
-import math
 import os
 import sys
 import time
@@ -36,11 +42,21 @@ for p in (os.path.join(ROOT, "mini-tp_amd"), ROOT):
 
 METRIC = "decode tok/s & % HBM roofline, Qwen2.5-0.5B-shape bf16 bs=1; p50 TTFT"
 HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
 PROMPT_LEN = 128
+NEW_TOKENS = 256
+DECODE_STEPS = NEW_TOKENS - 1  # token 1 comes from the prefill
+
+# name -> (shape, batch, prompt tokens, new tokens); new tokens 1 = prefill only
+WORKLOADS = {
+    "q7b": ("QWEN7B", 1, 512, 256),
+    "q05b-b32": ("QWEN05B", 32, 2048, 512),
+    "q7b-prefill": ("QWEN7B", 4, 4096, 1),
+}
 
 
 def step_bytes(cfg, ctx: int, batch: int = 1, esize: int = 2) -> int:
-    """Algorithmic HBM bytes of one decode step reading ctx cached positions."""
+    """Algorithmic HBM bytes of one decode step that reads `ctx` cached positions."""
     L, H, hq, hkv, d, inter, v = (cfg.num_hidden_layers, cfg.hidden_size, cfg.num_attention_heads,
                                   cfg.num_key_value_heads, cfg.head_dim, cfg.intermediate_size, cfg.vocab_size)
     p_stream = L * (H * (hq + 2 * hkv) * d + hq * d * H + 3 * inter * H) + v * H + H * (2 * L + 1) + L * (hq + 2 * hkv) * d
@@ -48,43 +64,10 @@ def step_bytes(cfg, ctx: int, batch: int = 1, esize: int = 2) -> int:
     return esize * p_stream + kv
 
 
-def parse(argv=None):
-    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
-    ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=255)
-    ap.add_argument("--warmup", type=int, default=510)
-    ap.add_argument("--prompt-len", type=int, default=PROMPT_LEN)
-    ap.add_argument("--ttft-iters", type=int, default=10)
-    ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--cpu-budget-s", type=float, default=15.0)
-    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
-                    help="only run a plain copy of MIB MiB (the --pmc byte-counter calibration) and exit")
-    ap.add_argument("--workload", default="q05b", choices=sorted(WORKLOADS),
-                    help="q05b (default): the headline line; the others measure the remaining workloads "
-                         "(one JSON line each, not the headline metric)")
-    ap.add_argument("--prefill-attention", type=int, default=0, metavar="ITERS",
-                    help="only time the causal prefill attention of the 7B 4 x 4096 prefill (q [4, 4096, 28, 128], "
-                         "4 KV heads, bf16) ITERS times after 3 warm-up calls, print one JSON line and exit")
-    ap.add_argument("--dominant-only", action="store_true",
-                    help="only launch the dominant kernel, eagerly (no graphs), once per layer 4 times over, and "
-                         "exit: the workload of the --pmc byte-counter passes")
-    return ap.parse_args(argv)
-
-
-# Other workloads: (shape, batch, prompt length, decode steps after the first token)
-WORKLOADS = {
-    "q05b": None,  # the headline line below
-    "q05b-b32": ("QWEN05B", 32, 2048, 511),
-    "q7b": ("QWEN7B", 1, 512, 255),
-    "q7b-prefill": ("QWEN7B", 4, 4096, 0),
-}
-MFMA_BF16_PEAK_TFLOPS = 2500.0
-
-
 def prefill_flops(cfg, batch: int, t: int) -> float:
-    """Dense FLOPs of a prefill of `t` tokens per row: the linear layers, causal
-    attention (QK^T and PV over the visible keys) and the LM head of the last
-    position only (what the prefill computes when no full logits are asked)."""
+    """Dense FLOPs of a prefill of `t` tokens per row: the linear layers,
+    causal attention (QK^T and PV over the visible keys) and the LM head of
+    the last position only (what generate_greedy's prefill computes)."""
     L, H, hq, hkv, d, inter, v = (cfg.num_hidden_layers, cfg.hidden_size, cfg.num_attention_heads,
                                   cfg.num_key_value_heads, cfg.head_dim, cfg.intermediate_size, cfg.vocab_size)
     m = batch * t
@@ -93,79 +76,195 @@ def prefill_flops(cfg, batch: int, t: int) -> float:
     return linear + attn + 2.0 * batch * v * H
 
 
-def secondary(args):
-    """One JSON line for a non-headline workload: decode tok/s with the step
-    roofline, or (prefill-only) TTFT with the dense-FLOP MFMA fraction."""
+def parse(argv=None):
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=DECODE_STEPS, help="timed decode steps K")
+    ap.add_argument("--warmup", type=int, default=DECODE_STEPS,
+                    help="untimed decode steps W before them (at least 1: the first captures the decode graph)")
+    ap.add_argument("--ttft-iters", type=int, default=10)
+    ap.add_argument("--no-workloads", action="store_true", help="skip the 7B and batch-32 workloads")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget-s", type=float, default=10.0,
+                    help="host seconds of decode steps per CPU-baseline sample (the prefill comes on top)")
+    ap.add_argument("--cpu-configs", default="tiny-fp32,q05b-bf16,q05b-fp32,q7b-bf16,q7b-fp32",
+                    help="comma-separated CPU-baseline samples")
+    ap.add_argument("--decode-path", default="auto", choices=["auto", "graph", "persistent"])
+    ap.add_argument("--workload", default="q05b", choices=["q05b", *sorted(WORKLOADS)],
+                    help="q05b (default): the headline line; another name prints only that workload's line")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="only run a plain copy of MIB MiB (the --pmc byte-counter calibration) and exit")
+    ap.add_argument("--prefill-attention", type=int, default=0, metavar="ITERS",
+                    help="only time the causal prefill attention of the 7B 4 x 4096 prefill (q [4, 4096, 28, 128], "
+                         "4 KV heads, bf16) ITERS times after 3 warm-up calls, print one JSON line and exit")
+    ap.add_argument("--dominant-only", action="store_true",
+                    help="only launch the dominant kernel, eagerly (no graphs), once per layer 4 times over, and "
+                         "exit: the workload of the --pmc byte-counter passes")
+    ap.add_argument("--decode-only", type=int, default=0, metavar="TOKENS",
+                    help="only run one generation of the headline workload with TOKENS new tokens after a warm-up "
+                         "one and exit: the workload of the decode kernel profiles")
+    return ap.parse_args(argv)
+
+
+def note(msg: str) -> None:
+    """One progress line on stderr as a phase of the run finishes."""
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+# ---------------------------------------------------------------------------
+# decode steps of back-to-back generations
+
+
+class StepSource:
+    """Decode steps of back-to-back generations of one workload. run(k)
+    performs the next k steps and returns the seconds they took; prefills
+    between generations run with the clock stopped."""
+
+    def __init__(self, model, prompt, new_tokens: int) -> None:
+        self.model, self.prompt, self.new_tokens = model, prompt, new_tokens
+        self.state = None
+        self.tok = None
+        self.left = 0
+        self.generations = 0
+        self.contexts: list[int] = []  # cached positions before each step run so far
+
+    def _next_generation(self) -> None:
+        import torch
+
+        from minitp.generation import GenerationState
+
+        torch.cuda.synchronize()
+        self.state = GenerationState(self.model, self.prompt, self.new_tokens, prefill_logits="last",
+                                     reuse_decode_logits=True)  # as generate_greedy runs it
+        self.tok = self.state.select_next(self.state.prefill())
+        self.left = self.new_tokens - 1
+        self.generations += 1
+        torch.cuda.synchronize()
+
+    def run(self, k: int) -> float:
+        import torch
+
+        seconds = 0.0
+        while k > 0:
+            if self.left == 0:
+                self._next_generation()
+            m = min(k, self.left)
+            st, tok = self.state, self.tok
+            start = st.cursor  # positions cached before the next step
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            for _ in range(m):
+                pos = st.append(tok)
+                tok = st.select_next(st.decode_step(tok, pos))
+            torch.cuda.synchronize()
+            seconds += time.perf_counter() - t0
+            self.tok = tok
+            self.contexts += range(start, start + m)
+            self.left -= m
+            k -= m
+        return seconds
+
+
+def set_decode_path(model, path: str) -> None:
+    from minitp import _native as N
+
+    code = {"auto": N.DECODE_AUTO, "graph": N.DECODE_GRAPH, "persistent": N.DECODE_PERSISTENT}[path]
+    model.program().set_decode_path(code)
+
+
+def one_generation(model, prompt, new_tokens: int, prefill_logits: str = "last") -> dict:
+    """One generation with the reference's windows (TTFT, prefill, TPOT) and
+    the peak device memory it reached."""
+    import torch
+
+    from minitp.bench.benchmark import percentiles, time_generation
+
+    torch.cuda.synchronize()
+    torch.cuda.reset_peak_memory_stats()
+    it = time_generation(model, prompt, new_tokens, prefill_logits=prefill_logits)
+    b, t = prompt.shape
+    tp = percentiles(it.step_ms)
+    out = {"ttft_ms": round(it.ttft_s * 1e3, 3), "prefill_ms": round(it.prefill_s * 1e3, 3),
+           "prefill_tok_s": round(b * t / it.prefill_s, 1), "tpot_ms": tp,
+           "peak_memory_gib": round(torch.cuda.max_memory_allocated() / 2 ** 30, 3)}
+    if tp:
+        out["decode_tok_s"] = round(b * 1e3 / tp["mean"], 1)  # reference: B * 1e3 / TPOT mean
+    return out
+
+
+def ttft_samples(model, prompt, iters: int, prefill_logits: str) -> list[float]:
+    """TTFT (prefill start -> first token selected) of `iters` prefills, ms."""
+    import torch
+
+    from minitp.generation import GenerationState
+
+    out = []
+    for _ in range(iters):
+        st = GenerationState(model, prompt, 1, prefill_logits=prefill_logits)
+        a, b = torch.cuda.Event(True), torch.cuda.Event(True)
+        a.record()
+        st.select_next(st.prefill())
+        b.record()
+        torch.cuda.synchronize()
+        out.append(a.elapsed_time(b))
+        del st
+    return out
+
+
+def p50(xs: list[float]) -> float:
+    from minitp.bench.benchmark import percentiles
+
+    return percentiles(xs)["p50"]
+
+
+# ---------------------------------------------------------------------------
+# the other workloads
+
+
+def measure_workload(name: str, model=None) -> dict:
+    """Decode tok/s and step roofline (decode workloads) or TTFT and the
+    dense-FLOP MFMA fraction (the prefill workload) of one workload, after
+    one untimed run of it."""
     import torch
 
     from minitp import synthetic
-    from minitp.generation import GenerationState
 
-    shape, batch, plen, steps = WORKLOADS[args.workload]
+    shape, batch, plen, new = WORKLOADS[name]
     cfg = getattr(synthetic, shape)
-    torch.cuda.set_device(0)
-    out = {"workload": args.workload, "shape": shape, "batch": batch, "prompt": plen, "dtype": "bf16"}
-    with torch.inference_mode():
+    out = {"shape": shape, "batch": batch, "prompt": plen, "new_tokens": new, "dtype": "bf16"}
+    if model is None:
         model = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device="cuda", seed=0)
-        prompt = synthetic.synthetic_prompt(cfg.vocab_size, batch, plen, seed=0, device="cuda")
-        torch.cuda.synchronize()
-        if steps:
-            decode_run(model, prompt, steps)  # warmup (graph capture for this batch / length)
-            dt, ttft, _, _ = decode_run(model, prompt, steps)
-            total = sum(step_bytes(cfg, plen + s, batch=batch) for s in range(steps))
-            out.update({"decode_tok_s": round(batch * steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 4),
-                        "step_roofline_frac": round(total / dt / 1e9 / HBM_PEAK_GBS, 4),
-                        "roofline_tok_s": round(batch * HBM_PEAK_GBS * 1e9 / (total / steps), 1),
-                        "ttft_ms": round(ttft * 1e3, 3)})
-        else:
-            ttfts = []
-            for _ in range(4):
-                st = GenerationState(model, prompt, 1, prefill_logits="last")
-                a, b = torch.cuda.Event(True), torch.cuda.Event(True)
-                a.record()
-                st.select_next(st.prefill())
-                b.record()
-                torch.cuda.synchronize()
-                ttfts.append(a.elapsed_time(b) / 1e3)
-                del st
-            ttft = sorted(ttfts)[1]  # p50 of the last three (the first includes one-time setup)
-            fl = prefill_flops(cfg, batch, plen)
-            out.update({"ttft_ms": round(ttft * 1e3, 3), "prefill_tflop": round(fl / 1e12, 2),
-                        "mfma_frac": round(fl / ttft / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-                        "ttft_ms_all": [round(t * 1e3, 3) for t in ttfts]})
-    print(json.dumps(out), flush=True)
-
-
-def decode_run(model, prompt, n_steps, record_steps=False):
-    """Prefill + first pick, then n_steps decode steps. Returns
-    (decode_seconds, ttft_s, step_ms list, out_ids)."""
-    import torch
-
-    from minitp.generation import GenerationState
-
-    st = GenerationState(model, prompt, n_steps + 1, prefill_logits="last")
-    e_t0, e_t1 = torch.cuda.Event(True), torch.cuda.Event(True)
-    e_t0.record()
-    logits = st.prefill()
-    tok = st.select_next(logits)
-    e_t1.record()
+    prompt = synthetic.synthetic_prompt(cfg.vocab_size, batch, plen, seed=0, device="cuda")
     torch.cuda.synchronize()
-    ttft = e_t0.elapsed_time(e_t1) / 1e3
-    evs = []
-    t0 = time.perf_counter()
-    for _ in range(n_steps):
-        if record_steps:
-            a, b = torch.cuda.Event(True), torch.cuda.Event(True)
-            a.record()
-        pos = st.append(tok)
-        logits = st.decode_step(tok, pos)
-        tok = st.select_next(logits)
-        if record_steps:
-            b.record()
-            evs.append((a, b))
-    torch.cuda.synchronize()
-    dt = time.perf_counter() - t0
-    return dt, ttft, [a.elapsed_time(b) for a, b in evs], st.out_ids
+    if new > 1:
+        src = StepSource(model, prompt, new)
+        src.run(new - 1)  # warm-up generation (graph capture for this batch / cache size)
+        src.contexts.clear()
+        dt = src.run(new - 1)
+        total = sum(step_bytes(cfg, c, batch=batch) for c in src.contexts)
+        steps = len(src.contexts)
+        out.update({"decode_tok_s": round(batch * steps / dt, 1), "ms_per_step": round(dt * 1e3 / steps, 4),
+                    "steps": steps, "step_roofline_frac": round(total / dt / 1e9 / HBM_PEAK_GBS, 4),
+                    "roofline_tok_s": round(batch * HBM_PEAK_GBS * 1e9 / (total / steps), 1)})
+        gen = one_generation(model, prompt, new)
+        out.update({k: gen[k] for k in ("ttft_ms", "prefill_tok_s", "peak_memory_gib")})
+        out["tpot_ms"] = gen["tpot_ms"]
+    else:
+        ttft_samples(model, prompt, 1, "last")  # one-time setup of this shape
+        torch.cuda.reset_peak_memory_stats()
+        xs = ttft_samples(model, prompt, 3, "last")
+        fl = prefill_flops(cfg, batch, plen)
+        ms = p50(xs)
+        out.update({"ttft_ms": ms, "ttft_ms_all": [round(x, 3) for x in xs], "prefill_tflop": round(fl / 1e12, 2),
+                    "prefill_tok_s": round(batch * plen / ms * 1e3, 1),
+                    "mfma_frac": round(fl / (ms * 1e-3) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                    "peak_memory_gib": round(torch.cuda.max_memory_allocated() / 2 ** 30, 3)})
+    note(f"workload {name} done")
+    return out
+
+
+# ---------------------------------------------------------------------------
+# the dominant kernel
 
 
 DOMINANT = "gemv_reg_kernel<minitp::bf16, 1, 1, 2, 1, 2>"  # PRO_NORM, EPI_SWIGLU: rocprofv3's name for it
@@ -173,8 +272,8 @@ TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gate_up_gemv_q05b_decode_traffic.
 
 
 def _dominant_launcher(model):
-    """A function launching the dominant kernel once per layer on the current
-    stream, with that layer's weights."""
+    """Launches the dominant kernel once per layer on the current stream,
+    with that layer's weights."""
     import torch
 
     from minitp import _native as N
@@ -193,13 +292,12 @@ def _dominant_launcher(model):
     return launch_all
 
 
-def dominant_kernel(model, reps: int = 20):
-    """The kernel with the largest share of a decode step: the fused
-    post-attention RMSNorm + gate/up GEMV + SwiGLU that the decode graph runs
-    once per layer. The same entry point and the same per-layer weights,
-    launched once per layer in a captured graph (so no launch re-reads a
-    cache-resident matrix and no host launch cost is counted), timed with
-    HIP events on the stream the graph replays on."""
+def dominant_kernel(model, reps: int = 20) -> dict:
+    """The fused post-attention RMSNorm + gate/up GEMV + SwiGLU, the kernel
+    with the largest share of a decode step: the same entry point and the
+    same per-layer weights as the decode graph, once per layer in a captured
+    graph (no launch re-reads a cache-resident matrix, no host launch cost),
+    timed with HIP events on the stream the graph replays on."""
     import torch
 
     launch_all = _dominant_launcher(model)
@@ -229,13 +327,16 @@ def dominant_kernel(model, reps: int = 20):
 
 def measured_traffic():
     """HBM bytes per launch of the dominant kernel from the committed
-    rocprofv3 --pmc summary (FETCH_SIZE, WRITE_SIZE scaled by a plain copy of
-    known size), or None when that summary is absent."""
+    rocprofv3 --pmc summary, or None when that summary is absent."""
     try:
         with open(TRAFFIC_FILE) as f:
             return int(json.load(f)["traffic_bytes_per_launch"])
     except (OSError, KeyError, ValueError):
         return None
+
+
+# ---------------------------------------------------------------------------
+# single-purpose runs (profiling workloads)
 
 
 def prefill_attention(iters: int) -> None:
@@ -278,49 +379,175 @@ def copy_calibration(mib: int) -> None:
     print(json.dumps({"copy_bytes_read": n * 2, "copy_bytes_written": n * 2, "launches": 3}), flush=True)
 
 
-def cpu_baseline(model, prompt, budget_s: float):
-    """The oracle (CPU restatement of the reference TP=1 path) in bf16 on the
-    host cores: prefill of the same prompt, then decode steps until the time
-    budget is spent. Reports decode tok/s."""
-    import torch
+# ---------------------------------------------------------------------------
+# CPU baseline
 
-    from oracle import qwen2_ref as R
 
-    threads = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
-    threads = min(threads, 16)
-    torch.set_num_threads(threads)
-    c = model.cfg
-    shape = R.Qwen2Shape(c.hidden_size, c.intermediate_size, c.num_hidden_layers, c.num_attention_heads,
-                         c.num_key_value_heads, c.head_dim, c.vocab_size, c.rms_norm_eps, c.rope_theta,
-                         c.max_position_embeddings, c.tie_word_embeddings)
-    sd = {k: v.detach().cpu() for k, v in model.state_dict().items()}
-    if c.tie_word_embeddings:
-        sd["lm_head.weight"] = sd["model.embed_tokens.weight"]
-    oracle = R.OracleQwen2(shape, sd)
-    ids = prompt.cpu()
-    with torch.inference_mode():
-        st = R.OracleGenerationState(oracle, ids, 1024)
-        t0 = time.perf_counter()
-        logits = st.prefill()
-        tok = st.select_next(logits)
-        ttft = time.perf_counter() - t0
-        steps, t0 = 0, time.perf_counter()
-        while steps < 3 or (time.perf_counter() - t0 < budget_s and steps < 255):
-            pos = st.append(tok)
-            logits = st.decode_step(tok, pos)
-            tok = st.select_next(logits)
-            steps += 1
-        dt = time.perf_counter() - t0
-    model_name = ""
+CPU_SAMPLES = {
+    # name -> (shape, dtype, batch, prompt tokens, new tokens)
+    "tiny-fp32": ("TINY", "fp32", 1, 8, 16),
+    "q05b-bf16": ("QWEN05B", "bf16", 1, 128, 256),
+    "q05b-fp32": ("QWEN05B", "fp32", 1, 128, 256),
+    "q7b-bf16": ("QWEN7B", "bf16", 1, 512, 256),
+    "q7b-fp32": ("QWEN7B", "fp32", 1, 512, 256),
+}
+
+
+def cpu_threads() -> tuple[int, int]:
+    """(threads used, affinity cores): the cores this process may run on,
+    capped by OMP_NUM_THREADS when the environment sets it (the host's CPU
+    share for this GPU)."""
+    affinity = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    cap = os.environ.get("OMP_NUM_THREADS", "")
+    threads = min(affinity, int(cap)) if cap.isdigit() and int(cap) > 0 else affinity
+    return threads, affinity
+
+
+def cpu_model_name() -> str:
     try:
         with open("/proc/cpuinfo") as f:
-            model_name = next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
+            return next(line.split(":", 1)[1].strip() for line in f if line.startswith("model name"))
     except (OSError, StopIteration):
-        pass
-    return {"value": round(steps / dt, 3), "unit": "tok/s", "cores": threads, "kind": "port",
-            "sample": f"oracle bf16 restatement of the reference TP=1 loop: prefill {ids.shape[1]} tokens "
-                      f"(TTFT {ttft:.2f} s) then {steps} greedy decode steps in {dt:.1f} s",
-            "cpu": model_name}
+        return ""
+
+
+def cpu_sample(name: str, budget_s: float, gpu_models: dict) -> dict:
+    """The oracle (the CPU restatement of the reference TP=1 loop) on the
+    host cores: the workload's prefill, then greedy decode steps until the
+    workload ends or `budget_s` seconds of decode are spent. Weights are the
+    workload's seeded synthetic ones (generated on the GPU, bit-identical to
+    the oracle's generator, copied to host memory)."""
+    import torch
+
+    from minitp import synthetic
+    from oracle import qwen2_ref as R
+
+    shape, dt, batch, plen, new = CPU_SAMPLES[name]
+    dtype = {"fp32": torch.float32, "bf16": torch.bfloat16}[dt]
+    cfg = getattr(synthetic, shape)
+    gm = gpu_models.get((shape, dtype))
+    built = gm is None
+    if built:
+        gm = synthetic.build_synthetic_model(cfg, dtype=dtype, device="cuda", seed=0)
+    sd = {k: v.detach().to("cpu") for k, v in gm.state_dict().items()}
+    if built:
+        del gm
+        torch.cuda.empty_cache()
+    if cfg.tie_word_embeddings:
+        sd["lm_head.weight"] = sd["model.embed_tokens.weight"]
+    oshape = R.Qwen2Shape(cfg.hidden_size, cfg.intermediate_size, cfg.num_hidden_layers, cfg.num_attention_heads,
+                          cfg.num_key_value_heads, cfg.head_dim, cfg.vocab_size, cfg.rms_norm_eps, cfg.rope_theta,
+                          cfg.max_position_embeddings, cfg.tie_word_embeddings)
+    oracle = R.OracleQwen2(oshape, sd)
+    ids = R.synthetic_prompt(cfg.vocab_size, batch, plen, seed=0)
+    with torch.inference_mode():
+        st = R.OracleGenerationState(oracle, ids, new)
+        t0 = time.perf_counter()
+        tok = st.select_next(st.prefill())
+        ttft = time.perf_counter() - t0
+        steps, t0 = 0, time.perf_counter()
+        while steps < new - 1 and (steps < 2 or time.perf_counter() - t0 < budget_s):
+            pos = st.append(tok)
+            tok = st.select_next(st.decode_step(tok, pos))
+            steps += 1
+        dt_s = time.perf_counter() - t0
+    del oracle, sd, st
+    bounded = steps < new - 1
+    note(f"CPU sample {name}: {batch * steps / dt_s:.3f} tok/s")
+    return {"workload": name, "value": round(batch * steps / dt_s, 3), "unit": "tok/s", "ttft_s": round(ttft, 3),
+            "decode_steps": steps,
+            "sample": f"{shape} {dt}: prefill {batch} x {plen} tokens, then {steps} of the workload's {new - 1} "
+                      f"decode steps in {dt_s:.1f} s" + (" (bounded by the time budget)" if bounded else "")}
+
+
+def cpu_baseline(names: list[str], budget_s: float, gpu_models: dict) -> tuple[dict, list[dict]]:
+    import torch
+
+    threads, affinity = cpu_threads()
+    torch.set_num_threads(threads)
+    rows = [cpu_sample(n, budget_s, gpu_models) for n in names]
+    head = next((r for r in rows if r["workload"] == "q05b-bf16"), rows[0] if rows else None)
+    common = {"cores": threads, "affinity_cores": affinity, "kind": "port", "cpu": cpu_model_name()}
+    main = None
+    if head is not None:
+        main = {"value": head["value"], "unit": "tok/s", **common,
+                "sample": "oracle restatement of the reference TP=1 loop, " + head["sample"]}
+    return main, [dict(r, **common) for r in rows]
+
+
+# ---------------------------------------------------------------------------
+
+
+def headline(args) -> dict:
+    import torch
+
+    from minitp.synthetic import QWEN05B, build_synthetic_model, synthetic_prompt
+
+    cfg = QWEN05B
+    warm = max(1, args.warmup)
+    with torch.inference_mode():
+        model = build_synthetic_model(cfg, dtype=torch.bfloat16, device="cuda", seed=0)
+        set_decode_path(model, args.decode_path)
+        prompt = synthetic_prompt(cfg.vocab_size, 1, PROMPT_LEN, seed=0, device="cuda")
+        src = StepSource(model, prompt, NEW_TOKENS)
+        src.run(warm)
+        first_ctx = len(src.contexts)
+        dt = src.run(args.steps)
+        ctxs = src.contexts[first_ctx:]
+        gens = src.generations
+        model.program().check_decode()
+        note(f"headline: {len(ctxs)} timed decode steps, {len(ctxs) / dt:.1f} tok/s")
+
+        # after the timed region: the reference's windows on whole generations
+        gen = one_generation(model, prompt, NEW_TOKENS)
+        full = ttft_samples(model, prompt, 3, "all")
+        ttfts = ttft_samples(model, prompt, args.ttft_iters, "last")
+        kern = dominant_kernel(model)
+        note("headline: generation windows, TTFT samples and the dominant kernel done")
+
+    tok_s = len(ctxs) / dt
+    total = sum(step_bytes(cfg, c) for c in ctxs)
+    achieved = total / dt / 1e9
+    k_gbs = kern["bytes_per_launch"] / (kern["us_per_launch"] * 1e-6) / 1e9
+    from minitp.bench.benchmark import percentiles
+
+    tt = percentiles(ttfts)
+    result = {
+        "metric": METRIC,
+        "value": round(tok_s, 1),
+        "unit": "tok/s",
+        "n_gpus": 1,
+        "steps": len(ctxs),
+        "warmup": warm,
+        "ms_per_step": round(dt * 1e3 / len(ctxs), 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded N(0,0.02) random-init weights, uniform prompt ids)",
+        "config": {"workload": f"Qwen2.5-0.5B-shape bf16 decode, batch 1, {PROMPT_LEN}-token prompt + {NEW_TOKENS} "
+                               f"greedy tokens (KV cache {PROMPT_LEN + NEW_TOKENS} positions); timed: decode steps "
+                               f"{warm + 1}-{warm + len(ctxs)} of back-to-back generations",
+                   "global_batch": 1, "seq_len": PROMPT_LEN + NEW_TOKENS, "parallelism": "tp1"},
+        "timed_contexts": {"min": min(ctxs), "max": max(ctxs), "mean": round(sum(ctxs) / len(ctxs), 1),
+                           "generations_started": gens},
+        "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(), "kernel": kern["name"],
+                     "bytes_per_launch": kern["bytes_per_launch"], "us_per_launch": round(kern["us_per_launch"], 3)},
+        "step_roofline": {"achieved_gbs": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
+                          "bytes_per_token_avg": int(total / len(ctxs)),
+                          "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / (total / len(ctxs)), 1)},
+        "ttft_ms": {"p50": tt["p50"], "mean": tt["mean"], "samples": len(ttfts),
+                    "prefill": "generate_greedy's (LM head on the last position)"},
+        "ttft_full_logits_ms": {"p50": p50(full), "samples": len(full),
+                                "prefill": "the reference's GenerationState.prefill (logits of all 128 positions)"},
+        "generation": gen,
+        "tpot_ms": gen["tpot_ms"],
+        "prefill_tok_s": gen["prefill_tok_s"],
+        "peak_memory_gib": gen["peak_memory_gib"],
+        "decode_path": model.program().decode_path_name(),
+    }
+    return result, model
 
 
 def main(argv=None):
@@ -328,98 +555,62 @@ def main(argv=None):
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": f"--gpus {args.gpus} (WORLD_SIZE {world}): this build runs the token loop on one "
-                                   "GPU only; multi-GPU sharding is a design note, not a measured path"}))
+                                   "GPU; the path's sharding is a design note, no figure at several GPUs is measured"}))
         sys.exit(2)
     import torch
 
+    torch.cuda.set_device(0)
     if args.copy_calibration:
-        torch.cuda.set_device(0)
         copy_calibration(args.copy_calibration)
         return
     if args.prefill_attention:
-        torch.cuda.set_device(0)
         prefill_attention(args.prefill_attention)
         return
-    if WORKLOADS[args.workload] is not None:
-        secondary(args)
+    if args.workload != "q05b":
+        with torch.inference_mode():
+            print(json.dumps({"workload": args.workload, **measure_workload(args.workload)}), flush=True)
         return
-    from minitp.bench.benchmark import _percentiles
-    from minitp.synthetic import QWEN05B, build_synthetic_model, synthetic_prompt
+    if args.dominant_only or args.decode_only:
+        from minitp.synthetic import QWEN05B, build_synthetic_model, synthetic_prompt
 
-    torch.cuda.set_device(0)
-    cfg = QWEN05B
-    with torch.inference_mode():
-        model = build_synthetic_model(cfg, dtype=torch.bfloat16, device="cuda", seed=0)
-        if args.dominant_only:
-            launch_all = _dominant_launcher(model)
-            for _ in range(4):
-                launch_all()
-            torch.cuda.synchronize()
-            print(json.dumps({"kernel": DOMINANT, "launches": 4 * cfg.num_hidden_layers}), flush=True)
+        with torch.inference_mode():
+            model = build_synthetic_model(QWEN05B, dtype=torch.bfloat16, device="cuda", seed=0)
+            if args.dominant_only:
+                launch_all = _dominant_launcher(model)
+                for _ in range(4):
+                    launch_all()
+                torch.cuda.synchronize()
+                print(json.dumps({"kernel": DOMINANT, "launches": 4 * QWEN05B.num_hidden_layers}), flush=True)
+                return
+            set_decode_path(model, args.decode_path)
+            prompt = synthetic_prompt(QWEN05B.vocab_size, 1, PROMPT_LEN, seed=0, device="cuda")
+            src = StepSource(model, prompt, args.decode_only)
+            src.run(args.decode_only - 1)
+            dt = src.run(args.decode_only - 1)
+            model.program().check_decode()
+            print(json.dumps({"decode_path": model.program().decode_path_name(),
+                              "ms_per_step": round(dt * 1e3 / (args.decode_only - 1), 4)}), flush=True)
             return
-        prompt = synthetic_prompt(cfg.vocab_size, 1, args.prompt_len, seed=0, device="cuda")
-        torch.cuda.synchronize()
 
-        # warmup: whole generations of 255 steps (graph capture happens here);
-        # the last one records per-step events for the TPOT percentiles
-        step_ms, ttfts = [], []
-        n_warm = max(1, math.ceil(args.warmup / 255))
-        for i in range(n_warm):
-            _, ttft, ms, _ = decode_run(model, prompt, 255, record_steps=(i == n_warm - 1))
-            if i > 0:  # the first prefill holds one-time setup (GEMM algorithm timing, first launches)
-                ttfts.append(ttft)
-            step_ms = ms or step_ms
-        for _ in range(args.ttft_iters):
-            from minitp.generation import GenerationState
+    result, model = headline(args)
+    gpu_models = {("QWEN05B", torch.bfloat16): model}
+    if not args.no_workloads:
+        from minitp import synthetic
 
-            st = GenerationState(model, prompt, 1, prefill_logits="last")
-            a, b = torch.cuda.Event(True), torch.cuda.Event(True)
-            a.record()
-            st.select_next(st.prefill())
-            b.record()
-            torch.cuda.synchronize()
-            ttfts.append(a.elapsed_time(b) / 1e3)
-
-        # timed region: exactly K decode steps
-        torch.cuda.synchronize()
-        dt, _, _, out_ids = decode_run(model, prompt, args.steps)
-        kern = dominant_kernel(model)
-
-    tok_s = args.steps / dt
-    total_bytes = sum(step_bytes(cfg, args.prompt_len + s) for s in range(args.steps))
-    achieved = total_bytes / dt / 1e9
-    k_gbs = kern["bytes_per_launch"] / (kern["us_per_launch"] * 1e-6) / 1e9
-    ttft_ms = sorted(t * 1e3 for t in ttfts)
-    result = {
-        "metric": METRIC,
-        "value": round(tok_s, 1),
-        "unit": "tok/s",
-        "n_gpus": 1,
-        "steps": args.steps,
-        "warmup": n_warm * 255,
-        "ms_per_step": round(dt * 1e3 / args.steps, 4),
-        "higher_is_better": True,
-        "scaling": "weak",
-        "vs_baseline": None,
-        "dtype": "bf16",
-        "data": "synthetic (seeded N(0,0.02) random-init weights, uniform prompt ids)",
-        "config": {"workload": f"Qwen2.5-0.5B-shape bf16 decode, batch 1, prompt {args.prompt_len}, "
-                               f"{args.steps + 1} greedy tokens",
-                   "global_batch": 1, "seq_len": args.prompt_len + args.steps + 1, "parallelism": "tp1"},
-        "roofline": {"bound": "hbm", "achieved": round(k_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(k_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(), "kernel": kern["name"],
-                     "bytes_per_launch": kern["bytes_per_launch"], "us_per_launch": round(kern["us_per_launch"], 3)},
-        "step_roofline": {"achieved_gbs": round(achieved, 1), "frac": round(achieved / HBM_PEAK_GBS, 4),
-                          "bytes_per_token_avg": int(total_bytes / args.steps),
-                          "roofline_tok_s": round(HBM_PEAK_GBS * 1e9 / (total_bytes / args.steps), 1)},
-        "ttft_ms": {"p50": round(ttft_ms[(len(ttft_ms) + 1) // 2 - 1], 3),
-                    "mean": round(sum(ttft_ms) / len(ttft_ms), 3), "samples": len(ttft_ms)},
-        "tpot_ms": _percentiles(step_ms),
-        "decode_path": "one hipGraph replay per token: embedding; per layer norm+QKV+RoPE+KV write, attention, "
-                       "o_proj+residual, norm+gate/up+SwiGLU, down+residual; norm+LM head+argmax partials, merge",
-    }
+        with torch.inference_mode():
+            q7b = synthetic.build_synthetic_model(synthetic.QWEN7B, dtype=torch.bfloat16, device="cuda", seed=0)
+            gpu_models[("QWEN7B", torch.bfloat16)] = q7b
+            result["workloads"] = {
+                "q7b": measure_workload("q7b", q7b),
+                "q05b-b32": measure_workload("q05b-b32", model),
+                "q7b-prefill": measure_workload("q7b-prefill", q7b),
+            }
     if not args.no_cpu_baseline:
-        result["cpu_baseline"] = cpu_baseline(model, prompt, args.cpu_budget_s)
+        names = [n for n in args.cpu_configs.split(",") if n]
+        main_cpu, rows = cpu_baseline(names, args.cpu_budget_s, gpu_models)
+        if main_cpu is not None:
+            result["cpu_baseline"] = main_cpu
+        result["cpu_baselines"] = rows
     print(json.dumps(result), flush=True)
 
 

@@ -1326,10 +1326,6 @@ __global__ __launch_bounds__(LT) void decode_loop_kernel(LoopParams p) {
 
 template <typename T>
 const void* pick_kernel(int D) {
-#ifdef LOOP_PROBE_ONLY
-  if (D == 64) return (const void*)decode_loop_kernel<T, 64>;
-  return nullptr;
-#else
   switch (D) {
     case 16:
       return (const void*)decode_loop_kernel<T, 16>;
@@ -1341,7 +1337,6 @@ const void* pick_kernel(int D) {
       return (const void*)decode_loop_kernel<T, 128>;
   }
   return nullptr;
-#endif
 }
 
 inline int align_up(int v, int a) { return (v + a - 1) / a * a; }
@@ -1349,11 +1344,7 @@ inline int align_up(int v, int a) { return (v + a - 1) / a * a; }
 }  // namespace
 
 const void* loop_kernel(int dtype, int D) {
-#ifdef LOOP_PROBE_ONLY
-  return dtype == MINITP_F32 ? nullptr : pick_kernel<bf16>(D);
-#else
   return dtype == MINITP_F32 ? pick_kernel<float>(D) : pick_kernel<bf16>(D);
-#endif
 }
 
 // LL words of one layer and their offsets; the same for every device.

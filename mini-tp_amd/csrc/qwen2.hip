@@ -100,6 +100,7 @@ struct GraphEntry {
   int64_t batch, max_seq;
   void* workspace;
   bool eos;  // records the end-of-sequence update after the token selection
+  bool pick; // records the token selection (next_tok set; batch > 4 has no pick node otherwise)
   hipGraph_t graph;
   hipGraphExec_t exec;
   hipGraphNode_t first;
@@ -689,7 +690,7 @@ int minitp_qwen2_decode(void* handle, void* stream, const minitp_qwen2_step* ste
   std::lock_guard<std::mutex> lock(p->mu);
   for (auto& g : p->graphs)
     if (g.batch == step->batch && g.max_seq == step->max_seq && g.workspace == step->workspace &&
-        g.eos == (step->eos_state != nullptr))
+        g.eos == (step->eos_state != nullptr) && g.pick == (step->next_tok != nullptr))
       return minitp::patch_and_launch(p, g, st, *step, w);
   // First step with this shape: run eagerly, then record the same sequence.
   if ((rc = p->run(st, *step, w))) return rc;
@@ -699,6 +700,7 @@ int minitp_qwen2_decode(void* handle, void* stream, const minitp_qwen2_step* ste
   g.max_seq = step->max_seq;
   g.workspace = step->workspace;
   g.eos = step->eos_state != nullptr;
+  g.pick = step->next_tok != nullptr;
   MINITP_RETURN_HIP(hipStreamBeginCapture(p->capture_stream, hipStreamCaptureModeRelaxed));
   rc = p->run(p->capture_stream, *step, w);
   hipError_t e = hipStreamEndCapture(p->capture_stream, &g.graph);

@@ -18,8 +18,11 @@ copy each step; it keeps at most ``EOS_LAG`` steps queued ahead of the GPU,
 and the steps it queued past the stop write no KV rows, so the result, the
 cursor and ``kv.seq_len`` are the reference's.
 
-The decode logits buffer [B, 1, V] is reused: logits returned by one
-``decode_step`` are overwritten by the next.
+Each ``decode_step`` returns a new logits tensor [B, 1, V], as the
+reference does. ``reuse_decode_logits=True`` (what ``generate_greedy`` and
+the benchmark use, since they only read the token the step picked) writes
+every step's logits into one buffer instead, so the logits a step returned
+are overwritten by the next step.
 
 ``prefill`` returns every prompt position's logits [B, T, V], as the
 reference does, unless the state was made with ``prefill_logits="last"``:
@@ -69,11 +72,12 @@ class GenerationState:
 
     def __init__(self, model: TPQwen2ForCausalLM, input_ids: torch.Tensor, max_new_tokens: int,
                  kv: KVCache | None = None, distributed_argmax: bool = True, kv_init: str = "empty",
-                 prefill_logits: str = "all") -> None:
+                 prefill_logits: str = "all", reuse_decode_logits: bool = False) -> None:
         if prefill_logits not in ("all", "last"):
             raise ValueError(f"prefill_logits must be 'all' or 'last', got {prefill_logits!r}")
         self.model = model
         self.prefill_logits = prefill_logits
+        self.reuse_decode_logits = reuse_decode_logits
         self.distributed_argmax = distributed_argmax
         b, t = input_ids.shape
         self.prompt_len = t
@@ -155,7 +159,7 @@ class GenerationState:
         b = tok.shape[0]
         if pos.data_ptr() == self.positions_buf.data_ptr() + (self.cursor - 1) * 8:
             self._check_position(self.cursor - 1)  # pos is positions_buf[cursor - 1]: value known
-        if self._decode_logits is None or self._decode_logits.shape[0] != b:
+        if not self.reuse_decode_logits or self._decode_logits is None or self._decode_logits.shape[0] != b:
             self._decode_logits = torch.empty(b, 1, self.model.cfg.vocab_size, dtype=self.kv.k_buf.dtype,
                                               device=self.out_ids.device)
         if tok.dtype != torch.long:
@@ -175,7 +179,7 @@ def generate_greedy(model: TPQwen2ForCausalLM, input_ids: torch.Tensor, max_new_
     the first step where every row has produced EOS when ``early_stop``;
     exactly prompt + max_new_tokens columns otherwise."""
     state = GenerationState(model, input_ids, max_new_tokens, kv=kv, distributed_argmax=distributed_argmax,
-                            kv_init=kv_init, prefill_logits="last")
+                            kv_init=kv_init, prefill_logits="last", reuse_decode_logits=True)
     b = input_ids.shape[0]
     if early_stop and eos_token_id is not None and state._native and max_new_tokens > 0:
         return _generate_device_eos(state, eos_token_id, max_new_tokens)

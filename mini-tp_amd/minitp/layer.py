@@ -94,6 +94,7 @@ class _Program:
         h = ctypes.c_void_p()
         N.check(lib.minitp_qwen2_create(ctypes.byref(c), ctypes.byref(w), ctypes.byref(h)), "qwen2_create")
         self.handle = h
+        self.cfg = c
         self.device = head[0].device
         self.dtype = head[0].dtype
         self.fwd_ws: torch.Tensor | None = None
@@ -103,9 +104,30 @@ class _Program:
         """N.DECODE_AUTO (the graph of per-op kernels),
         N.DECODE_GRAPH or N.DECODE_PERSISTENT."""
         N.check(N.lib().minitp_qwen2_set_decode_path(self.handle, path), "qwen2_set_decode_path")
+        self.decode_path = path
 
     def persistent_ok(self) -> bool:
         return bool(N.lib().minitp_qwen2_persistent_ok(self.handle))
+
+    def decode_path_name(self, batch: int = 1) -> str:
+        """Which decode form serves a step of `batch` rows."""
+        persistent = getattr(self, "decode_path", N.DECODE_AUTO) == N.DECODE_PERSISTENT
+        if persistent and batch == 1 and self.persistent_ok():
+            return ("persistent: one launch per token, one block per CU, blocks exchange each layer's results "
+                    "through epoch-tagged words in HBM")
+        return ("one hipGraph replay per token: embedding; per layer norm+QKV+RoPE+KV write, attention, "
+                "o_proj+residual, norm+gate/up+SwiGLU, down+residual; norm+LM head+argmax partials, merge")
+
+    def check_cache(self, kv: KVCache, batch: int) -> None:
+        """The cache must be this model's: [L, batch, Hkv, S, D] in the model
+        dtype on the model's device (the kernels index it with those sizes)."""
+        c = self.cfg
+        want = (c.num_layers, batch, c.kv_heads, kv.max_seq_len, c.head_dim)
+        for buf in (kv.k_buf, kv.v_buf):
+            if tuple(buf.shape) != want or buf.dtype != self.dtype or buf.device != self.device or \
+                    not buf.is_contiguous():
+                raise ValueError(f"KV cache {tuple(buf.shape)} {buf.dtype} on {buf.device} does not fit this model: "
+                                 f"need a contiguous {want} {self.dtype} cache on {self.device}")
 
     def check_decode(self) -> None:
         """Synchronise and raise if a persistent decode step on any of this
@@ -202,6 +224,9 @@ class TPQwen2ForCausalLM(nn.Module):
         prog = self.program()
         b, t = input_ids.shape
         dev = prog.device
+        N.require_gpu(input_ids, positions, next_tok, what="TPQwen2ForCausalLM.forward")
+        if kv_cache is not None:
+            self._check_kv(prog, kv_cache, b)
         ids = input_ids if (input_ids.dtype == torch.long and input_ids.stride(-1) == 1) else \
             input_ids.long().contiguous()
         pos = positions if (positions.dtype == torch.long and positions.is_contiguous()) else \
@@ -231,6 +256,10 @@ class TPQwen2ForCausalLM(nn.Module):
         on-device early stop, or None."""
         prog = self._prog if self._prog is not None else self.program()
         b = tok.shape[0]
+        N.require_gpu(tok, pos, next_tok, what="GenerationState.decode_step")
+        if pos.dtype != torch.long or pos.numel() != 1:
+            raise ValueError(f"decode_step: pos must be one int64 position, got {pos.dtype} of {pos.numel()}")
+        self._check_kv(prog, kv_cache, b)
         kv_cache.check_room(1)
         ws = prog.decode_workspace(b, kv_cache.max_seq_len)
         step = N.Qwen2Step(tok.data_ptr(), tok.stride(0), pos.data_ptr(), b, 1, kv_cache.seq_len,
@@ -241,14 +270,35 @@ class TPQwen2ForCausalLM(nn.Module):
         kv_cache.advance(1)
         return logits
 
+    @staticmethod
+    def _check_kv(prog: _Program, kv: KVCache, batch: int) -> None:
+        """Once per (cache, program, batch): the cache's buffers must be the
+        [L, batch, Hkv, S, D] model-dtype tensors the kernels index."""
+        key = (id(prog), batch)
+        if getattr(kv, "_minitp_fits", None) != key:
+            prog.check_cache(kv, batch)
+            kv._minitp_fits = key
+
     # -- reference API ---------------------------------------------------------
     def forward(self, input_ids: torch.Tensor, positions: torch.Tensor | None = None,
                 kv_cache: KVCache | None = None, gather_logits: bool = False) -> torch.Tensor:
         b, t = input_ids.shape
         N.require_gpu(input_ids, self.model.embed_tokens.weight, what="TPQwen2ForCausalLM.forward")
+        limit = self.cfg.max_position_embeddings
         if positions is None:  # layer.py:99-101
             offset = kv_cache.seq_len if kv_cache is not None and t == 1 else 0
+            if offset + t > limit:
+                raise IndexError(f"position {offset + t - 1} out of range for RoPE table of {limit} rows")
             positions = torch.arange(offset, offset + t, device=input_ids.device)
+        else:
+            # explicit positions index the RoPE table as the reference's
+            # cos_cache[positions] does: negative ones wrap, others past the
+            # table raise (rope.py:37-45). One host read of min / max.
+            from minitp.rope import _check_positions
+
+            _check_positions(positions, limit)
+            positions = positions.to(input_ids.device).long()
+            positions = torch.where(positions < 0, positions + limit, positions)
         if kv_cache is not None:
             kv_cache.check_room(t)
         if self.native_path():

@@ -211,3 +211,48 @@ def test_program_create_validates_and_sizes_workspace():
         lib.minitp_qwen2_destroy(h)
     bad = N.Qwen2Config(N.BF16, 2, 64, 5, 2, 16, 128, 1000, 256, 1e-6)
     assert lib.minitp_qwen2_create(ctypes.byref(bad), ctypes.byref(w), ctypes.byref(h)) == N.ERR_ARG
+
+
+def test_model_config_from_hf_dict_object_and_fallbacks():
+    from types import SimpleNamespace
+
+    from minitp.config import ModelConfig
+
+    base = {"hidden_size": 896, "intermediate_size": 4864, "num_hidden_layers": 24, "num_attention_heads": 14,
+            "num_key_value_heads": 2, "vocab_size": 151936, "rms_norm_eps": 1e-6, "max_position_embeddings": 32768}
+    # transformers >= 5: theta only inside rope_parameters; no head_dim key; tie flag absent
+    cfg = ModelConfig.from_hf({**base, "rope_parameters": {"rope_theta": 1000000}})
+    assert cfg.head_dim == 64 and cfg.rope_theta == 1e6 and isinstance(cfg.rope_theta, float)
+    assert cfg.tie_word_embeddings is True
+    cfg2 = ModelConfig.from_hf(SimpleNamespace(**base, rope_theta=1e4, head_dim=128, tie_word_embeddings=False))
+    assert (cfg2.head_dim, cfg2.rope_theta, cfg2.tie_word_embeddings) == (128, 1e4, False)
+    with pytest.raises(KeyError):
+        ModelConfig.from_hf({k: v for k, v in base.items() if k != "vocab_size"} | {"rope_theta": 1.0})
+    with pytest.raises(ValueError, match="divisible"):
+        ModelConfig.from_hf({**base, "rope_theta": 1.0}, tp_size=3)
+    # KV heads replicate when tp exceeds them, shard otherwise
+    assert cfg.kv_replication(4) == 2 and cfg.kv_replication(2) == 1 and cfg.kv_replication(1) == 1
+    assert cfg.local_heads(2) == (7, 1) and cfg.local_heads(1) == (14, 2)
+
+
+def test_percentiles_follow_the_reference_rank_rule():
+    from minitp.bench.benchmark import percentiles
+
+    # known answers of round(q * n) - 1 over sorted samples (benchmark.py:58-74)
+    five = percentiles([5.0, 1.0, 4.0, 2.0, 3.0])
+    assert (five["p50"], five["p90"], five["p99"], five["min"], five["max"]) == (2.0, 4.0, 5.0, 1.0, 5.0)
+    ten = percentiles([float(i) for i in range(1, 11)])
+    assert (ten["p50"], ten["p90"], ten["p99"], ten["mean"]) == (5.0, 9.0, 10.0, 5.5)
+    assert percentiles([]) is None
+    assert percentiles([7.0])["p99"] == 7.0
+
+
+def test_bench_refuses_more_than_one_gpu():
+    import json
+    import subprocess
+    import sys
+
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in json.loads(r.stdout.strip().splitlines()[-1])["error"]
