@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MINITP_ABI_VERSION 3
+#define MINITP_ABI_VERSION 4
 
 enum {
   MINITP_OK = 0,
@@ -147,6 +147,18 @@ int minitp_attention(void* stream, int dtype, const void* q, const void* k_cache
 int64_t minitp_argmax_workspace_bytes(int64_t B, int64_t V);
 int minitp_argmax(void* stream, int dtype, const void* logits, int64_t ld, int64_t B, int64_t V,
                   int64_t* out, int64_t out_stride, void* workspace, int64_t workspace_bytes);
+/* minitp_argmax without a workspace: no counterpart in the reference. For
+ * callers that cannot allocate device memory (code under hipGraph capture,
+ * serving loops, harnesses that forbid hipMalloc). The slice partials live in
+ * a static device array of minitp_argmax_static_max_bytes() bytes (1 MiB) per
+ * device, held until the process ends; the call allocates nothing. Requests
+ * needing more (B * ceil(V / 4096) * 12 bytes) return MINITP_ERR_ARG. Every
+ * call on one device shares that device's array: calls that overlap on one
+ * device (other streams, other threads) race and must be serialised by the
+ * caller. Same arguments and results as minitp_argmax. */
+int64_t minitp_argmax_static_max_bytes(void);
+int minitp_argmax_static(void* stream, int dtype, const void* logits, int64_t ld, int64_t B, int64_t V,
+                         int64_t* out, int64_t out_stride);
 
 /* ---- whole-model programs ------------------------------------------------ */
 /* TPQwen2ForCausalLM (layer.py:68-124) at tp_size == 1, run as one native

@@ -2,8 +2,17 @@
 // torch.argmax order: the first maximum wins; a NaN beats every number.
 // Grid (slices, rows): each block reduces one slice of a row to a (value,
 // index) partial; a one-block-per-row kernel merges the partials.
+#include <mutex>
+
 #include "common.h"
 #include "kernels.h"
+
+// Slice partials of minitp_argmax_static, the allocation-free argmax: one
+// array per device, held until the process ends. Host code never passes
+// `scratch` itself to a kernel (on the host it is only a stand-in symbol);
+// it passes the device address hipGetSymbolAddress returns for the device.
+constexpr int64_t ARGMAX_SCRATCH_BYTES = 1 << 20;
+static __device__ __align__(256) unsigned char scratch[ARGMAX_SCRATCH_BYTES];
 
 namespace minitp {
 
@@ -146,6 +155,63 @@ int launch_argmax_merge(hipStream_t st, const float* pv, const int64_t* pi, int6
   argmax_merge_kernel<<<(unsigned)rows, 256, 0, st>>>(pv, pi, nb, out, out_stride, state);
   MINITP_LAUNCH_CHECK();
   return MINITP_OK;
+}
+
+namespace {
+
+constexpr int SCRATCH_MAX_DEVICES = 64;
+std::mutex scratch_mu;
+void* scratch_ptr[SCRATCH_MAX_DEVICES];  // device address of `scratch`, per device
+
+// Device address of `scratch` on `dev`, looked up once per device with that
+// device current (each device holds its own copy at its own address).
+int scratch_address(int dev, void** out) {
+  if (dev < 0 || dev >= SCRATCH_MAX_DEVICES) {
+    set_error("argmax_static: device %d beyond the %d this library tracks", dev, SCRATCH_MAX_DEVICES);
+    return MINITP_ERR_ARG;
+  }
+  std::lock_guard<std::mutex> lock(scratch_mu);
+  if (scratch_ptr[dev] == nullptr) {
+    int cur = 0;
+    MINITP_RETURN_HIP(hipGetDevice(&cur));
+    if (cur != dev) MINITP_RETURN_HIP(hipSetDevice(dev));
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (cur != dev) MINITP_RETURN_HIP(hipSetDevice(cur));
+    MINITP_RETURN_HIP(e);
+    scratch_ptr[dev] = p;
+  }
+  *out = scratch_ptr[dev];
+  return MINITP_OK;
+}
+
+}  // namespace
+
+int64_t argmax_static_scratch_bytes() { return ARGMAX_SCRATCH_BYTES; }
+
+int launch_argmax_static(hipStream_t st, int dtype, const void* logits, int64_t ld, int64_t B, int64_t V, int64_t* out,
+                         int64_t out_stride) {
+  if (B == 0) return MINITP_OK;
+  const int64_t need = argmax_workspace_bytes(B, V);
+  if (need > ARGMAX_SCRATCH_BYTES) {
+    set_error("argmax_static: %lld rows x %lld slices need %lld B of partials, more than the %lld B static scratch "
+              "(use minitp_argmax with a workspace)",
+              (long long)B, (long long)nslices(V), (long long)need, (long long)ARGMAX_SCRATCH_BYTES);
+    return MINITP_ERR_ARG;
+  }
+  int dev = 0;
+  if (st != nullptr) {
+    hipDevice_t d = 0;
+    MINITP_RETURN_HIP(hipStreamGetDevice(st, &d));
+    dev = (int)d;
+  } else {
+    MINITP_RETURN_HIP(hipGetDevice(&dev));
+  }
+  void* ws = nullptr;
+  if (const int rc = scratch_address(dev, &ws)) return rc;
+  // every partial the merge reads is written by the slice kernel first:
+  // nothing in the scratch has to start at zero
+  return launch_argmax(st, dtype, logits, ld, B, V, out, out_stride, ws, need, nullptr, 0);
 }
 
 int launch_argmax(hipStream_t st, int dtype, const void* logits, int64_t ld, int64_t B, int64_t V, int64_t* out,

@@ -300,6 +300,18 @@ int minitp_argmax(void* stream, int dtype, const void* logits, int64_t ld, int64
   return launch_argmax(S(stream), dtype, logits, ld, B, V, out, out_stride, workspace, workspace_bytes);
 }
 
+int64_t minitp_argmax_static_max_bytes(void) { return argmax_static_scratch_bytes(); }
+
+int minitp_argmax_static(void* stream, int dtype, const void* logits, int64_t ld, int64_t B, int64_t V, int64_t* out,
+                         int64_t out_stride) {
+  CHECK_DTYPE(dtype);
+  MINITP_CHECK_ARG(B >= 0 && V > 0 && ld >= V, "argmax_static: B=%lld V=%lld ld=%lld", (long long)B, (long long)V,
+                   (long long)ld);
+  if (B == 0) return MINITP_OK;
+  MINITP_CHECK_ARG(logits && out, "argmax_static: NULL pointer");
+  return launch_argmax_static(S(stream), dtype, logits, ld, B, V, out, out_stride);
+}
+
 }  // extern "C"
 
 namespace minitp {

@@ -137,6 +137,10 @@ int launch_prefill_attention(hipStream_t st, int dtype, const void* q, const voi
 
 // argmax.hip
 int64_t argmax_workspace_bytes(int64_t B, int64_t V);
+// The argmax with its partials in the library's static device scratch.
+int64_t argmax_static_scratch_bytes();
+int launch_argmax_static(hipStream_t st, int dtype, const void* logits, int64_t ld, int64_t B, int64_t V, int64_t* out,
+                         int64_t out_stride);
 // Winner of each of `rows` rows of nb (value, index) partials -> out (or
 // state->next_tok when state is non-null; nothing when that is null).
 // End-of-sequence bookkeeping after a forward's token selection (one block).

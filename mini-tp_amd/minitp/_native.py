@@ -54,6 +54,8 @@ SIGNATURES = {
                                 _i64]),
     "minitp_argmax_workspace_bytes": (_i64, [_i64, _i64]),
     "minitp_argmax": (_int, [_vp, _int, _vp, _i64, _i64, _i64, _vp, _i64, _vp, _i64]),
+    "minitp_argmax_static_max_bytes": (_i64, []),
+    "minitp_argmax_static": (_int, [_vp, _int, _vp, _i64, _i64, _i64, _vp, _i64]),
     "minitp_qwen2_create": (_int, [_vp, _vp, ctypes.POINTER(_vp)]),
     "minitp_qwen2_destroy": (_int, [_vp]),
     "minitp_qwen2_workspace_bytes": (_i64, [_vp, _i64, _i64, _i64]),
