@@ -140,3 +140,40 @@ def test_generation_resumes_on_filled_cache(dtype):
         kv2, _ = _filled(model, oracle, first)
         out = generate_greedy(model, second.to(DEV), n, early_stop=False, kv=kv2).cpu()
         assert torch.equal(out, ref)
+
+
+def test_chunks_and_resume_match_the_reference_fixture():
+    """The reference's own chunked prefill (7, 9, 1, 5 tokens) and the
+    generation it resumed on that cache (tests/golden/tiny_chunked_fp32.npz):
+    chunk logits within the fp32 bar with the same argmax, resumed ids exact,
+    the same cache cursor."""
+    import os
+
+    import numpy as np
+
+    from oracle import qwen2_ref
+    from tests.conftest import GOLDEN
+
+    from minitp.generation import generate_greedy, make_kv_cache
+
+    fx = np.load(os.path.join(GOLDEN, "tiny_chunked_fp32.npz"))
+    shape = qwen2_ref.TINY
+    model = _model_from_state(shape, qwen2_ref.synthetic_state(shape, seed=0, dtype=torch.float32), torch.float32)
+    prompt = torch.from_numpy(fx["prompt"]).to(DEV)
+    resume = torch.from_numpy(fx["resume_prompt"]).to(DEV)
+    new = fx["resume_ids"].shape[1] - resume.shape[1]
+    kv = make_kv_cache(model, prompt.shape[0], prompt.shape[1] + fx["resume_ids"].shape[1])
+    kv.poison(float("nan"))
+    outs, s = [], 0
+    with torch.inference_mode():
+        for n in fx["chunks"].tolist():
+            pos = torch.arange(s, s + n, device=DEV)
+            outs.append(model(prompt[:, s:s + n], positions=pos, kv_cache=kv).float().cpu())
+            s += n
+        got = torch.cat(outs, dim=1)
+        ref = torch.from_numpy(fx["chunk_logits"])
+        assert (got - ref).abs().max().item() <= FP32_LOGIT_ATOL
+        assert torch.equal(got.argmax(-1), ref.argmax(-1))
+        ids = generate_greedy(model, resume, new, early_stop=False, kv=kv).cpu()
+    assert np.array_equal(ids.numpy(), fx["resume_ids"])
+    assert kv.seq_len == int(fx["seq_len"])

@@ -143,3 +143,34 @@ def _copy_cache(oracle, okv):
         dst.copy_(src)
     c.seq_len = okv.seq_len
     return c
+
+
+def test_early_stop_matches_the_reference_fixture():
+    """generate_greedy(eos_token_id=e) against the reference's own outputs
+    (tests/golden/tiny_eos_fp32.npz, tiny shape with std-0.3 weights): every
+    row stopping at a different step, partial finishes padded with EOS, a
+    first pick and an EOS never produced; ids, length and cache cursor
+    exact, nothing written past the cursor."""
+    import os
+
+    import numpy as np
+
+    from oracle import qwen2_ref
+    from tests.conftest import GOLDEN
+
+    from minitp.generation import generate_greedy, make_kv_cache
+
+    fx = np.load(os.path.join(GOLDEN, "tiny_eos_fp32.npz"))
+    shape = qwen2_ref.TINY
+    state = qwen2_ref.synthetic_state(shape, seed=0, dtype=torch.float32, std=float(fx["weight_std"]))
+    model = _model_from_state(shape, state, torch.float32)
+    for i, eos in enumerate(fx["eos"].tolist()):
+        b, n = int(fx["batch"][i]), int(fx["length"][i])
+        prompt = torch.from_numpy(fx["prompts"][i, :b]).to(DEV)
+        kv = make_kv_cache(model, b, prompt.shape[1] + 12)
+        kv.poison(float("nan"))
+        got = generate_greedy(model, prompt, 12, eos_token_id=eos, early_stop=True, kv=kv).cpu()
+        assert np.array_equal(got.numpy(), fx["ids"][i, :b, :n]), (i, eos, got)
+        assert kv.seq_len == int(fx["seq_len"][i])
+        for buf in kv.k + kv.v:
+            assert torch.isnan(buf[:, :, kv.seq_len:]).all()

@@ -209,3 +209,51 @@ def test_uniform_ids_cover_vocab():
     assert ids.min() == 0 and ids.max() == 999
     counts = np.bincount(ids, minlength=1000)
     assert counts.min() > 800 and counts.max() < 1200
+
+
+def _tiny_oracle(std=0.02):
+    sd = R.synthetic_state(R.TINY, seed=0, dtype=torch.float32, std=std)
+    return R.OracleQwen2(R.TINY, sd)
+
+
+def test_oracle_reproduces_reference_chunked_prefill_and_resume():
+    """Chunks through forward(kv_cache=) (the tril(diagonal=cache_len) mask,
+    attention.py:96-103) and a state resumed on the filled cache
+    (generation.py:93,103): the reference's own values, bit for bit."""
+    fx = _fx("tiny_chunked_fp32")
+    m = _tiny_oracle()
+    prompt = torch.from_numpy(fx["prompt"])
+    kv = m.make_kv_cache(prompt.shape[0], prompt.shape[1] + int(fx["resume_ids"].shape[1]))
+    start, outs = 0, []
+    with torch.inference_mode():
+        for c in fx["chunks"].tolist():
+            outs.append(m(prompt[:, start:start + c], positions=torch.arange(start, start + c), kv_cache=kv))
+            start += c
+        assert torch.equal(torch.cat(outs, dim=1), torch.from_numpy(fx["chunk_logits"]))
+        resume = torch.from_numpy(fx["resume_prompt"])
+        new = fx["resume_ids"].shape[1] - resume.shape[1]
+        rows = []
+        ids = R.generate_greedy(m, resume, new, early_stop=False, kv=kv,
+                                on_logits=lambda s, lg: rows.append(lg[:, -1].clone()))
+    assert np.array_equal(ids.numpy(), fx["resume_ids"])
+    assert torch.equal(torch.stack(rows), torch.from_numpy(fx["resume_step_logits"]))
+    assert kv.seq_len == int(fx["seq_len"])
+
+
+def test_oracle_reproduces_reference_early_stop():
+    """generate_greedy's early stop (generation.py:150-168): trimmed ids,
+    EOS padding of finished rows and the cache cursor, as the reference wrote
+    them, over rows stopping at different steps, partial finishes, a first
+    pick and an EOS never produced."""
+    fx = _fx("tiny_eos_fp32")
+    m = _tiny_oracle(float(fx["weight_std"]))
+    stopped_early = 0
+    for i, eos in enumerate(fx["eos"].tolist()):
+        b, n = int(fx["batch"][i]), int(fx["length"][i])
+        prompt = torch.from_numpy(fx["prompts"][i, :b])
+        kv = m.make_kv_cache(b, prompt.shape[1] + 12)
+        ids = R.generate_greedy(m, prompt, 12, eos_token_id=eos, early_stop=True, kv=kv)
+        assert np.array_equal(ids.numpy(), fx["ids"][i, :b, :n]), (i, eos)
+        assert kv.seq_len == int(fx["seq_len"][i])
+        stopped_early += n < prompt.shape[1] + 12
+    assert stopped_early >= 1  # the fixture holds a case where every row stops before the end
