@@ -100,6 +100,9 @@ def parse(argv=None):
     ap.add_argument("--dominant-only", action="store_true",
                     help="only launch the dominant kernel, eagerly (no graphs), once per layer 4 times over, and "
                          "exit: the workload of the --pmc byte-counter passes")
+    ap.add_argument("--gemm", default="", metavar="M,N,K[,swiglu]",
+                    help="only time one bf16 product y = x W^T (minitp_linear; swiglu: W is [2N, K] and y = "
+                         "silu(gate) * up) 10 times after 3 warm-up calls, print one JSON line and exit")
     ap.add_argument("--decode-only", type=int, default=0, metavar="TOKENS",
                     help="only run one generation of the headline workload with TOKENS new tokens after a warm-up "
                          "one and exit: the workload of the decode kernel profiles")
@@ -365,6 +368,37 @@ def prefill_attention(iters: int) -> None:
                       "tflop_s": round(flop / us / 1e6, 1), "calls": iters + 3}), flush=True)
 
 
+def gemm_alone(spec: str, iters: int = 10) -> None:
+    """One bf16 product of a prompt (the kernel minitp_linear picks for the
+    shape), timed with HIP events on the launch stream."""
+    import torch
+
+    from minitp import _native as N
+    from minitp import kernels as K
+
+    parts = spec.split(",")
+    m, n, k = (int(v) for v in parts[:3])
+    swiglu = len(parts) > 3 and parts[3] == "swiglu"
+    g = torch.Generator(device="cuda").manual_seed(0)
+    x = torch.randn(m, k, device="cuda", generator=g).to(torch.bfloat16)
+    w = (torch.randn(2 * n if swiglu else n, k, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+    epi = N.EPI_SWIGLU if swiglu else N.EPI_NONE
+    out = K.linear(x, w, epilogue=epi)
+    for _ in range(2):
+        K.linear(x, w, out=out, epilogue=epi)
+    e0, e1 = torch.cuda.Event(True), torch.cuda.Event(True)
+    e0.record()
+    for _ in range(iters):
+        K.linear(x, w, out=out, epilogue=epi)
+    e1.record()
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / iters
+    flop = 2.0 * m * (2 * n if swiglu else n) * k
+    print(json.dumps({"gemm": spec, "us_per_call": round(us, 1), "tflop_s": round(flop / us / 1e6, 1),
+                      "mfma_frac": round(flop / us / 1e6 / MFMA_BF16_PEAK_TFLOPS, 4), "calls": iters + 3}),
+          flush=True)
+
+
 def copy_calibration(mib: int) -> None:
     """A plain device copy of `mib` MiB (bf16 tensor copy_), three times: the
     known-size kernel that --pmc FETCH_SIZE / WRITE_SIZE are scaled by."""
@@ -565,6 +599,9 @@ def main(argv=None):
         return
     if args.prefill_attention:
         prefill_attention(args.prefill_attention)
+        return
+    if args.gemm:
+        gemm_alone(args.gemm)
         return
     if args.workload != "q05b":
         with torch.inference_mode():

@@ -87,7 +87,9 @@ int minitp_cast_f32_bf16(void* stream, const float* in, void* out, int64_t n);
  * x: [M, K] (row stride ldx), W: [N, K] (or [2N, K] for SWIGLU), bias: [N]
  * or NULL, y: [M, N] (row stride ldy), aux: [M, N] (stride ldy) for RESID
  * (may alias y). Small M streams W once as a GEMV; larger M runs an MFMA
- * GEMM. K must be a multiple of 8; pointers 16-byte aligned. */
+ * GEMM. K must be a multiple of 8; pointers 16-byte aligned. SWIGLU is
+ * served for decode rows (M <= 4) and for bf16 products of at least 96
+ * output tiles of 256 rows x 128 columns (no bias). */
 int minitp_linear(void* stream, int dtype, const void* x, int64_t ldx, const void* w,
                   const void* bias, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                   int epilogue, const void* aux);

@@ -1,6 +1,9 @@
 // Plain bf16 prefill GEMMs on hipBLASLt: y[M, N] = x[M, K] W[N, K]^T (+ bias),
 // fp32 accumulation, one rounding to bf16 (bias added before it, as
-// F.linear's addmm does, fused.py:58). Used only for prompt-sized M and
+// F.linear's addmm does, fused.py:58). Not the product path: the prompt
+// GEMMs run on the library's own MFMA kernels, and these calls happen only
+// when MINITP_GEMM=blaslt is set in the environment, as a comparison for the
+// benchmark. Used only for prompt-sized M and
 // never while the stream is being captured: the library's split-K
 // algorithms may record memsets, which a captured decode graph must not
 // hold. Residual adds stay outside (a separate rounded add, the reference's
@@ -28,6 +31,7 @@
 #include <map>
 #include <vector>
 #include <mutex>
+#include <string>
 #include <tuple>
 
 #include "common.h"
@@ -40,6 +44,18 @@ namespace {
 constexpr int TUNE_CANDIDATES = 8;
 constexpr int TUNE_REPS = 2;
 constexpr float TUNE_MARGIN = 0.03f;
+
+}  // namespace
+
+bool blaslt_requested() {
+  static const bool on = [] {
+    const char* v = getenv("MINITP_GEMM");
+    return v != nullptr && std::string(v) == "blaslt";
+  }();
+  return on;
+}
+
+namespace {
 
 bool tune_enabled() {
   static const bool on = [] {

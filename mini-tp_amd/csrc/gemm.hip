@@ -299,6 +299,10 @@ int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const voi
     set_error("gemm: epilogue %d not supported (split SwiGLU runs as its own kernel)", epi);
     return MINITP_ERR_UNSUPPORTED;
   }
+  // bf16 products large enough to fill the chip with 256 x 256 tiles
+  if (dtype == MINITP_BF16 && epi == MINITP_EPI_NONE && state == nullptr && aligned16(x) && aligned16(w) &&
+      gemm_tile_supported(M, N, K, ldx, ldy, false))
+    return launch_gemm_tile(st, x, ldx, w, bias, y, ldy, M, N, K, false);
   return dtype == MINITP_F32 ? gemm_typed<float>(st, x, ldx, w, bias, y, ldy, M, N, K, epi, aux, state, ws, ws_bytes)
                              : gemm_typed<bf16>(st, x, ldx, w, bias, y, ldy, M, N, K, epi, aux, state, ws, ws_bytes);
 }

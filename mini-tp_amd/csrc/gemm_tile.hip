@@ -1,0 +1,306 @@
+// Large bf16 linear layers of a prompt on gfx950's 32x32x16 MFMA:
+// y[M, N] = bf16(x[M, K] W[N, K]^T (+ bias)), or with the SwiGLU pairing of a
+// [gate; up] weight, act[M, I] = bf16(bf16(silu(g)) * u) where g, u are the
+// bf16-rounded products with rows j and I + j of W (mlp.py:34-38,
+// fused.py:102-104; F.linear semantics of fused.py:57-61 / linear.py:117).
+//
+// Block tile 256 x 256 x (K steps of 64), 512 threads = 8 waves in a 2 x 4
+// grid, each wave owning a 128 x 64 output tile as 4 x 2 fragments of
+// 32 x 32 (16 fp32 accumulators per lane each). Both operands are
+// K-contiguous (x rows, W rows), the layout the MFMA operands want:
+//   v_mfma_f32_32x32x16_bf16: lane l holds A[l % 32][8 (l / 32) + 0..7] and
+//   B[8 (l / 32) + 0..7][l % 32]; accumulator register r of lane l is
+//   D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
+// K steps are staged in LDS (two buffers, 64 KiB each: 256 rows of x and of
+// W, 128 bytes per row), each 16-byte chunk c of row r stored at chunk
+// position c ^ (r & 7), so the 32 lanes reading one fragment column spread
+// over all banks. The global loads of the step after next are in flight in
+// registers while a step's MFMAs run (one LDS barrier per step). Loads are
+// buffer loads: rows past M or N and K past the matrix read zeros, so no load
+// is predicated.
+//
+// Tile order: blocks are dispatched to the 8 XCDs round-robin (block b runs on
+// XCD b % 8, each XCD with its own L2). Block b takes tile (b % 8) * per_xcd +
+// b / 8, so each XCD works through one contiguous range of tiles, and inside
+// a range tiles go in groups of 8 row-tiles (all column tiles of one group of
+// x rows before the next): the 32 blocks an XCD runs at once share 8 x panels
+// and 4 W panels through its L2.
+//
+// Deterministic: every output element is one fixed-order fp32 sum over K.
+#include "common.h"
+#include "kernels.h"
+
+namespace minitp {
+
+namespace {
+
+typedef __bf16 bf16x8_g __attribute__((ext_vector_type(8)));
+typedef float f32x16_g __attribute__((ext_vector_type(16)));
+
+constexpr int TM = 256, TN = 256, TK = 64;
+constexpr int WTM = 128;  // wave tile rows (2 waves along M)
+constexpr int FM = WTM / 32;
+constexpr int ROWB = TK * 2;  // bytes per row per stage
+constexpr int A_BYTES = TM * ROWB, B_BYTES = TN * ROWB;
+constexpr int STAGE_BYTES = A_BYTES + B_BYTES;  // 64 KiB
+constexpr int LDS_TILE_BYTES = 2 * STAGE_BYTES;
+constexpr int CPR = ROWB / 16;  // 16-byte chunks per row per stage
+constexpr int GROUP_M = 8;  // row tiles per group (4 and 16 measured no better)
+// waves along N: 4 (8 waves of 128 x 64, two per SIMD; the default) or 2
+// (4 waves of 128 x 128, one per SIMD: a third less LDS traffic, but 15 %
+// slower at the 7B prefill shapes, one wave per SIMD hiding no latency)
+#ifndef MINITP_TILE_WAVES_N
+#define MINITP_TILE_WAVES_N 4
+#endif
+constexpr uint32_t OOB_OFF = 0xffffffffu;
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  const int n = (int)__builtin_amdgcn_readfirstlane(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
+}
+
+__device__ __forceinline__ uint4 tile_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
+
+// byte offset of chunk c of row r inside an operand's stage buffer. The LDS
+// has 64 banks of 4 bytes (256 bytes across), and a ds_read_b128 serves 16
+// lanes at a time: the 16 lanes of a fragment read (rows r .. r + 15, one
+// chunk column) fall on 16 distinct 16-byte slots when row pairs (2i, 2i + 1)
+// take chunk positions c ^ i.
+#ifndef MINITP_TILE_SWZ_SHIFT
+#define MINITP_TILE_SWZ_SHIFT 1
+#endif
+__device__ __forceinline__ int lds_off(int r, int c) {
+  return r * ROWB + ((c ^ ((r >> MINITP_TILE_SWZ_SHIFT) & 7)) << 4);
+}
+
+enum { TILE_STORE = 0, TILE_SWIGLU = 1 };
+
+template <int EPI, int WAVES_N>
+__global__ __launch_bounds__(128 * WAVES_N) void gemm_tile_kernel(const bf16* __restrict__ x, int64_t ldx,
+                                                             const bf16* __restrict__ w, const bf16* __restrict__ bias,
+                                                             bf16* __restrict__ y, int64_t ldy, int M, int N, int K,
+                                                             int tiles_m, int tiles_n, int per_xcd) {
+  constexpr int TTHREADS = 128 * WAVES_N;
+  constexpr int WTN = TN / WAVES_N, FN = WTN / 32;
+  constexpr int LPT_A = TM * CPR / TTHREADS;  // chunks per thread per stage (x)
+  constexpr int LPT_B = TN * CPR / TTHREADS;  // (W)
+  extern __shared__ __attribute__((aligned(16))) char lds[];
+  const int b = blockIdx.x;
+  const int local = b >> 3;
+  const int t = (b & 7) * per_xcd + local;
+  if (local >= per_xcd || t >= tiles_m * tiles_n) return;
+  const int group = t / (GROUP_M * tiles_n);
+  const int first_m = group * GROUP_M;
+  const int gsz = min(tiles_m - first_m, GROUP_M);
+  const int in_group = t - group * GROUP_M * tiles_n;
+  const int tm = first_m + in_group % gsz, tn = in_group / gsz;
+  const int m0 = tm * TM;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+
+  // Rows of W this block streams: STORE, tile columns n0 .. n0 + 255; SWIGLU,
+  // per 64-row group g of the tile, 32 gate rows then the 32 matching up rows
+  // (output columns c0 + 32 g .. + 31, c0 = 128 tn), so a wave's two column
+  // fragments are a gate fragment and its up fragment.
+  auto w_row = [&](int r) -> int {
+    if (EPI == TILE_SWIGLU) {
+      const int g = r >> 6, within = r & 63, col = tn * 128 + g * 32 + (within & 31);
+      if (col >= N) return -1;
+      return within < 32 ? col : N + col;
+    }
+    const int n = tn * TN + r;
+    return n < N ? n : -1;
+  };
+
+  const __amdgpu_buffer_rsrc_t xr = tile_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
+  const int64_t w_rows = EPI == TILE_SWIGLU ? 2LL * N : (int64_t)N;
+  const __amdgpu_buffer_rsrc_t wr = tile_rsrc(w, (uint32_t)(w_rows * K * 2));
+
+  // per-thread load slots: chunk q = tid + i * 512 -> row q / CPR, chunk q % CPR
+  uint32_t a_base[LPT_A], b_base[LPT_B];
+  int a_lds[LPT_A], b_lds[LPT_B], a_c[LPT_A], b_c[LPT_B];
+#pragma unroll
+  for (int i = 0; i < LPT_A; ++i) {
+    const int q = tid + i * TTHREADS, r = q / CPR, c = q % CPR;
+    a_base[i] = m0 + r < M ? (uint32_t)(((int64_t)(m0 + r) * ldx + c * 8) * 2) : OOB_OFF;
+    a_lds[i] = lds_off(r, c);
+    a_c[i] = c * 8;
+  }
+#pragma unroll
+  for (int i = 0; i < LPT_B; ++i) {
+    const int q = tid + i * TTHREADS, r = q / CPR, c = q % CPR;
+    const int wrow = w_row(r);
+    b_base[i] = wrow >= 0 ? (uint32_t)(((int64_t)wrow * K + c * 8) * 2) : OOB_OFF;
+    b_lds[i] = A_BYTES + lds_off(r, c);
+    b_c[i] = c * 8;
+  }
+
+  // The NCH 16-byte chunks a thread moves per K step: 0 .. LPT_A - 1 of x,
+  // the rest of W; one register each.
+  constexpr int NCH = LPT_A + LPT_B;
+  uint4 rr[NCH];
+  auto load_chunk = [&](int i, int kstep) {
+    const int k0 = kstep * TK;
+    if (i < LPT_A) {
+      const bool ok = a_base[i] != OOB_OFF && k0 + a_c[i] < K;
+      rr[i] = tile_load16(xr, ok ? a_base[i] + (uint32_t)k0 * 2 : OOB_OFF);
+    } else {
+      const int j = i - LPT_A;
+      const bool ok = b_base[j] != OOB_OFF && k0 + b_c[j] < K;
+      rr[i] = tile_load16(wr, ok ? b_base[j] + (uint32_t)k0 * 2 : OOB_OFF);
+    }
+  };
+  auto stash_chunk = [&](int i, char* stage) {
+    *(uint4*)(stage + (i < LPT_A ? a_lds[i] : b_lds[i - LPT_A])) = rr[i];
+  };
+
+  f32x16_g acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.f;
+
+  // fragment rows this lane reads
+  const int ar0 = wm * WTM + (lane & 31), br0 = wn * WTN + (lane & 31);
+  const int half = lane >> 5;
+
+  // K step kt: the MFMAs read stage kt % 2; the registers hold step kt + 1,
+  // written to the other stage two chunks per 16-wide substep, and each
+  // freed register takes the same chunk of step kt + 2. Fragment reads run
+  // one substep ahead of the MFMAs that use them (two register sets). The
+  // stage writes and global loads sit between the two halves of a substep's
+  // MFMAs, so the matrix pipe has work queued while they issue; one barrier
+  // per step.
+  const int nk = (K + TK - 1) / TK;
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) load_chunk(i, 0);
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) stash_chunk(i, lds);
+#pragma unroll
+  for (int i = 0; i < NCH; ++i) load_chunk(i, 1);
+  __syncthreads();
+  constexpr int KS = TK / 16;              // MFMA k substeps per step
+  constexpr int CH_PER_KS = NCH / KS;      // chunks moved per substep
+  static_assert(NCH % KS == 0, "chunks must split evenly over the substeps");
+  for (int kt = 0; kt < nk; ++kt) {
+    const char* sa = lds + (kt & 1) * STAGE_BYTES;
+    const char* sb = sa + A_BYTES;
+    char* nxt = lds + ((kt + 1) & 1) * STAGE_BYTES;
+    bf16x8_g av[2][FM], bv[2][FN];
+    auto fetch = [&](int ks, bf16x8_g(&a)[FM], bf16x8_g(&bb)[FN]) {
+      const int c = ks * 2 + half;
+#pragma unroll
+      for (int i = 0; i < FM; ++i) a[i] = *(const bf16x8_g*)(sa + lds_off(ar0 + i * 32, c));
+#pragma unroll
+      for (int j = 0; j < FN; ++j) bb[j] = *(const bf16x8_g*)(sb + lds_off(br0 + j * 32, c));
+    };
+    fetch(0, av[0], bv[0]);
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks) {
+      if (ks + 1 < KS) fetch(ks + 1, av[(ks + 1) & 1], bv[(ks + 1) & 1]);
+#pragma unroll
+      for (int i = 0; i < FM / 2; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[ks & 1][i], bv[ks & 1][j], acc[i][j], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+      // unconditional: past the last step the loads read zeros (K bound) and
+      // land in a stage nothing reads, and the loop stays one basic block, so
+      // the compiler's load counting waits only for the chunk it stores
+#pragma unroll
+      for (int q = 0; q < CH_PER_KS; ++q) stash_chunk(ks * CH_PER_KS + q, nxt);
+#pragma unroll
+      for (int q = 0; q < CH_PER_KS; ++q) load_chunk(ks * CH_PER_KS + q, kt + 2);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = FM / 2; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[ks & 1][i], bv[ks & 1][j], acc[i][j], 0, 0, 0);
+    }
+    __syncthreads();
+  }
+
+  // epilogue: lane holds column (lane % 32) of rows 8 (r / 4) + 4 half + r % 4
+  const int row_base = m0 + wm * WTM + 4 * half;
+  if (EPI == TILE_SWIGLU) {
+    // column fragments 2p (gate) and 2p + 1 (up) of 64-row group wn (WTN / 64) + p
+#pragma unroll
+    for (int pr = 0; pr < FN / 2; ++pr) {
+      const int col = tn * 128 + (wn * (WTN / 64) + pr) * 32 + (lane & 31);
+      if (col >= N) continue;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = row_base + i * 32 + 8 * (r >> 2) + (r & 3);
+          if (row < M) {
+            const float g = round_to<bf16>(acc[i][2 * pr][r]), u = round_to<bf16>(acc[i][2 * pr + 1][r]);
+            y[(int64_t)row * ldy + col].bits = f32_to_bf16(swiglu<bf16>(g, u));
+          }
+        }
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < FN; ++j) {
+      const int col = tn * TN + wn * WTN + j * 32 + (lane & 31);
+      if (col >= N) continue;
+      const float bv = bias != nullptr ? bf16_to_f32(bias[col].bits) : 0.f;
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int row = row_base + i * 32 + 8 * (r >> 2) + (r & 3);
+          if (row < M) y[(int64_t)row * ldy + col].bits = f32_to_bf16(acc[i][j][r] + bv);
+        }
+    }
+  }
+}
+
+template <int EPI>
+int launch_tile(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy,
+                int64_t M, int64_t N, int64_t K) {
+  constexpr int WN = MINITP_TILE_WAVES_N;
+  const void* kern = (const void*)gemm_tile_kernel<EPI, WN>;
+  if (const int rc = ensure_lds_limit(kern, LDS_TILE_BYTES)) return rc;
+  const int tiles_m = (int)cdiv(M, TM);
+  const int tiles_n = (int)cdiv(N, EPI == TILE_SWIGLU ? TN / 2 : TN);
+  const int tiles = tiles_m * tiles_n;
+  const int per_xcd = (tiles + 7) / 8;
+  hipLaunchKernelGGL((gemm_tile_kernel<EPI, WN>), dim3((unsigned)(8 * per_xcd)), dim3(128 * WN), LDS_TILE_BYTES, st,
+                     (const bf16*)x, ldx, (const bf16*)w, (const bf16*)bias, (bf16*)y, ldy, (int)M, (int)N, (int)K,
+                     tiles_m, tiles_n, per_xcd);
+  MINITP_LAUNCH_CHECK();
+  return MINITP_OK;
+}
+
+}  // namespace
+
+bool gemm_tile_supported(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, bool swiglu) {
+  const int64_t w_rows = swiglu ? 2 * N : N;
+  const int64_t tiles = cdiv(M, TM) * cdiv(N, swiglu ? TN / 2 : TN);
+  return M >= TM && tiles >= 96 && K % 8 == 0 && ldx % 8 == 0 && ldx >= K && ldy >= N && M < (1LL << 31) &&
+         N < (1LL << 30) && ((M - 1) * ldx + K) * 2 < (1LL << 32) && w_rows * K * 2 < (1LL << 32);
+}
+
+int launch_gemm_tile(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy,
+                     int64_t M, int64_t N, int64_t K, bool swiglu) {
+  if (!gemm_tile_supported(M, N, K, ldx, ldy, swiglu) || !aligned16(x) || !aligned16(w)) {
+    set_error("gemm_tile: shape M=%lld N=%lld K=%lld (ldx %lld) not served", (long long)M, (long long)N, (long long)K,
+              (long long)ldx);
+    return MINITP_ERR_UNSUPPORTED;
+  }
+  if (swiglu) return launch_tile<TILE_SWIGLU>(st, x, ldx, w, nullptr, y, ldy, M, N, K);
+  return launch_tile<TILE_STORE>(st, x, ldx, w, bias, y, ldy, M, N, K);
+}
+
+}  // namespace minitp

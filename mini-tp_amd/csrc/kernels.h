@@ -94,6 +94,14 @@ int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const voi
                 int64_t ldy, int64_t M, int64_t N, int64_t K, int epi, const void* aux,
                 const StepState* state = nullptr, void* ws = nullptr, int64_t ws_bytes = 0);
 
+// gemm_tile.hip: 256 x 256 MFMA tiles (32x32x16 bf16) for prompt-sized
+// bf16 products; swiglu: W is [2N, K] = [gate; up] and y = silu(gate) * up
+// [M, N]. MINITP_ERR_UNSUPPORTED for shapes it does not serve (too few
+// tiles, operands past 4 GiB, unaligned rows).
+bool gemm_tile_supported(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, bool swiglu);
+int launch_gemm_tile(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy,
+                     int64_t M, int64_t N, int64_t K, bool swiglu);
+
 // elementwise.hip
 int launch_fill_normal(hipStream_t st, int dtype, void* dst, int64_t count, uint64_t seed, uint64_t sid,
                        double std_dev);
@@ -109,6 +117,9 @@ int launch_silu_mul(hipStream_t st, int dtype, const void* gate, const void* up,
 int launch_cast_f32_bf16(hipStream_t st, const float* in, void* out, int64_t n);
 int launch_add_rmsnorm(hipStream_t st, int dtype, void* x, const void* delta, const void* w, void* out, int64_t rows,
                        int64_t hidden, float eps);
+// MINITP_GEMM=blaslt in the environment: prompt GEMMs on hipBLASLt (a
+// benchmark comparison; the product path runs the library's own kernels)
+bool blaslt_requested();
 // hipBLASLt bf16 y = x W^T (+ bias) for prompt-sized M outside stream capture;
 // MINITP_ERR_UNSUPPORTED when it does not apply (the caller then runs launch_gemm)
 int blaslt_linear_bf16(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y,

@@ -200,16 +200,22 @@ struct Qwen2Program {
     const bool fz = fused(M);
     AttnShape as{(int)B, (int)T, c.heads, c.kv_heads, D, s.max_seq};
     const int64_t layer_elems = B * c.kv_heads * s.max_seq * D;
-    // bf16 prompts (outside stream capture) run their plain GEMMs on
-    // hipBLASLt. The residual adds then go with the next RMSNorm (one fused
-    // kernel, the reference's rounding order), the projections that feed
-    // them writing into the normed-input buffer h, free at that point.
+    // bf16 prompts: plain GEMMs (the 256 x 256 MFMA tile kernel where the
+    // shape fills the chip, else the split-K one), gate/up with SwiGLU in
+    // the tile kernel's epilogue. The residual adds go with the next RMSNorm
+    // (one fused kernel, the reference's rounding order), the projections
+    // that feed them writing into the normed-input buffer h, free at that
+    // point. MINITP_GEMM=blaslt runs the plain GEMMs on hipBLASLt instead
+    // (outside stream capture only): a comparison for the benchmark, not
+    // the product path.
+    const bool blas = c.dtype == MINITP_BF16 && !fz && T > 1;
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    const bool blas = c.dtype == MINITP_BF16 && !fz && T > 1 && hipStreamIsCapturing(st, &cap) == hipSuccess &&
-                      cap == hipStreamCaptureStatusNone;
+    const bool use_blaslt = blas && blaslt_requested() && hipStreamIsCapturing(st, &cap) == hipSuccess &&
+                            cap == hipStreamCaptureStatusNone;
     auto lin = [&](const void* xin, int64_t ldx, const void* wt, const void* b, void* y, int64_t ldy, int64_t n,
                    int64_t k) -> int {
-      int r = blaslt_linear_bf16(st, xin, ldx, wt, b, y, ldy, M, n, k, w.gemm_ws, GEMM_WS_BYTES);
+      int r = use_blaslt ? blaslt_linear_bf16(st, xin, ldx, wt, b, y, ldy, M, n, k, w.gemm_ws, GEMM_WS_BYTES)
+                         : MINITP_ERR_UNSUPPORTED;
       if (r == MINITP_ERR_UNSUPPORTED)
         r = launch_gemm(st, c.dtype, xin, ldx, wt, b, y, ldy, M, n, k, MINITP_EPI_NONE, nullptr, nullptr, w.gemm_ws,
                         GEMM_SPLIT_BYTES);
@@ -229,9 +235,13 @@ struct Qwen2Program {
         if ((rc = launch_prefill_attention(st, c.dtype, w.q, kc, vc, w.attn, as, s.cache_len))) return rc;
         if ((rc = lin(w.attn, q_rows(), L(l, MINITP_W_O), nullptr, w.h, H, H, q_rows()))) return rc;
         if ((rc = launch_add_rmsnorm(st, c.dtype, w.x, w.h, L(l, MINITP_W_LN2), w.h, M, H, c.eps))) return rc;
-        if ((rc = lin(w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.gu, 2 * I, 2 * I, H))) return rc;
-        const char* up = (const char*)w.gu + I * es();
-        if ((rc = launch_silu_mul(st, c.dtype, w.gu, up, 2 * I, w.act, I, M, I))) return rc;
+        if (!use_blaslt && gemm_tile_supported(M, I, H, H, I, true)) {
+          if ((rc = launch_gemm_tile(st, w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.act, I, M, I, H, true))) return rc;
+        } else {
+          if ((rc = lin(w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.gu, 2 * I, 2 * I, H))) return rc;
+          const char* up = (const char*)w.gu + I * es();
+          if ((rc = launch_silu_mul(st, c.dtype, w.gu, up, 2 * I, w.act, I, M, I))) return rc;
+        }
         if ((rc = lin(w.act, I, L(l, MINITP_W_DOWN), nullptr, w.h, H, H, I))) return rc;
         const void* next_norm = l + 1 < c.num_layers ? L(l + 1, MINITP_W_LN1) : final_norm;
         if ((rc = launch_add_rmsnorm(st, c.dtype, w.x, w.h, next_norm, w.h, M, H, c.eps))) return rc;
@@ -366,8 +376,10 @@ struct Qwen2Program {
     }
     if (!blas && (rc = launch_rmsnorm(st, c.dtype, w.x, final_norm, w.h, M, H, c.eps))) return rc;
     if (s.logits_all) {  // (with blas, h already holds norm(x))
-      rc = blas ? blaslt_linear_bf16(st, w.h, H, lm_head, nullptr, s.logits, V, M, V, H, w.gemm_ws, GEMM_WS_BYTES)
-                : MINITP_ERR_UNSUPPORTED;
+      rc = use_blaslt ? blaslt_linear_bf16(st, w.h, H, lm_head, nullptr, s.logits, V, M, V, H, w.gemm_ws, GEMM_WS_BYTES)
+                      : MINITP_ERR_UNSUPPORTED;
+      if (rc == MINITP_ERR_UNSUPPORTED && blas && gemm_tile_supported(M, V, H, H, V, false))
+        rc = launch_gemm_tile(st, w.h, H, lm_head, nullptr, s.logits, V, M, V, H, false);
       if (rc == MINITP_ERR_UNSUPPORTED)
         rc = launch_gemm(st, c.dtype, w.h, H, lm_head, nullptr, nullptr, V, M, V, H, MINITP_EPI_NONE, nullptr, w.st);
       if (rc) return rc;
