@@ -205,7 +205,7 @@ int minitp_rmsnorm_linear(void* stream, int dtype, const void* x, int64_t ldx, c
   if (rc || M == 0 || N == 0) return rc;
   MINITP_CHECK_ARG(norm_w != nullptr, "rmsnorm_linear: NULL norm weight");
   MINITP_CHECK_ARG(epilogue != MINITP_EPI_RESID || aux != x, "rmsnorm_linear: RESID aux must not alias x");
-  if (!gemv_supported(dtype, M, K)) {
+  if (!gemv_norm_supported(dtype, M, K)) {
     set_error("rmsnorm_linear: M=%lld K=%lld is not a decode shape; use minitp_rmsnorm + minitp_linear",
               (long long)M, (long long)K);
     return MINITP_ERR_UNSUPPORTED;

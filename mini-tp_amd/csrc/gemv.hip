@@ -19,6 +19,7 @@
 // LDS staging, no barrier unless K is split across waves); and each tuple
 // prefetches the next tuple's weights before its own reduction and epilogue.
 // gemv_lds_kernel stages the input in LDS and serves longer rows.
+// gemv_mfma_kernel serves bf16 decode batches of 5 to 32 rows on MFMA.
 #include "common.h"
 #include "kernels.h"
 
@@ -743,6 +744,316 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvArgs a) {
 }
 
 
+// ---------------------------------------------------------------------------
+// Decode rows 5..32 (bf16) on MFMA. The same tuples and epilogues as the
+// register GEMV, with 16 weight rows per tuple: rows ra + 0..7 and rb + 0..7
+// (pairs (ra + p, rb + p): SwiGLU gate j / up I + j, RoPE dims i / i + D/2,
+// plain rows t*16 + p / t*16 + 8 + p). A wave owns one tuple and a K range
+// (KSPLIT waves share a tuple and add their sums in a fixed order), and runs
+// v_mfma_f32_16x16x32_bf16 with the input rows as the A operand (rows 0-15 and
+// 16-31: two fragments; lane l reads x[l % 16][8 (l / 16) + 0..7] straight
+// from memory) and the weights as B (lane l reads 16 bytes of tuple row
+// l % 16). Lane l's accumulator r is then (row 4 (l / 16) + r, tuple row
+// l % 16), so the pair partner of a result sits in lane l ^ 8. The RMSNorm
+// prologue computes each input row's scale from the block's K-split partial
+// sums and normalizes the A fragments in registers (layer.py:39-42).
+constexpr int P16 = 8;  // pairs per 16-row tuple
+
+template <int EPI>
+__device__ __forceinline__ void tuple16_rows(int64_t t, const GemvArgs& a, int64_t& ra, int64_t& rb) {
+  if constexpr (EPI == EPI_SWIGLU) {
+    ra = t * P16;
+    rb = a.N + t * P16;
+  } else if constexpr (is_qkv<EPI>()) {
+    const int half = a.a.D / 2;
+    const int per_head = half / P16;
+    const int64_t head = t / per_head;
+    ra = head * a.a.D + (t % per_head) * P16;
+    rb = ra + half;
+  } else {
+    ra = t * 2 * P16;
+    rb = ra + P16;
+  }
+}
+
+template <int EPI>
+__host__ __device__ __forceinline__ int64_t num_tuples16(const GemvArgs& a) {
+  if constexpr (EPI == EPI_SWIGLU) return a.N / P16;
+  if constexpr (is_qkv<EPI>()) return (int64_t)(a.a.Hq + 2 * a.a.Hkv) * (a.a.D / 2) / P16;
+  return cdiv(a.N, 2 * P16);
+}
+
+typedef __bf16 bf16x8_m __attribute__((ext_vector_type(8)));
+typedef float f32x4_m __attribute__((ext_vector_type(4)));
+
+// One k step's A fragments normalized in registers: o = dtype((x * r) * w).
+__device__ __forceinline__ uint4 norm_chunk(const uint4& xb, const uint4& wb, float r) {
+  float xf[8], wf[8], o[8];
+  unpack16(xb, xf, (bf16*)nullptr);
+  unpack16(wb, wf, (bf16*)nullptr);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = mul_rn(mul_rn(xf[e], r), wf[e]);
+  return pack_bf16x8(o);
+}
+
+template <int PRO, int EPI, int KSPLIT, int NT, int NB, bool MULTI>
+__global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
+  // A wave owns NT tuples that share each A fragment it loads, over a K
+  // range of steps of 32. !MULTI: the range fits one batch of NB steps and
+  // every load (weights, input rows, norm weight) goes out at once, so the
+  // kernel waits one memory round trip; the RMSNorm scale comes from the
+  // same input registers. MULTI: batches of NB steps, each batch's loads
+  // issued while the previous one is multiplied (no norm prologue).
+  constexpr int SLOTS = 4 / KSPLIT;
+  constexpr uint32_t OOBW = 0xffffffffu;
+  static_assert(!(MULTI && PRO == PRO_NORM), "the norm prologue needs the K range in one batch");
+  __shared__ float nrm[4][32];
+  __shared__ f32x4_m red[4][NT][2][64];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int kw = wave % KSPLIT, slot = wave / KSPLIT;
+  const int M = (int)a.M;
+  const int64_t K = a.K;
+  const int64_t t0 = ((int64_t)blockIdx.x * SLOTS + slot) * NT;
+  const int64_t ntup = num_tuples16<EPI>(a);
+  const int nidx = lane & 15, kq = lane >> 4;
+  const int64_t w_rows = EPI == EPI_SWIGLU ? 2 * a.N : a.N;
+  // whole-matrix resources; lane offsets past a row's K or past M read zeros
+  const __amdgpu_buffer_rsrc_t wr = span_rsrc(a.w, (uint32_t)(w_rows * K * 2));
+  const __amdgpu_buffer_rsrc_t xr = span_rsrc(a.x, (uint32_t)(((int64_t)(M - 1) * a.ldx + K) * 2));
+  const __amdgpu_buffer_rsrc_t nr = span_rsrc(a.norm_w, PRO == PRO_NORM ? (uint32_t)(K * 2) : 0u);
+  int64_t ra[NT], rb[NT];
+  uint32_t wbase[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const bool live = t0 + j < ntup;
+    ra[j] = rb[j] = 0;
+    if (live) tuple16_rows<EPI>(t0 + j, a, ra[j], rb[j]);
+    const int64_t wrow = nidx < P16 ? ra[j] + nidx : rb[j] + (nidx - P16);
+    wbase[j] = live && row_valid<EPI>(wrow, a) ? (uint32_t)(wrow * K * 2) : OOBW;
+  }
+  const int m0 = nidx, m1 = 16 + nidx;
+  const uint32_t xb0 = m0 < M ? (uint32_t)((int64_t)m0 * a.ldx * 2) : OOBW;
+  const uint32_t xb1 = m1 < M ? (uint32_t)((int64_t)m1 * a.ldx * 2) : OOBW;
+  const int64_t nsteps = cdiv(K, 32), per = cdiv(nsteps, KSPLIT);
+  const int64_t s_begin = kw * per, s_end = std::min(nsteps, s_begin + per);
+  auto off = [&](uint32_t base, int64_t s) -> uint32_t {
+    const int64_t k = s * 32 + kq * 8;
+    return (base != OOBW && s < s_end && k < K) ? base + (uint32_t)(k * 2) : OOBW;
+  };
+  struct Batch {
+    uint4 w[NB][NT], xa[NB], xc[NB], nw[NB];
+  };
+  auto issue = [&](Batch& b, int64_t s0) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) b.w[i][j] = span_load16<W_AUX>(wr, off(wbase[j], s0 + i));
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      b.xa[i] = span_load16<0>(xr, off(xb0, s0 + i));
+      b.xc[i] = span_load16<0>(xr, off(xb1, s0 + i));
+      if constexpr (PRO == PRO_NORM) b.nw[i] = span_load16<0>(nr, off(0u, s0 + i));
+    }
+  };
+  f32x4_m acc[NT][2];
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) acc[j][h] = f32x4_m{0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](Batch& b) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const bf16x8_m aa = __builtin_bit_cast(bf16x8_m, b.xa[i]), ac = __builtin_bit_cast(bf16x8_m, b.xc[i]);
+#pragma unroll
+      for (int j = 0; j < NT; ++j) {
+        const bf16x8_m bw = __builtin_bit_cast(bf16x8_m, b.w[i][j]);
+        acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aa, bw, acc[j][0], 0, 0, 0);
+        acc[j][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac, bw, acc[j][1], 0, 0, 0);
+      }
+    }
+  };
+
+  Batch b0;
+  issue(b0, s_begin);
+  // the epilogue's side inputs (residual, QKV bias, the single-token RoPE
+  // rows) load now, underneath the weights, not after the products: lane
+  // l < 8 of a K-split leader finishes pair l of each tuple for rows
+  // 4 (l / 16) + r and 16 + 4 (l / 16) + r
+  constexpr int NSIDE = EPI == EPI_RESID ? 16 : (EPI == EPI_QKV_ROPE1 ? 6 : (EPI == EPI_QKV_ROPE ? 2 : 1));
+  float sv[NT][NSIDE];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int p = nidx & (P16 - 1);
+    const int64_t row_a = ra[j] + p, row_b = rb[j] + p;
+    const bool oka = t0 + j < ntup && row_valid<EPI>(row_a, a), okb = t0 + j < ntup && row_valid<EPI>(row_b, a);
+#pragma unroll
+    for (int q = 0; q < NSIDE; ++q) sv[j][q] = 0.f;
+    if constexpr (EPI == EPI_RESID) {
+      const bf16* aux = (const bf16*)a.aux;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = h * 16 + 4 * kq + r;
+          const int mm = m < M ? m : 0;
+          sv[j][h * 8 + r] = load_f32<bf16>(aux, mm * a.ldy + (oka ? row_a : 0));
+          sv[j][h * 8 + 4 + r] = load_f32<bf16>(aux, mm * a.ldy + (okb ? row_b : 0));
+        }
+    } else if constexpr (is_qkv<EPI>()) {
+      sv[j][0] = load_f32<bf16>((const bf16*)a.bias, oka ? row_a : 0);
+      sv[j][1] = load_f32<bf16>((const bf16*)a.bias, okb ? row_b : 0);
+      if constexpr (EPI == EPI_QKV_ROPE1) {
+        const int D = a.a.D, i = (int)(row_a % D);
+        sv[j][2] = a.st->rope_cos[i];
+        sv[j][3] = a.st->rope_sin[i];
+        sv[j][4] = a.st->rope_cos[i + D / 2];
+        sv[j][5] = a.st->rope_sin[i + D / 2];
+      }
+    }
+  }
+  if constexpr (!MULTI) {
+    if constexpr (PRO == PRO_NORM) {
+      // sums of squares of this wave's K range (packed dots: exact products,
+      // fp32 sums), over the four lanes of a row (l, l + 16, l + 32, l + 48),
+      // then over the block's K-split waves in order
+      float ss0 = 0.f, ss1 = 0.f;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        ss0 = dot_chunk<bf16>(b0.xa[i], nullptr, b0.xa[i], ss0);
+        ss1 = dot_chunk<bf16>(b0.xc[i], nullptr, b0.xc[i], ss1);
+      }
+      ss0 += __shfl_xor(ss0, 16);
+      ss0 += __shfl_xor(ss0, 32);
+      ss1 += __shfl_xor(ss1, 16);
+      ss1 += __shfl_xor(ss1, 32);
+      if (kq == 0) {
+        nrm[wave][m0] = ss0;
+        nrm[wave][m1] = ss1;
+      }
+      __syncthreads();
+      float u0 = 0.f, u1 = 0.f;
+      for (int k = 0; k < KSPLIT; ++k) {
+        u0 += nrm[slot * KSPLIT + k][m0];
+        u1 += nrm[slot * KSPLIT + k][m1];
+      }
+      const float r0 = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(u0, (float)K), a.eps)));
+      const float r1 = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(u1, (float)K), a.eps)));
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        b0.xa[i] = norm_chunk(b0.xa[i], b0.nw[i], r0);
+        b0.xc[i] = norm_chunk(b0.xc[i], b0.nw[i], r1);
+      }
+    }
+    consume(b0);
+  } else {
+    Batch b1;
+    for (int64_t s0 = s_begin; s0 < s_end; s0 += 2 * NB) {
+      issue(b1, s0 + NB);
+      consume(b0);
+      if (s0 + 2 * NB < s_end) issue(b0, s0 + 2 * NB);
+      consume(b1);
+    }
+  }
+
+  if constexpr (KSPLIT > 1) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      red[wave][j][0][lane] = acc[j][0];
+      red[wave][j][1][lane] = acc[j][1];
+    }
+    __syncthreads();
+    if (kw == 0) {
+      for (int k = 1; k < KSPLIT; ++k)
+#pragma unroll
+        for (int j = 0; j < NT; ++j) {
+          acc[j][0] += red[wave + k][j][0][lane];
+          acc[j][1] += red[wave + k][j][1][lane];
+        }
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    float pa0[4], pa1[4];  // the pair partners' sums (lane l ^ 8)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      pa0[r] = __shfl_xor(acc[j][0][r], 8);
+      pa1[r] = __shfl_xor(acc[j][1][r], 8);
+    }
+    if (kw != 0 || t0 + j >= ntup || nidx >= P16) continue;
+    const int p = nidx;
+    const int64_t row_a = ra[j] + p, row_b = rb[j] + p;
+    const bool oka = row_valid<EPI>(row_a, a), okb = row_valid<EPI>(row_b, a);
+    float side[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    if constexpr (is_qkv<EPI>()) {
+      side[4] = sv[j][0];
+      side[5] = sv[j][1];
+    }
+    if constexpr (EPI == EPI_QKV_ROPE1) {
+      side[0] = sv[j][2];
+      side[1] = sv[j][3];
+      side[2] = sv[j][4];
+      side[3] = sv[j][5];
+    }
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int m = h * 16 + 4 * kq + r;
+        if (m >= M) continue;
+        const float va = acc[j][h][r], vb = h ? pa1[r] : pa0[r];
+        int64_t pos = 0;
+        if constexpr (EPI == EPI_QKV_ROPE) {
+          const int D = a.a.D, i = (int)(row_a % D);
+          pos = a.st->args.positions[m % a.a.T];
+          if (row_a / D < a.a.Hq + a.a.Hkv && pos >= 0 && pos < a.max_pos) {
+            side[0] = a.cos_tab[pos * D + i];
+            side[1] = a.sin_tab[pos * D + i];
+            side[2] = a.cos_tab[pos * D + i + D / 2];
+            side[3] = a.sin_tab[pos * D + i + D / 2];
+          }
+        } else if constexpr (EPI == EPI_RESID) {
+          side[0] = sv[j][h * 8 + r];
+          side[1] = sv[j][h * 8 + 4 + r];
+        }
+        finish_pair<bf16, EPI>(a, m, row_a, row_b, oka, okb, va, vb, side, pos);
+      }
+  }
+}
+
+// steps of 32 per wave that one batch holds (the whole K range of a wave
+// when it fits: the norm prologue needs that)
+constexpr int MF_ONE = 8;
+
+template <int PRO, int EPI, int NT>
+int launch_mfma_nt(hipStream_t st, const GemvArgs& a, int64_t ntup) {
+  const unsigned grid = (unsigned)cdiv(ntup, NT);
+  const int64_t per_wave = cdiv(cdiv(a.K, 32), 4);
+  if (per_wave <= MF_ONE) {
+    hipLaunchKernelGGL((gemv_mfma_kernel<PRO, EPI, 4, NT, MF_ONE, false>), dim3(grid), dim3(256), 0, st, a);
+  } else if constexpr (PRO == PRO_NORM) {
+    set_error("gemv: the RMSNorm prologue on MFMA serves K <= %d", 4 * 32 * MF_ONE);
+    return MINITP_ERR_UNSUPPORTED;
+  } else {
+    hipLaunchKernelGGL((gemv_mfma_kernel<PRO, EPI, 4, NT, 4, true>), dim3(grid), dim3(256), 0, st, a);
+  }
+  MINITP_LAUNCH_CHECK();
+  return MINITP_OK;
+}
+
+template <int PRO, int EPI>
+int launch_mfma(hipStream_t st, const GemvArgs& a) {
+  if constexpr (EPI == EPI_ARGMAX) {
+    set_error("gemv: the argmax epilogue serves at most 4 rows");
+    return MINITP_ERR_UNSUPPORTED;
+  } else {
+    // K split over the block's 4 waves; many tuples: 2 per wave (the input
+    // rows read once per 32 weight rows), few: 1 per wave (more blocks)
+    const int64_t ntup = num_tuples16<EPI>(a);
+    if (ntup >= 512) return launch_mfma_nt<PRO, EPI, 2>(st, a, ntup);
+    return launch_mfma_nt<PRO, EPI, 1>(st, a, ntup);
+  }
+}
+
 template <typename T, int MM, int KSPLIT, int JMAX, int PRO, int EPI>
 int launch_reg(hipStream_t st, const GemvArgs& a) {
   const int64_t slots = 4 / KSPLIT;
@@ -783,6 +1094,9 @@ int pick_k(hipStream_t st, const GemvArgs& a) {
 
 template <typename T, int PRO, int EPI>
 int pick_m(hipStream_t st, const GemvArgs& a) {
+  if constexpr (sizeof(T) == 2) {
+    if (a.M > 4) return launch_mfma<PRO, EPI>(st, a);
+  }
   if (a.M == 1) return pick_k<T, 1, PRO, EPI>(st, a);
   if (a.M == 2) return pick_k<T, 2, PRO, EPI>(st, a);
   return pick_k<T, 4, PRO, EPI>(st, a);
@@ -816,11 +1130,20 @@ int64_t gemv_argmax_partials(int64_t N) { return std::min<int64_t>(cdiv(cdiv(N, 
 // that stages the input in LDS (up to 80 KiB). Other shapes run the GEMM.
 bool gemv_supported(int dtype, int64_t M, int64_t K) {
   const int v = dtype == MINITP_F32 ? 4 : 8;
+  // bf16 rows 5..32 run the MFMA form (K a multiple of 8, rows under 2 GiB)
+  if (dtype == MINITP_BF16 && M >= 5 && M <= 32) return K % v == 0 && K * 2 < (1LL << 31);
   if (M < 1 || M > 4 || K % v != 0) return false;
   const int64_t nchunk = K / v;
   if (nchunk <= 128) return true;
   if (nchunk <= REG_MAX_CHUNKS) return M <= 2;
   return M == 1 && K * 4 <= 80 * 1024;
+}
+
+// The RMSNorm prologue holds a wave's whole K range: on the MFMA form (bf16
+// rows 5..32) that is K <= 4 waves x 8 steps x 32.
+bool gemv_norm_supported(int dtype, int64_t M, int64_t K) {
+  if (!gemv_supported(dtype, M, K)) return false;
+  return M <= 4 || K <= 4 * 32 * MF_ONE;
 }
 
 int launch_gemv(hipStream_t st, int dtype, int pro, int epi, const GemvArgs& a) {

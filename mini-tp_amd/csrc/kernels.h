@@ -80,6 +80,8 @@ struct GemvArgs {
 int64_t gemv_argmax_partials(int64_t N);
 int launch_gemv(hipStream_t st, int dtype, int pro, int epi, const GemvArgs& a);
 bool gemv_supported(int dtype, int64_t M, int64_t K);
+// ... and with the RMSNorm prologue (PRO_NORM)
+bool gemv_norm_supported(int dtype, int64_t M, int64_t K);
 
 // gemm.hip: y[M, N] = epilogue(x[M, K] W[N, K]^T (+ bias)), MFMA tiles.
 // When `state` is non-null the output base is state->logits (graph replays).

@@ -171,7 +171,7 @@ struct Qwen2Program {
   }
 
   bool fused(int64_t M) const {
-    return gemv_supported(c.dtype, M, c.hidden) && gemv_supported(c.dtype, M, c.intermediate) &&
+    return gemv_norm_supported(c.dtype, M, c.hidden) && gemv_supported(c.dtype, M, c.intermediate) &&
            gemv_supported(c.dtype, M, q_rows());
   }
 
@@ -317,6 +317,15 @@ struct Qwen2Program {
         g.N = I;
         g.K = H;
         if ((rc = launch_gemv(st, c.dtype, PRO_NORM, EPI_SWIGLU, g))) return rc;
+        if (M > 4) {
+          // 5..32 rows: the long-K down projection keeps the split-K GEMM (its
+          // K splits over blocks keep more weight bytes in flight than the
+          // MFMA GEMV's 56 tuples of 16 rows can)
+          if ((rc = launch_gemm(st, c.dtype, w.act, I, L(l, MINITP_W_DOWN), nullptr, w.x, H, M, H, I, MINITP_EPI_RESID,
+                                w.x, nullptr, w.gemm_ws, GEMM_SPLIT_BYTES)))
+            return rc;
+          continue;
+        }
         GemvArgs d{};
         d.x = w.act;
         d.ldx = I;
