@@ -106,6 +106,9 @@ def parse(argv=None):
     ap.add_argument("--decode-only", type=int, default=0, metavar="TOKENS",
                     help="only run one generation of the headline workload with TOKENS new tokens after a warm-up "
                          "one and exit: the workload of the decode kernel profiles")
+    ap.add_argument("--eager-decode", type=int, default=0, metavar="STEPS",
+                    help="prefill the --workload's prompt, then run STEPS decode steps as eager launches (no graph, "
+                         "no persistent kernel) and exit: the workload of the per-kernel counter passes")
     return ap.parse_args(argv)
 
 
@@ -222,6 +225,34 @@ def p50(xs: list[float]) -> float:
 
 # ---------------------------------------------------------------------------
 # the other workloads
+
+
+def eager_decode(name: str, steps: int) -> dict:
+    """Prefill one workload's prompt (last-position logits), then `steps`
+    T = 1 forwards through the native program launched eagerly, each
+    feeding back its greedy pick: the same kernels as the decode graph, one
+    dispatch at a time, so counter profilers see every launch."""
+    import torch
+
+    from minitp import kernels as K
+    from minitp import synthetic
+    from minitp.generation import make_kv_cache
+
+    shape, batch, plen, _ = ("QWEN05B", 1, PROMPT_LEN, NEW_TOKENS) if name == "q05b" else WORKLOADS[name]
+    cfg = getattr(synthetic, shape)
+    model = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device="cuda", seed=0)
+    prompt = synthetic.synthetic_prompt(cfg.vocab_size, batch, plen, seed=0, device="cuda")
+    kv = make_kv_cache(model, batch, plen + steps)
+    logits = model._native(prompt, torch.arange(plen, device="cuda"), kv, last_only=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        tok = K.argmax(logits[:, -1]).view(batch, 1)
+        logits = model(tok, kv_cache=kv)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    return {"workload": name, "eager_steps": steps, "contexts": [plen + 1, plen + steps],
+            "ms_per_step": round(dt * 1e3 / max(steps, 1), 4)}
 
 
 def measure_workload(name: str, model=None) -> dict:
@@ -602,6 +633,12 @@ def main(argv=None):
         return
     if args.gemm:
         gemm_alone(args.gemm)
+        return
+    if args.eager_decode:
+        if args.workload == "q7b-prefill":
+            raise SystemExit("--eager-decode needs a decode workload (q05b, q7b, q05b-b32)")
+        with torch.inference_mode():
+            print(json.dumps(eager_decode(args.workload, args.eager_decode)), flush=True)
         return
     if args.workload != "q05b":
         with torch.inference_mode():

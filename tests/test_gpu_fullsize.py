@@ -2,18 +2,24 @@
 through properties that do not need the oracle to run at that size.
 
 The model is the Qwen2.5-7B layer shape with 2 layers and the untied
-152,064-row head (the oracle covers the same shapes at small sizes); the last
-test does the same for the batch-32 decode workload's shapes. At 4 x
-4096 the prompt runs the long-prompt attention kernel, hipBLASLt GEMMs at
-M = 16,384 and the 16-byte elementwise kernels, so these properties exercise
-exactly the full-size path:
+152,064-row head (the oracle covers the same shapes at small sizes); the
+batch-32 tests do the same for the batch-32 decode workload's shapes. At 4 x
+4096 the prompt runs the long-prompt attention kernel, the 256 x 256 MFMA tile
+GEMMs at M = 16,384 and the 16-byte elementwise kernels, so these properties
+exercise exactly the full-size path:
 
 * the whole-prompt prefill's last-position logits equal those of a prefill of
   the first 4,095 tokens followed by one decode step of the last token (the
   decode attention and GEMV path over the 4,095 cached rows);
 * a prefill in two chunks of 2,048 (the second attending over the first
   through the cache offset, positions 2,048 .. 4,095 given explicitly) gives
-  the same last-position logits and the same cache rows as the whole prompt.
+  the same last-position logits and the same cache rows as the whole prompt;
+* over a whole generation's contexts: every position of a 768-token 7B prompt
+  (the 512 + 256 decode workload, contexts 513 .. 768) and checkpoints up to
+  context 2,559 of the batch-32 workload (2,048 + 512) give the same logits
+  from one whole-prompt prefill as from a prefill of the first part followed
+  by one teacher-forced decode step per remaining token, on every decode
+  form that serves the batch.
 
 Bars: the bf16 logit bar of the model tests (0.5 abs); for layer 0's cache
 rows a few bf16 steps (3e-2 + |value| / 32: the two prompts run the QKV GEMM
@@ -117,3 +123,80 @@ def test_batch32_long_prompt_last_row_equals_prefill_then_decode():
     print(f"32 x 2048: whole-prompt vs prefill(2047) + decode: max |logit diff| {err:.4f}")
     assert torch.isfinite(whole).all() and torch.isfinite(step).all() and err <= BF16_LOGIT_ATOL
 
+
+
+def _teacher_forced(model, prompt, start, check):
+    """Prefill prompt[:, :start], then decode prompt[:, start:] one token per
+    step; ``check(pos, logits)`` gets each step's [B, V] logits, the prefill's
+    last row included (pos = start - 1)."""
+    from minitp.generation import GenerationState
+
+    t = prompt.shape[1]
+    st = GenerationState(model, prompt[:, :start], t - start, prefill_logits="last")
+    check(start - 1, st.prefill()[:, -1])
+    for i in range(start, t):
+        tok = prompt[:, i].contiguous()
+        pos = st.append(tok)
+        check(i, st.decode_step(tok, pos)[:, 0])
+    assert st.kv.seq_len == t
+
+
+@pytest.mark.parametrize("path", ["graph", "persistent"])
+def test_7b_every_decode_context_equals_whole_prompt(path):
+    """7B shapes (2 layers, batch 1): the whole 768-token prompt's logits at
+    each position 511 .. 767 against prefill(512) plus 256 teacher-forced
+    decode steps (contexts 513 .. 768: the generation's 255 steps plus one)."""
+    from minitp import _native as N
+    from minitp import synthetic
+    from minitp.generation import GenerationState
+
+    cfg = dataclasses.replace(synthetic.QWEN7B, num_hidden_layers=2)
+    model = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device=DEV, seed=2)
+    prog = model.program()
+    prog.set_decode_path(N.DECODE_PERSISTENT if path == "persistent" else N.DECODE_GRAPH)
+    if path == "persistent" and not prog.persistent_ok():
+        pytest.skip(f"persistent decode not available for this shape: {N.last_error()}")
+    prompt = synthetic.synthetic_prompt(cfg.vocab_size, 1, 768, seed=7, device=DEV)
+    whole = GenerationState(model, prompt, 1, prefill_logits="all").prefill()[0].float()
+    assert whole.shape == (768, cfg.vocab_size) and torch.isfinite(whole).all()
+    errs = {}
+
+    def check(pos, logits):
+        assert torch.isfinite(logits).all(), pos
+        errs[pos] = (whole[pos] - logits[0].float()).abs().max().item()
+
+    with torch.inference_mode():
+        _teacher_forced(model, prompt, 512, check)
+    prog.check_decode()
+    worst = max(errs, key=errs.get)
+    print(f"7B {path}: {len(errs)} positions, max |logit diff| {errs[worst]:.4f} at position {worst}")
+    assert len(errs) == 257 and errs[worst] <= BF16_LOGIT_ATOL
+
+
+def test_batch32_decode_to_context_2559_equals_whole_prompts():
+    """0.5B shapes (2 layers), batch 32: prefill(2048) plus 511 teacher-forced
+    decode steps (contexts 2,049 .. 2,559) against whole-prompt prefills that
+    end at the checkpoints 2,048, 2,049, 2,304 and 2,559 (last rows)."""
+    from minitp import synthetic
+    from minitp.generation import GenerationState
+
+    cfg = dataclasses.replace(synthetic.QWEN05B, num_hidden_layers=2)
+    model = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device=DEV, seed=4)
+    prompt = synthetic.synthetic_prompt(cfg.vocab_size, 32, 2559, seed=9, device=DEV)
+    checkpoints = (2048, 2049, 2304, 2559)
+    whole = {}
+    for n in checkpoints:
+        whole[n - 1] = GenerationState(model, prompt[:, :n], 1, prefill_logits="last").prefill()[:, -1].float()
+        assert torch.isfinite(whole[n - 1]).all(), n
+    seen = []
+
+    def check(pos, logits):
+        if pos in whole:
+            err = (whole[pos] - logits.float()).abs().max().item()
+            print(f"batch 32, context {pos + 1}: max |logit diff| {err:.4f}")
+            assert torch.isfinite(logits).all() and err <= BF16_LOGIT_ATOL, pos
+            seen.append(pos)
+
+    with torch.inference_mode():
+        _teacher_forced(model, prompt, 2048, check)
+    assert seen == [n - 1 for n in checkpoints]
