@@ -32,6 +32,16 @@ constexpr int R = 2 * P;
 constexpr int U = 2;  // gemv_lds_kernel chunk unroll
 constexpr int MAX_GRID = 2048;
 constexpr int64_t REG_MAX_CHUNKS = 1024;
+// Split-K form: chunks per lane and row in one segment, and the row length
+// (in 16-byte chunks) above which single-row products take it.
+#ifndef MINITP_SPLIT_JMAX
+#define MINITP_SPLIT_JMAX 3
+#endif
+#ifndef MINITP_SPLIT_MIN_CHUNKS
+#define MINITP_SPLIT_MIN_CHUNKS 1024
+#endif
+constexpr int SPLIT_JMAX = MINITP_SPLIT_JMAX;
+constexpr int64_t SPLIT_MIN_CHUNKS = MINITP_SPLIT_MIN_CHUNKS;
 
 // EPI_QKV_ROPE of a single-token forward: the RoPE rows come from the
 // StepState, so the epilogue's side inputs need no position load first.
@@ -745,6 +755,124 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvArgs a) {
 
 
 // ---------------------------------------------------------------------------
+// gemv_split_kernel: M <= 4 rows with K split over blocks (no RMSNorm
+// prologue; plain, residual and SwiGLU epilogues). The grid is tuples x
+// segments: block b takes segment b % nseg (seg_bytes of every row) of tuple
+// b / nseg, so a long-K matrix is spread over many more blocks than it has
+// tuples and every block issues all of its loads at once (JMAX 16-byte
+// chunks per row per lane, input chunks beside them, no LDS stage). Each
+// block reduces its segment to one fp32 partial per (row, tuple row) and
+// stores it at device scope; one lane then counts the block in on the
+// tuple's arrival word (agent-scope acq_rel add). The block that arrives
+// last adds the nseg partials in segment order, the same sum whatever the
+// arrival order, runs the epilogue and puts the word back to 0 for the next
+// launch. No block ever waits for another.
+template <typename T, int MM, int JMAX, int EPI>
+__global__ __launch_bounds__(256) void gemv_split_kernel(GemvArgs a, int nseg, uint32_t seg_bytes) {
+  constexpr int V = Vec<T>::N;
+  __shared__ float red[4][MM * R];
+  __shared__ int last;
+  const int tid = threadIdx.x, lane = tid & 63, kw = tid >> 6;
+  const int M = (int)a.M;
+  const int64_t t = blockIdx.x / nseg;
+  const int seg = (int)(blockIdx.x % nseg);
+  const uint32_t row_bytes = (uint32_t)(a.K * (int64_t)sizeof(T));
+  const uint32_t seg0 = (uint32_t)seg * seg_bytes;
+  const uint32_t len = min(seg_bytes, row_bytes - seg0);
+
+  int64_t ra = 0, rb = 0;
+  tuple_rows<EPI>(t, a, ra, rb);
+  int64_t rows[R];
+  bool rok[R];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    rows[p] = ra + p;
+    rows[P + p] = rb + p;
+  }
+#pragma unroll
+  for (int r = 0; r < R; ++r) rok[r] = row_valid<EPI>(rows[r], a);
+
+  // lane l of wave kw reads chunks kw * 64 + l + 256 j of the segment; past
+  // its end (or the row's) the buffer loads return zeros
+  uint32_t coff[JMAX];
+#pragma unroll
+  for (int j = 0; j < JMAX; ++j) coff[j] = (uint32_t)((kw * 64 + lane + j * 256) * 16);
+  uint4 wv[JMAX][R];
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const __amdgpu_buffer_rsrc_t rs =
+        span_rsrc((const char*)a.w + (rok[r] ? rows[r] : 0) * (int64_t)row_bytes + seg0, rok[r] ? len : 0u);
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) wv[j][r] = span_load16<W_AUX>(rs, coff[j]);
+  }
+  uint4 xb[MM][JMAX];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    const __amdgpu_buffer_rsrc_t xr =
+        span_rsrc((const char*)a.x + (m < M ? m : 0) * a.ldx * (int64_t)sizeof(T) + seg0, m < M ? len : 0u);
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) xb[m][j] = span_load16<0>(xr, coff[j]);
+  }
+
+  float acc[MM][R];
+#pragma unroll
+  for (int m = 0; m < MM; ++m) {
+    float xf[JMAX][V];
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) unpack16(xb[m][j], xf[j], (T*)nullptr);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < JMAX; ++j) s = dot_chunk<T>(wv[j][r], xf[j], xb[m][j], s);
+      acc[m][r] = wave_sum(s);
+    }
+  }
+  if (lane == 0) {
+#pragma unroll
+    for (int m = 0; m < MM; ++m)
+#pragma unroll
+      for (int r = 0; r < R; ++r) red[kw][m * R + r] = acc[m][r];
+  }
+  __syncthreads();
+  // wave 0 publishes the block's partials, then counts the block in
+  float* part = a.split_part + (t * nseg + seg) * (MM * R);
+  if (kw == 0) {
+    if (lane < MM * R) {
+      const float v = ((red[0][lane] + red[1][lane]) + red[2][lane]) + red[3][lane];
+      __hip_atomic_store(part + lane, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // The partials are device-coherent stores (sc1); the wave waits for
+    // their completion (vmcnt(0)) before it counts the block in. This is
+    // what an agent-scope release does for atomic stores, without its L2
+    // write-back, which covers the whole cache and costs far more than the
+    // GEMV. The builtin's operand encodes vmcnt(0) expcnt(7) lgkmcnt(15).
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    if (lane == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(a.split_count + t, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = old == (uint32_t)(nseg - 1);
+      if (last) __hip_atomic_store(a.split_count + t, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+  if (!last || kw != 0) return;
+
+  // ---- the last block: segment sums in order, then the epilogue -----------
+  // (device-coherent loads, issued after every count was seen)
+  const int em = lane / P, ep = lane % P;
+  if (em >= M) return;
+  const float* tp = a.split_part + t * nseg * (MM * R);
+  float va = 0.f, vb = 0.f;
+  for (int s = 0; s < nseg; ++s) {
+    va += __hip_atomic_load(tp + s * (MM * R) + em * R + ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    vb += __hip_atomic_load(tp + s * (MM * R) + em * R + P + ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  float side[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  load_side<T, EPI>(a, em, ep, rows, rok, 0, side);
+  finish_pair<T, EPI>(a, em, rows[ep], rows[P + ep], rok[ep], rok[P + ep], va, vb, side, 0);
+}
+
+// ---------------------------------------------------------------------------
 // Decode rows 5..32 (bf16) on MFMA. The same tuples and epilogues as the
 // register GEMV, with 16 weight rows per tuple: rows ra + 0..7 and rb + 0..7
 // (pairs (ra + p, rb + p): SwiGLU gate j / up I + j, RoPE dims i / i + D/2,
@@ -1079,9 +1207,57 @@ int launch_lds(hipStream_t st, const GemvArgs& a) {
   return MINITP_OK;
 }
 
+template <typename T, int MM, int JMAX, int EPI>
+int launch_split_j(hipStream_t st, const GemvArgs& a, int nseg, int64_t seg_chunks) {
+  const int64_t grid = num_tuples<EPI>(a) * nseg;
+  hipLaunchKernelGGL((gemv_split_kernel<T, MM, JMAX, EPI>), dim3((unsigned)grid), dim3(256), 0, st, a, nseg,
+                     (uint32_t)(seg_chunks * 16));
+  MINITP_LAUNCH_CHECK();
+  return MINITP_OK;
+}
+
+// Segments of at most 256 x SPLIT_JMAX chunks, sized evenly.
+template <typename T, int MM, int EPI>
+int launch_split(hipStream_t st, const GemvArgs& a) {
+  const int64_t nchunk = a.K / Vec<T>::N;
+  const int nseg = (int)cdiv(nchunk, 256 * SPLIT_JMAX);
+  const int64_t seg_chunks = cdiv(nchunk, nseg);
+  if ((nseg - 1) * seg_chunks >= nchunk || nseg > SPLIT_MAX_SEG || num_tuples<EPI>(a) > SPLIT_MAX_TUPLES) {
+    set_error("gemv split: %lld chunks in %d segments of %lld", (long long)nchunk, nseg, (long long)seg_chunks);
+    return MINITP_ERR_UNSUPPORTED;
+  }
+  switch (cdiv(seg_chunks, 256)) {
+    case 1:
+      return launch_split_j<T, MM, 1, EPI>(st, a, nseg, seg_chunks);
+    case 2:
+      return launch_split_j<T, MM, 2, EPI>(st, a, nseg, seg_chunks);
+    case 3:
+      return launch_split_j<T, MM, 3, EPI>(st, a, nseg, seg_chunks);
+    default:
+      return launch_split_j<T, MM, 4, EPI>(st, a, nseg, seg_chunks);
+  }
+}
+
+// The split form serves rows of more than SPLIT_MIN_CHUNKS chunks when the
+// caller gave it its buffers, the input is not normalized in the prologue
+// and the tuples and segments fit them.
+template <typename T, int PRO, int EPI>
+bool use_split(const GemvArgs& a) {
+  if constexpr (PRO != PRO_NONE || !(EPI == EPI_STORE || EPI == EPI_RESID || EPI == EPI_SWIGLU)) {
+    return false;
+  } else {
+    const int64_t nchunk = a.K / Vec<T>::N;
+    return a.split_part != nullptr && a.split_count != nullptr && nchunk > SPLIT_MIN_CHUNKS &&
+           num_tuples<EPI>(a) <= SPLIT_MAX_TUPLES && cdiv(nchunk, 256 * SPLIT_JMAX) <= SPLIT_MAX_SEG &&
+           a.K * (int64_t)sizeof(T) < (1LL << 31);
+  }
+}
+
 template <typename T, int MM, int PRO, int EPI>
 int pick_k(hipStream_t st, const GemvArgs& a) {
   const int64_t nchunk = a.K / Vec<T>::N;
+  if constexpr (MM == 1 && PRO == PRO_NONE && (EPI == EPI_STORE || EPI == EPI_RESID || EPI == EPI_SWIGLU))
+    if (use_split<T, PRO, EPI>(a)) return launch_split<T, MM, EPI>(st, a);
   if (nchunk <= 128) return launch_reg<T, MM, 1, 2, PRO, EPI>(st, a);
   if constexpr (MM <= 2) {
     if (nchunk <= 512) return launch_reg<T, MM, 2, 4, PRO, EPI>(st, a);
@@ -1121,6 +1297,8 @@ int pick_epi(hipStream_t st, int epi, const GemvArgs& a) {
 }
 
 }  // namespace
+
+int64_t gemv_split_part_bytes() { return (int64_t)SPLIT_MAX_TUPLES * SPLIT_MAX_SEG * 4 * R * sizeof(float); }
 
 // Block count (and so partial count per row) of the LM-head argmax GEMV.
 int64_t gemv_argmax_partials(int64_t N) { return std::min<int64_t>(cdiv(cdiv(N, R), 4), 1024); }

@@ -32,6 +32,10 @@ struct StepArgs {
 // What the forward's later kernels read from device memory, so a captured
 // hipGraph stays valid from step to step: only the first node's arguments
 // change, and that node writes this struct.
+// Tuples (4 output rows each) and K segments of one split-K GEMV launch.
+constexpr int SPLIT_MAX_TUPLES = 2048;
+constexpr int SPLIT_MAX_SEG = 8;
+
 struct StepState {
   StepArgs args;
   int32_t error;   // 1: a position was outside the RoPE table
@@ -41,6 +45,9 @@ struct StepState {
   // the position is outside the table).
   float rope_cos[MAX_HEAD_DIM];
   float rope_sin[MAX_HEAD_DIM];
+  // arrival words of the split-K GEMV, zeroed by the first kernel of every
+  // forward (each launch also leaves them at 0)
+  uint32_t split_count[SPLIT_MAX_TUPLES];
 };
 
 // Layer-independent shape of the attention / KV layout.
@@ -74,12 +81,19 @@ struct GemvArgs {
   // argmax_merge_kernel, launched right after the GEMV)
   float* part_val;  // [M, gridDim.x] block partials
   int64_t* part_idx;
+  // Split-K form (rows longer than the register path holds): fp32 segment
+  // partials [tuples, segments, M, 4] and one arrival word per tuple, 0
+  // between launches. Both null: the split form is not used.
+  float* split_part;
+  uint32_t* split_count;
 };
 
 // gemv.hip
 int64_t gemv_argmax_partials(int64_t N);
 int launch_gemv(hipStream_t st, int dtype, int pro, int epi, const GemvArgs& a);
 bool gemv_supported(int dtype, int64_t M, int64_t K);
+// Bytes of GemvArgs::split_part (SPLIT_MAX_TUPLES x SPLIT_MAX_SEG x 4 rows x 4).
+int64_t gemv_split_part_bytes();
 // ... and with the RMSNorm prologue (PRO_NORM)
 bool gemv_norm_supported(int dtype, int64_t M, int64_t K);
 

@@ -14,6 +14,7 @@
 // and the final RMSNorm -> LM head -> argmax is one more kernel. Larger M
 // runs MFMA GEMMs with separate norm / RoPE / SwiGLU kernels.
 #include <cmath>
+#include <cstddef>
 #include <mutex>
 #include <string>
 #include <vector>
@@ -35,6 +36,7 @@ __global__ void step_embed_kernel(StepState* dst, StepArgs val, const T* __restr
                                   int64_t hidden, int64_t vocab, int64_t T_, const float* cos_tab,
                                   const float* sin_tab, int64_t max_pos, int head_dim) {
   if (blockIdx.x == 0) {
+    for (int i = threadIdx.x; i < SPLIT_MAX_TUPLES; i += blockDim.x) dst->split_count[i] = 0u;
     if (threadIdx.x == 0) {
       dst->args = val;
       dst->error = 0;
@@ -93,6 +95,8 @@ struct Ws {
   void* amax_ws;
   int64_t amax_ws_bytes;
   void* gemm_ws;  // split-K partials of the prefill / batched GEMMs
+  float* split_part;  // segment partials of the split-K GEMV
+  uint32_t* split_count;  // its arrival words (in the StepState)
   int64_t bytes;
 };
 
@@ -166,6 +170,8 @@ struct Qwen2Program {
     w.amax_ws_bytes = argmax_workspace_bytes(B, c.vocab);
     w.amax_ws = take(w.amax_ws_bytes);
     w.gemm_ws = take(GEMM_WS_BYTES);
+    w.split_part = (float*)take(gemv_split_part_bytes());
+    w.split_count = w.st ? (uint32_t*)((char*)w.st + offsetof(StepState, split_count)) : nullptr;
     w.bytes = off;
     return w;
   }
@@ -297,6 +303,8 @@ struct Qwen2Program {
         g.M = M;
         g.N = H;
         g.K = q_rows();
+        g.split_part = w.split_part;
+        g.split_count = w.split_count;
         if ((rc = launch_gemv(st, c.dtype, PRO_NONE, EPI_RESID, g))) return rc;
       } else {
         if ((rc = launch_gemm(st, c.dtype, w.attn, q_rows(), L(l, MINITP_W_O), nullptr, w.x, H, M, H, q_rows(),
@@ -336,6 +344,8 @@ struct Qwen2Program {
         d.M = M;
         d.N = H;
         d.K = I;
+        d.split_part = w.split_part;
+        d.split_count = w.split_count;
         if ((rc = launch_gemv(st, c.dtype, PRO_NONE, EPI_RESID, d))) return rc;
       } else {
         if ((rc = launch_rmsnorm(st, c.dtype, w.x, L(l, MINITP_W_LN2), w.h, M, H, c.eps))) return rc;
