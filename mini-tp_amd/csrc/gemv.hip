@@ -1152,6 +1152,287 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
 // when it fits: the norm prologue needs that)
 constexpr int MF_ONE = 8;
 
+// ---------------------------------------------------------------------------
+// gemv_mfma_split_kernel: decode rows 5..32 (bf16) with K split over blocks
+// as well as over a block's 4 waves, no RMSNorm prologue. The grid is groups
+// of NT tuples (x) by K segments of seg_steps steps of 32 (y): the few-tuple
+// products (QKV: 72 tuples at the 0.5B shape, o_proj 56, down 56) spread over
+// hundreds of blocks, and each block loads only its segment of the input
+// rows. Every block issues all of its loads at once (at most MF_ONE steps
+// per wave), multiplies, adds its waves' tiles in order, and stores the
+// block's 16 x 32 tile per tuple device-coherent; the block that brings the
+// group's arrival word to nseg adds the segments in order and runs the
+// epilogue (the same sum whatever the arrival order), then puts the word
+// back to 0. Each extra device-scope round trip (partial stores, the
+// count, the partial loads) costs about as much as the load phase, so this
+// pays only where the unsplit form leaves most of the chip idle for long:
+// the down projection at the 0.5B shape (K = 4,864, 56 tuples).
+constexpr int AUX_SC1 = 16;  // buffer-op cache policy: device scope (sc1)
+
+__device__ __forceinline__ void store16_dev(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4_m v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, AUX_SC1);
+}
+__device__ __forceinline__ f32x4_m load16_dev(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4_m, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX_SC1));
+}
+
+template <int EPI, int NT>
+__global__ __launch_bounds__(256) void gemv_mfma_split_kernel(GemvArgs a, int nseg, int seg_steps) {
+  constexpr uint32_t OOBW = 0xffffffffu;
+  __shared__ f32x4_m red[4][NT][2][64];
+  __shared__ int last;
+  const int tid = threadIdx.x, lane = tid & 63, kw = tid >> 6;
+  const int M = (int)a.M;
+  const int64_t K = a.K;
+  const int64_t grp = blockIdx.x;
+  const int seg = (int)blockIdx.y;
+  const int64_t t0 = grp * NT;
+  const int64_t ntup = num_tuples16<EPI>(a);
+  const int nidx = lane & 15, kq = lane >> 4;
+  const int64_t w_rows = EPI == EPI_SWIGLU ? 2 * a.N : a.N;
+  const __amdgpu_buffer_rsrc_t wr = span_rsrc(a.w, (uint32_t)(w_rows * K * 2));
+  const __amdgpu_buffer_rsrc_t xr = span_rsrc(a.x, (uint32_t)(((int64_t)(M - 1) * a.ldx + K) * 2));
+  int64_t ra[NT], rb[NT];
+  uint32_t wbase[NT];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const bool live = t0 + j < ntup;
+    ra[j] = rb[j] = 0;
+    if (live) tuple16_rows<EPI>(t0 + j, a, ra[j], rb[j]);
+    const int64_t wrow = nidx < P16 ? ra[j] + nidx : rb[j] + (nidx - P16);
+    wbase[j] = live && row_valid<EPI>(wrow, a) ? (uint32_t)(wrow * K * 2) : OOBW;
+  }
+  const int m0 = nidx, m1 = 16 + nidx;
+  const uint32_t xb0 = m0 < M ? (uint32_t)((int64_t)m0 * a.ldx * 2) : OOBW;
+  const uint32_t xb1 = m1 < M ? (uint32_t)((int64_t)m1 * a.ldx * 2) : OOBW;
+  const int64_t nsteps = cdiv(K, 32);
+  const int64_t sb = (int64_t)seg * seg_steps, se = std::min(nsteps, sb + seg_steps);
+  const int64_t per = cdiv((int64_t)seg_steps, 4);
+  const int64_t s_begin = sb + kw * per, s_end = std::min(se, s_begin + per);
+  auto off = [&](uint32_t base, int64_t s) -> uint32_t {
+    const int64_t k = s * 32 + kq * 8;
+    return (base != OOBW && s < s_end && k < K) ? base + (uint32_t)(k * 2) : OOBW;
+  };
+  uint4 w[MF_ONE][NT], xa[MF_ONE], xc[MF_ONE];
+#pragma unroll
+  for (int i = 0; i < MF_ONE; ++i)
+#pragma unroll
+    for (int j = 0; j < NT; ++j) w[i][j] = span_load16<W_AUX>(wr, off(wbase[j], s_begin + i));
+#pragma unroll
+  for (int i = 0; i < MF_ONE; ++i) {
+    xa[i] = span_load16<0>(xr, off(xb0, s_begin + i));
+    xc[i] = span_load16<0>(xr, off(xb1, s_begin + i));
+  }
+  // the epilogue's side inputs, loaded underneath the weights (only the
+  // block that finishes a group uses them)
+  constexpr int NSIDE = EPI == EPI_RESID ? 16 : (EPI == EPI_QKV_ROPE1 ? 6 : (EPI == EPI_QKV_ROPE ? 2 : 1));
+  float sv[NT][NSIDE];
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    const int p = nidx & (P16 - 1);
+    const int64_t row_a = ra[j] + p, row_b = rb[j] + p;
+    const bool oka = t0 + j < ntup && row_valid<EPI>(row_a, a), okb = t0 + j < ntup && row_valid<EPI>(row_b, a);
+#pragma unroll
+    for (int q = 0; q < NSIDE; ++q) sv[j][q] = 0.f;
+    if constexpr (EPI == EPI_RESID) {
+      const bf16* aux = (const bf16*)a.aux;
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = h * 16 + 4 * kq + r;
+          const int mm = m < M ? m : 0;
+          sv[j][h * 8 + r] = load_f32<bf16>(aux, mm * a.ldy + (oka ? row_a : 0));
+          sv[j][h * 8 + 4 + r] = load_f32<bf16>(aux, mm * a.ldy + (okb ? row_b : 0));
+        }
+    } else if constexpr (is_qkv<EPI>()) {
+      sv[j][0] = load_f32<bf16>((const bf16*)a.bias, oka ? row_a : 0);
+      sv[j][1] = load_f32<bf16>((const bf16*)a.bias, okb ? row_b : 0);
+      if constexpr (EPI == EPI_QKV_ROPE1) {
+        const int D = a.a.D, i = (int)(row_a % D);
+        sv[j][2] = a.st->rope_cos[i];
+        sv[j][3] = a.st->rope_sin[i];
+        sv[j][4] = a.st->rope_cos[i + D / 2];
+        sv[j][5] = a.st->rope_sin[i + D / 2];
+      }
+    }
+  }
+  f32x4_m acc[NT][2];
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int h = 0; h < 2; ++h) acc[j][h] = f32x4_m{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+  for (int i = 0; i < MF_ONE; ++i) {
+    const bf16x8_m aa = __builtin_bit_cast(bf16x8_m, xa[i]), ac = __builtin_bit_cast(bf16x8_m, xc[i]);
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      const bf16x8_m bw = __builtin_bit_cast(bf16x8_m, w[i][j]);
+      acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aa, bw, acc[j][0], 0, 0, 0);
+      acc[j][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac, bw, acc[j][1], 0, 0, 0);
+    }
+  }
+  // the block's tile: its waves' K ranges added in order
+#pragma unroll
+  for (int j = 0; j < NT; ++j) {
+    red[kw][j][0][lane] = acc[j][0];
+    red[kw][j][1][lane] = acc[j][1];
+  }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t pr = span_rsrc(a.split_part, (uint32_t)a.split_part_bytes);
+  auto part_off = [&](int64_t sg, int j, int h) -> uint32_t {
+    return (uint32_t)(((((grp * nseg + sg) * NT + j) * 2 + h) * 64 + lane) * 16);
+  };
+  if (kw == 0) {
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        f32x4_m v = red[0][j][h][lane];
+        for (int k = 1; k < 4; ++k) v += red[k][j][h][lane];
+        store16_dev(pr, part_off(seg, j, h), v);
+      }
+    // device-coherent stores complete (vmcnt(0) expcnt(7) lgkmcnt(15))
+    // before the block is counted in: an agent-scope release without its
+    // whole-L2 write-back
+    __builtin_amdgcn_s_waitcnt(0x0F70);
+    if (lane == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(a.split_count + grp, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last = old == (uint32_t)(nseg - 1);
+      if (last) __hip_atomic_store(a.split_count + grp, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+  __syncthreads();
+  if (last && kw == 0) {
+    // ---- the group's last block: segments in order, then the epilogue ----
+    // (SB segments' loads in flight at a time; past nseg they read zeros)
+    constexpr int SB = 8 / NT;
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) acc[j][h] = f32x4_m{0.f, 0.f, 0.f, 0.f};
+    for (int sg0 = 0; sg0 < nseg; sg0 += SB) {
+      f32x4_m v[SB][NT][2];
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) v[u][j][h] = load16_dev(pr, sg0 + u < nseg ? part_off(sg0 + u, j, h) : OOBW);
+#pragma unroll
+      for (int u = 0; u < SB; ++u)
+#pragma unroll
+        for (int j = 0; j < NT; ++j)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) acc[j][h] += v[u][j][h];
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j) {
+      float pa0[4], pa1[4];  // the pair partners' sums (lane l ^ 8)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        pa0[r] = __shfl_xor(acc[j][0][r], 8);
+        pa1[r] = __shfl_xor(acc[j][1][r], 8);
+      }
+      if (t0 + j >= ntup || nidx >= P16) continue;
+      const int p = nidx;
+      const int64_t row_a = ra[j] + p, row_b = rb[j] + p;
+      const bool oka = row_valid<EPI>(row_a, a), okb = row_valid<EPI>(row_b, a);
+      float side[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+      if constexpr (is_qkv<EPI>()) {
+        side[4] = sv[j][0];
+        side[5] = sv[j][1];
+      }
+      if constexpr (EPI == EPI_QKV_ROPE1) {
+        side[0] = sv[j][2];
+        side[1] = sv[j][3];
+        side[2] = sv[j][4];
+        side[3] = sv[j][5];
+      }
+#pragma unroll
+      for (int h = 0; h < 2; ++h)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = h * 16 + 4 * kq + r;
+          if (m >= M) continue;
+          const float va = acc[j][h][r], vb = h ? pa1[r] : pa0[r];
+          int64_t pos = 0;
+          if constexpr (EPI == EPI_QKV_ROPE) {
+            const int D = a.a.D, i = (int)(row_a % D);
+            pos = a.st->args.positions[m % a.a.T];
+            if (row_a / D < a.a.Hq + a.a.Hkv && pos >= 0 && pos < a.max_pos) {
+              side[0] = a.cos_tab[pos * D + i];
+              side[1] = a.sin_tab[pos * D + i];
+              side[2] = a.cos_tab[pos * D + i + D / 2];
+              side[3] = a.sin_tab[pos * D + i + D / 2];
+            }
+          } else if constexpr (EPI == EPI_RESID) {
+            side[0] = sv[j][h * 8 + r];
+            side[1] = sv[j][h * 8 + 4 + r];
+          }
+          finish_pair<bf16, EPI>(a, m, row_a, row_b, oka, okb, va, vb, side, pos);
+        }
+    }
+  }
+}
+
+// Split form geometry: NT tuples per group, nseg segments of seg_steps.
+struct MfSplit {
+  int nt, nseg, seg_steps;
+  int64_t groups, part_bytes;
+};
+#ifndef MINITP_MF_TARGET_BLOCKS
+#define MINITP_MF_TARGET_BLOCKS 512
+#endif
+#ifndef MINITP_MF_MIN_STEPS
+#define MINITP_MF_MIN_STEPS 1
+#endif
+template <int EPI>
+MfSplit mf_split(const GemvArgs& a) {
+  MfSplit g{};
+  const int64_t ntup = num_tuples16<EPI>(a), nsteps = cdiv(a.K, 32);
+  g.nt = ntup >= 512 ? 2 : 1;
+  g.groups = cdiv(ntup, g.nt);
+  const int64_t lo = cdiv(nsteps, 4 * MF_ONE);
+  const int64_t hi = std::max<int64_t>(1, nsteps / (4 * MINITP_MF_MIN_STEPS));
+  int64_t n = std::max(lo, std::min(cdiv((int64_t)MINITP_MF_TARGET_BLOCKS, g.groups), hi));
+  g.seg_steps = (int)cdiv(nsteps, n);
+  g.nseg = (int)cdiv(nsteps, (int64_t)g.seg_steps);
+  g.part_bytes = g.groups * g.nseg * g.nt * 2 * 64 * 16;
+  return g;
+}
+
+template <int EPI>
+bool mf_split_ok(const GemvArgs& a) {
+  if constexpr (!(EPI == EPI_STORE || EPI == EPI_RESID || EPI == EPI_SWIGLU || is_qkv<EPI>())) {
+    return false;
+  } else {
+    if (a.split_part == nullptr || a.split_count == nullptr) return false;
+    const MfSplit g = mf_split<EPI>(a);
+    return g.groups <= SPLIT_MAX_TUPLES && g.part_bytes <= a.split_part_bytes &&
+           a.split_part_bytes < (1LL << 32) && (int64_t)g.seg_steps <= 4 * MF_ONE;
+  }
+}
+
+template <int EPI, int NT>
+int launch_mfma_split_nt(hipStream_t st, const GemvArgs& a, const MfSplit& g) {
+  const dim3 grid((unsigned)g.groups, (unsigned)g.nseg);
+  hipLaunchKernelGGL((gemv_mfma_split_kernel<EPI, NT>), grid, dim3(256), 0, st, a, g.nseg, g.seg_steps);
+  MINITP_LAUNCH_CHECK();
+  return MINITP_OK;
+}
+
+template <int EPI>
+int launch_mfma_split(hipStream_t st, const GemvArgs& a) {
+  if constexpr (!(EPI == EPI_STORE || EPI == EPI_RESID || EPI == EPI_SWIGLU || is_qkv<EPI>())) {
+    set_error("gemv: no split form for epilogue %d", EPI);
+    return MINITP_ERR_UNSUPPORTED;
+  } else {
+    const MfSplit g = mf_split<EPI>(a);
+    return g.nt == 2 ? launch_mfma_split_nt<EPI, 2>(st, a, g) : launch_mfma_split_nt<EPI, 1>(st, a, g);
+  }
+}
+
 template <int PRO, int EPI, int NT>
 int launch_mfma_nt(hipStream_t st, const GemvArgs& a, int64_t ntup) {
   const unsigned grid = (unsigned)cdiv(ntup, NT);
@@ -1174,6 +1455,10 @@ int launch_mfma(hipStream_t st, const GemvArgs& a) {
     set_error("gemv: the argmax epilogue serves at most 4 rows");
     return MINITP_ERR_UNSUPPORTED;
   } else {
+    // with split buffers and no norm prologue: K split over blocks too
+    if constexpr (PRO == PRO_NONE) {
+      if (mf_split_ok<EPI>(a)) return launch_mfma_split<EPI>(st, a);
+    }
     // K split over the block's 4 waves; many tuples: 2 per wave (the input
     // rows read once per 32 weight rows), few: 1 per wave (more blocks)
     const int64_t ntup = num_tuples16<EPI>(a);
@@ -1248,6 +1533,7 @@ bool use_split(const GemvArgs& a) {
   } else {
     const int64_t nchunk = a.K / Vec<T>::N;
     return a.split_part != nullptr && a.split_count != nullptr && nchunk > SPLIT_MIN_CHUNKS &&
+           a.split_part_bytes >= gemv_split_part_bytes(1) &&
            num_tuples<EPI>(a) <= SPLIT_MAX_TUPLES && cdiv(nchunk, 256 * SPLIT_JMAX) <= SPLIT_MAX_SEG &&
            a.K * (int64_t)sizeof(T) < (1LL << 31);
   }
@@ -1298,7 +1584,10 @@ int pick_epi(hipStream_t st, int epi, const GemvArgs& a) {
 
 }  // namespace
 
-int64_t gemv_split_part_bytes() { return (int64_t)SPLIT_MAX_TUPLES * SPLIT_MAX_SEG * 4 * R * sizeof(float); }
+int64_t gemv_split_part_bytes(int64_t M) {
+  const int64_t reg = (int64_t)SPLIT_MAX_TUPLES * SPLIT_MAX_SEG * 4 * R * sizeof(float);
+  return M > 4 && M <= 32 ? std::max<int64_t>(reg, 16LL << 20) : reg;
+}
 
 // Block count (and so partial count per row) of the LM-head argmax GEMV.
 int64_t gemv_argmax_partials(int64_t N) { return std::min<int64_t>(cdiv(cdiv(N, R), 4), 1024); }

@@ -86,14 +86,17 @@ struct GemvArgs {
   // between launches. Both null: the split form is not used.
   float* split_part;
   uint32_t* split_count;
+  int64_t split_part_bytes;
 };
 
 // gemv.hip
 int64_t gemv_argmax_partials(int64_t N);
 int launch_gemv(hipStream_t st, int dtype, int pro, int epi, const GemvArgs& a);
 bool gemv_supported(int dtype, int64_t M, int64_t K);
-// Bytes of GemvArgs::split_part (SPLIT_MAX_TUPLES x SPLIT_MAX_SEG x 4 rows x 4).
-int64_t gemv_split_part_bytes();
+// Bytes of GemvArgs::split_part for products of M input rows (the register
+// form's SPLIT_MAX_TUPLES x SPLIT_MAX_SEG x 4 x 4 floats; 16 MiB for the
+// MFMA form's 16 x 32 tiles at M = 5..32).
+int64_t gemv_split_part_bytes(int64_t M);
 // ... and with the RMSNorm prologue (PRO_NORM)
 bool gemv_norm_supported(int dtype, int64_t M, int64_t K);
 

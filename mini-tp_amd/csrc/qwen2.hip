@@ -95,8 +95,9 @@ struct Ws {
   void* amax_ws;
   int64_t amax_ws_bytes;
   void* gemm_ws;  // split-K partials of the prefill / batched GEMMs
-  float* split_part;  // segment partials of the split-K GEMV
-  uint32_t* split_count;  // its arrival words (in the StepState)
+  float* split_part;  // segment partials of the split-K GEMVs
+  int64_t split_part_bytes;
+  uint32_t* split_count;  // their arrival words (in the StepState)
   int64_t bytes;
 };
 
@@ -170,7 +171,8 @@ struct Qwen2Program {
     w.amax_ws_bytes = argmax_workspace_bytes(B, c.vocab);
     w.amax_ws = take(w.amax_ws_bytes);
     w.gemm_ws = take(GEMM_WS_BYTES);
-    w.split_part = (float*)take(gemv_split_part_bytes());
+    w.split_part_bytes = gemv_split_part_bytes(M);
+    w.split_part = (float*)take(w.split_part_bytes);
     w.split_count = w.st ? (uint32_t*)((char*)w.st + offsetof(StepState, split_count)) : nullptr;
     w.bytes = off;
     return w;
@@ -228,6 +230,11 @@ struct Qwen2Program {
       return r;
     };
     if (blas && (rc = launch_rmsnorm(st, c.dtype, w.x, L(0, MINITP_W_LN1), w.h, M, H, c.eps))) return rc;
+    auto split_bufs = [&](GemvArgs& g) {
+      g.split_part = w.split_part;
+      g.split_part_bytes = w.split_part_bytes;
+      g.split_count = w.split_count;
+    };
     for (int l = 0; l < c.num_layers; ++l) {
       if (blas) {
         // h holds input_layernorm(x) of this layer
@@ -303,8 +310,9 @@ struct Qwen2Program {
         g.M = M;
         g.N = H;
         g.K = q_rows();
-        g.split_part = w.split_part;
-        g.split_count = w.split_count;
+        // (5..32 rows: the unsplit MFMA form; its one round trip beats the
+        // split form's three extra at K = 896)
+        if (M <= 4) split_bufs(g);
         if ((rc = launch_gemv(st, c.dtype, PRO_NONE, EPI_RESID, g))) return rc;
       } else {
         if ((rc = launch_gemm(st, c.dtype, w.attn, q_rows(), L(l, MINITP_W_O), nullptr, w.x, H, M, H, q_rows(),
@@ -325,15 +333,8 @@ struct Qwen2Program {
         g.N = I;
         g.K = H;
         if ((rc = launch_gemv(st, c.dtype, PRO_NORM, EPI_SWIGLU, g))) return rc;
-        if (M > 4) {
-          // 5..32 rows: the long-K down projection keeps the split-K GEMM (its
-          // K splits over blocks keep more weight bytes in flight than the
-          // MFMA GEMV's 56 tuples of 16 rows can)
-          if ((rc = launch_gemm(st, c.dtype, w.act, I, L(l, MINITP_W_DOWN), nullptr, w.x, H, M, H, I, MINITP_EPI_RESID,
-                                w.x, nullptr, w.gemm_ws, GEMM_SPLIT_BYTES)))
-            return rc;
-          continue;
-        }
+        // the down projection's long K splits over blocks (register form
+        // past 8,192, MFMA form at 5..32 rows)
         GemvArgs d{};
         d.x = w.act;
         d.ldx = I;
@@ -344,8 +345,7 @@ struct Qwen2Program {
         d.M = M;
         d.N = H;
         d.K = I;
-        d.split_part = w.split_part;
-        d.split_count = w.split_count;
+        split_bufs(d);
         if ((rc = launch_gemv(st, c.dtype, PRO_NONE, EPI_RESID, d))) return rc;
       } else {
         if ((rc = launch_rmsnorm(st, c.dtype, w.x, L(l, MINITP_W_LN2), w.h, M, H, c.eps))) return rc;
