@@ -328,27 +328,266 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(DecodeArgs a) {
 }
 
 // Merge of the splits of each (batch row, KV head) (a separate launch, so
-// the partials are visible without any grid-wide fence).
+// the partials are visible without any grid-wide fence). Block (bh, part)
+// takes MERGE_T of the group's G x D outputs; a thread loads the partials
+// of MERGE_NS splits at once (one memory round trip for nsplit <= MERGE_NS)
+// and folds them into a running (max, sum, output) in split order.
+constexpr int MERGE_T = 128;
+constexpr int MERGE_NS = 8;
+
 template <typename T, int D>
-__global__ __launch_bounds__(256) void decode_merge_kernel(DecodeArgs a, int nsplit) {
+__global__ __launch_bounds__(MERGE_T) void decode_merge_kernel(DecodeArgs a, int nsplit) {
   const AttnShape& s = a.s;
   const int G = s.Hq / s.Hkv;
   const int bh = blockIdx.x, b = bh / s.Hkv, g = bh % s.Hkv;
-  T* out = (T*)a.out;
-  for (int i = threadIdx.x; i < G * D; i += 256) {
+  const int i = blockIdx.y * MERGE_T + threadIdx.x;
+  if (i >= G * D) return;
+  const int h = i / D, d = i % D;
+  float mx = -__builtin_inff(), l = 0.f, o = 0.f;
+  for (int sp0 = 0; sp0 < nsplit; sp0 += MERGE_NS) {
+    float ms[MERGE_NS], ls[MERGE_NS], os[MERGE_NS];
+#pragma unroll
+    for (int u = 0; u < MERGE_NS; ++u) {
+      const int sp = sp0 + u < nsplit ? sp0 + u : sp0;
+      const int64_t slot = ((int64_t)bh * nsplit + sp) * GMAX + h;
+      ms[u] = sp0 + u < nsplit ? a.ws_ml[slot * 2] : -__builtin_inff();
+      ls[u] = a.ws_ml[slot * 2 + 1];
+      os[u] = a.ws_o[slot * D + d];
+    }
+    float cm = mx;
+#pragma unroll
+    for (int u = 0; u < MERGE_NS; ++u) cm = fmaxf(cm, ms[u]);
+    if (cm == -__builtin_inff()) continue;  // no split of this chunk saw a position yet
+    const float alpha = mx == -__builtin_inff() ? 0.f : expf(mx - cm);
+    l *= alpha;
+    o *= alpha;
+#pragma unroll
+    for (int u = 0; u < MERGE_NS; ++u) {
+      if (ms[u] == -__builtin_inff()) continue;  // split saw no position
+      const float sc = expf(ms[u] - cm);
+      l = fmaf(sc, ls[u], l);
+      o = fmaf(sc, os[u], o);
+    }
+    mx = cm;
+  }
+  store_f32<T>((T*)a.out, ((int64_t)b * s.Hq + g * G + h) * D + d, o / l);
+}
+
+// ---------------------------------------------------------------------------
+// Grouped decode attention on MFMA (bf16, D = 64 or 128, G <= GMAX query
+// heads per KV head). The G heads of a KV group are the 16-row side of
+// v_mfma_f32_16x16x32_bf16 (rows G..15 zero): the scores of 16 key positions
+// are D / 32 MFMAs (A: lane l holds q head l % 16, dims 32 s + 8 (l / 16)
+// .. +7; B: key row p + l % 16, the same dims) and P V of 32 positions is
+// D / 16 MFMAs. P V wants each lane's 8 consecutive positions of one V
+// column and of one P row, so both pass through wave-private LDS: the V tile
+// row-major with a row stride of 2 D + 8 bytes (the four lane groups' 16-bit
+// column reads, 8 rows apart, land in different banks), P as [head][position]
+// bf16 rows of 80 bytes (one conflict-free 16-byte read per lane). Softmax
+// per head in fp32 (base 2, the 1/sqrt(D) scale folded into the exponent);
+// P is rounded to bf16 for its MFMA.
+// Block = NWM waves over one split's position range, 32-position tiles
+// round robin, each tile's K and V loads issued before the previous tile's
+// math. Waves and splits merge as in decode_attn_kernel (same workspace
+// layout and merge kernel).
+constexpr int NWM = 4;
+typedef __bf16 bf16x8_a __attribute__((ext_vector_type(8)));
+typedef float f32x4_a __attribute__((ext_vector_type(4)));
+
+template <int D>
+struct MfDec {
+  static constexpr int VS = 2 * D + 8;         // V tile row stride in LDS (bytes)
+  static constexpr int PS = 80;                // P row stride in LDS (bytes)
+  static constexpr int VL = D / 16;            // 16-byte V loads per lane per tile (32 rows x D)
+  static constexpr int WAVE_LDS = 32 * VS + 16 * PS;
+};
+
+template <int D>
+__global__ __launch_bounds__(NWM * 64) void decode_attn_mfma_kernel(DecodeArgs a) {
+  using Geo = MfDec<D>;
+  constexpr int KS = D / 32;   // 32-dim steps of the scores
+  constexpr int DB = D / 16;   // 16-column blocks of the output
+  constexpr int VL = Geo::VL;
+  constexpr uint32_t OOB = 0xffffffffu;
+  __shared__ __attribute__((aligned(16))) char lds[NWM * Geo::WAVE_LDS];
+  __shared__ float pm[NWM][GMAX], pl[NWM][GMAX];
+
+  const AttnShape& s = a.s;
+  const int G = s.Hq / s.Hkv;
+  const int bh = blockIdx.x, b = bh / s.Hkv, g = bh % s.Hkv;
+  const int split = blockIdx.y, nsplit = gridDim.y;
+  const int64_t ctx = (a.st ? a.st->args.cache_len : a.cache_len) + 1;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int n16 = lane & 15, q4 = lane >> 4;
+  char* vs = lds + w * Geo::WAVE_LDS;
+  char* ps = vs + 32 * Geo::VS;
+
+  const int64_t tiles = cdiv(ctx, (int64_t)32);
+  const int64_t span = cdiv(tiles, (int64_t)nsplit);
+  const int64_t t_begin = split * span, t_end = std::min(tiles, t_begin + span);
+
+  const int64_t layer_off = (int64_t)a.layer * s.B * s.Hkv * s.S * D;
+  const bf16* kc = (const bf16*)(a.st ? a.st->args.k_cache : a.k) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
+  const bf16* vc = (const bf16*)(a.st ? a.st->args.v_cache : a.v) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
+  const uint32_t kv_bytes = (uint32_t)(ctx * D * 2);  // rows past the context read zeros
+  const __amdgpu_buffer_rsrc_t kr = attn_rsrc(kc, kv_bytes), vr = attn_rsrc(vc, kv_bytes);
+
+  // q heads of the group as the A operand (rows G..15 zero)
+  bf16x8_a qa[KS];
+  {
+    const bf16* qp = (const bf16*)a.q + ((int64_t)b * s.Hq + (int64_t)g * G) * D;
+    const __amdgpu_buffer_rsrc_t qr = attn_rsrc(qp, (uint32_t)(G * D * 2));
+#pragma unroll
+    for (int k = 0; k < KS; ++k)
+      qa[k] = __builtin_bit_cast(bf16x8_a, attn_load16(qr, n16 < G ? (uint32_t)((n16 * D + 32 * k + 8 * q4) * 2) : OOB));
+  }
+
+  // loads of one tile: K as B operands (two 16-position halves x KS steps),
+  // V rows for the LDS stage (lane l: row l % 32, dims (l / 32) D / 2 ..)
+  struct Tile {
+    uint4 k[2][KS];
+    uint4 v[VL];
+  };
+  auto issue = [&](Tile& tl, int64_t t) {
+    const bool live = t < t_end;
+    const int64_t p0 = t * 32;
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int k = 0; k < KS; ++k)
+        tl.k[h][k] = attn_load16(kr, live ? (uint32_t)(((p0 + 16 * h + n16) * D + 32 * k + 8 * q4) * 2) : OOB);
+#pragma unroll
+    for (int i = 0; i < VL; ++i)
+      tl.v[i] = attn_load16(vr, live ? (uint32_t)(((p0 + (lane & 31)) * D + (lane >> 5) * (D / 2) + 8 * i) * 2) : OOB);
+  };
+
+  const float sl2 = a.scale * 1.4426950408889634f;  // scores to base-2 exponent units
+  float m[4], l[4];
+  f32x4_a o[DB];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    m[r] = -__builtin_inff();
+    l[r] = 0.f;
+  }
+#pragma unroll
+  for (int c = 0; c < DB; ++c) o[c] = f32x4_a{0.f, 0.f, 0.f, 0.f};
+
+  Tile cur, nxt;
+  int64_t t = t_begin + w;
+  issue(cur, t);
+  for (; t < t_end; t += NWM) {
+    issue(nxt, t + NWM);
+    // V tile -> LDS, row-major (two 8-byte writes per 16-byte piece)
+#pragma unroll
+    for (int i = 0; i < VL; ++i) {
+      char* dst = vs + (lane & 31) * Geo::VS + ((lane >> 5) * (D / 2) + 8 * i) * 2;
+      *(uint2*)dst = make_uint2(cur.v[i].x, cur.v[i].y);
+      *(uint2*)(dst + 8) = make_uint2(cur.v[i].z, cur.v[i].w);
+    }
+    // scores: lane l holds head 4 (l / 16) + r, position p0 + 16 h + l % 16
+    f32x4_a sc[2];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      sc[h] = f32x4_a{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k = 0; k < KS; ++k)
+        sc[h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qa[k], __builtin_bit_cast(bf16x8_a, cur.k[h][k]), sc[h], 0, 0, 0);
+    }
+    const int64_t p0 = t * 32;
+    float pv[2][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      float x0 = p0 + n16 < ctx ? sc[0][r] * sl2 : -__builtin_inff();
+      float x1 = p0 + 16 + n16 < ctx ? sc[1][r] * sl2 : -__builtin_inff();
+      float mx = fmaxf(x0, x1);
+      mx = fmaxf(mx, flip_low<1>(mx));
+      mx = fmaxf(mx, flip_low<2>(mx));
+      mx = fmaxf(mx, flip_low<4>(mx));
+      mx = fmaxf(mx, flip_low<8>(mx));
+      const float mn = fmaxf(m[r], mx);  // finite: the tile's first position is valid
+      const float alpha = __builtin_amdgcn_exp2f(m[r] - mn);
+      const float e0 = __builtin_amdgcn_exp2f(x0 - mn), e1 = __builtin_amdgcn_exp2f(x1 - mn);
+      float sum = e0 + e1;
+      sum += flip_low<1>(sum);
+      sum += flip_low<2>(sum);
+      sum += flip_low<4>(sum);
+      sum += flip_low<8>(sum);
+      l[r] = fmaf(l[r], alpha, sum);
+      m[r] = mn;
+#pragma unroll
+      for (int c = 0; c < DB; ++c) o[c][r] *= alpha;
+      pv[0][r] = e0;
+      pv[1][r] = e1;
+    }
+    // P -> LDS as [head][position] bf16
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        *(uint16_t*)(ps + (4 * q4 + r) * Geo::PS + (16 * h + n16) * 2) = f32_to_bf16(pv[h][r]);
+    wave_lds_sync();
+    // P V: A = P (head l % 16, positions 8 (l / 16) .. +7), B = V column
+    // block c (positions 8 (l / 16) .. +7 of column 16 c + l % 16)
+    const bf16x8_a pa = __builtin_bit_cast(bf16x8_a, *(const uint4*)(ps + n16 * Geo::PS + 16 * q4));
+#pragma unroll
+    for (int c = 0; c < DB; ++c) {
+      uint32_t vw[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const char* src = vs + (8 * q4 + 2 * e) * Geo::VS + (16 * c + n16) * 2;
+        vw[e] = (uint32_t)*(const uint16_t*)src | ((uint32_t)*(const uint16_t*)(src + Geo::VS) << 16);
+      }
+      o[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, __builtin_bit_cast(bf16x8_a, make_uint4(vw[0], vw[1], vw[2], vw[3])),
+                                                    o[c], 0, 0, 0);
+    }
+    wave_lds_sync();  // this tile's LDS reads done before the next tile's writes
+    cur = nxt;
+  }
+
+  // ---- the waves' states -> LDS (the V stage is free now) -------------------
+  float* po = (float*)vs;  // [GMAX][D] of this wave
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int h = 4 * q4 + r;
+    if (h < G) {
+#pragma unroll
+      for (int c = 0; c < DB; ++c) po[h * D + 16 * c + n16] = o[c][r];
+      if (n16 == 0) {
+        pm[w][h] = m[r];
+        pl[w][h] = l[r];
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- merge the waves (m in base-2 units) ---------------------------------
+  bf16* out = (bf16*)a.out;
+  for (int i = tid; i < G * D; i += NWM * 64) {
     const int h = i / D, d = i % D;
     float mx = -__builtin_inff();
-    for (int sp = 0; sp < nsplit; ++sp) mx = fmaxf(mx, a.ws_ml[(((int64_t)bh * nsplit + sp) * GMAX + h) * 2]);
-    float l = 0.f, o = 0.f;
-    for (int sp = 0; sp < nsplit; ++sp) {
-      const int64_t slot = ((int64_t)bh * nsplit + sp) * GMAX + h;
-      const float ms = a.ws_ml[slot * 2];
-      if (ms == -__builtin_inff()) continue;  // split saw no chunk
-      const float sc = expf(ms - mx);
-      l = fmaf(sc, a.ws_ml[slot * 2 + 1], l);
-      o = fmaf(sc, a.ws_o[slot * D + d], o);
+#pragma unroll
+    for (int j = 0; j < NWM; ++j) mx = fmaxf(mx, pm[j][h]);
+    float lsum = 0.f, acc = 0.f;
+    if (mx != -__builtin_inff()) {
+#pragma unroll
+      for (int j = 0; j < NWM; ++j) {
+        if (pm[j][h] == -__builtin_inff()) continue;  // wave saw no tile
+        const float sc = __builtin_amdgcn_exp2f(pm[j][h] - mx);
+        lsum = fmaf(sc, pl[j][h], lsum);
+        acc = fmaf(sc, ((const float*)(lds + j * Geo::WAVE_LDS))[h * D + d], acc);
+      }
     }
-    store_f32<T>(out, ((int64_t)b * s.Hq + g * G + h) * D + d, o / l);
+    if (nsplit == 1) {
+      store_f32<bf16>(out, ((int64_t)b * s.Hq + g * G + h) * D + d, acc / lsum);
+    } else {
+      // the merge kernel works in natural-log units
+      const int64_t slot = ((int64_t)bh * nsplit + split) * GMAX + h;
+      a.ws_o[slot * D + d] = acc;
+      if (d == 0) {
+        a.ws_ml[slot * 2] = mx == -__builtin_inff() ? mx : mx * 0.6931471805599453f;
+        a.ws_ml[slot * 2 + 1] = lsum;
+      }
+    }
   }
 }
 
@@ -883,7 +1122,8 @@ int decode_launch(hipStream_t st, DecodeArgs& a, int nsplit) {
   hipLaunchKernelGGL((decode_attn_kernel<T, D, HP>), grid, dim3(NW * 64), 0, st, a);
   MINITP_LAUNCH_CHECK();
   if (nsplit > 1) {
-    hipLaunchKernelGGL((decode_merge_kernel<T, D>), dim3(a.s.B * a.s.Hkv), dim3(256), 0, st, a, nsplit);
+    const dim3 mg((unsigned)(a.s.B * a.s.Hkv), (unsigned)cdiv(a.s.Hq / a.s.Hkv * D, MERGE_T));
+    hipLaunchKernelGGL((decode_merge_kernel<T, D>), mg, dim3(MERGE_T), 0, st, a, nsplit);
     MINITP_LAUNCH_CHECK();
   }
   return MINITP_OK;
@@ -963,6 +1203,21 @@ int prefill_by_d(hipStream_t st, const void* q, const void* k, const void* v, vo
 // two chunks per wave, up to about four blocks per CU: at batch 32 x 2,300
 // positions (64 units, 40 chunks) that is 3 splits instead of 2, 3.8 % more
 // tokens per second; one chunk per wave (5 splits) measured 8 % fewer.
+// Splits of the MFMA form: about 2 blocks per CU, each wave at least two
+// 32-position tiles.
+int64_t decode_mfma_nsplit(int64_t units, int64_t ctx) {
+  const int64_t tiles = cdiv(std::max<int64_t>(ctx, 1), 32);
+  const int64_t by_tiles = std::max<int64_t>(1, tiles / (2 * NWM));
+  return std::max<int64_t>(1, std::min<int64_t>(cdiv(512, std::max<int64_t>(units, 1)), by_tiles));
+}
+
+// The MFMA form serves bf16 groups of 2..GMAX heads at D = 64 / 128 once
+// (rows x KV heads) fill a quarter of the chip: below that the per-head
+// blocks of decode_attn_kernel spread the few units wider.
+bool decode_use_mfma(int dtype, int64_t units, int G, int D) {
+  return dtype == MINITP_BF16 && (D == 64 || D == 128) && G >= 2 && G <= GMAX && units >= 64;
+}
+
 int64_t decode_nsplit(int64_t units, int64_t ctx, int64_t D) {
   const int64_t cp = D >= 128 ? 32 : 64;
   const int64_t chunks = cdiv(std::max<int64_t>(ctx, 1), cp);
@@ -976,7 +1231,8 @@ int64_t decode_nsplit(int64_t units, int64_t ctx, int64_t D) {
 int64_t attention_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t S) {
   (void)T;
   (void)Hq;
-  const int64_t units = B * Hkv, ns = decode_nsplit(units, S, D);
+  const int64_t units = B * Hkv;
+  const int64_t ns = std::max(decode_nsplit(units, S, D), decode_mfma_nsplit(units, S));
   return units * ns * GMAX * 2 * 4 + units * ns * GMAX * D * 4;
 }
 
@@ -1005,9 +1261,28 @@ int launch_decode_attention(hipStream_t st, int dtype, const void* q, const void
   a.scale = 1.0f / sqrtf((float)s.D);
   const int64_t units = (int64_t)s.B * s.Hkv;
   // graph replays size the grid for a full cache; direct calls for this step
-  const int nsplit = (int)decode_nsplit(units, state ? s.S : cache_len + 1, s.D);
+  const int64_t ctx = state ? s.S : cache_len + 1;
+  const bool mf = decode_use_mfma(dtype, units, s.Hq / s.Hkv, s.D);
+  const int nsplit = (int)(mf ? decode_mfma_nsplit(units, ctx) : decode_nsplit(units, ctx, s.D));
   a.ws_ml = (float*)workspace;
   a.ws_o = a.ws_ml + units * nsplit * GMAX * 2;
+  if (mf) {
+    const dim3 grid((unsigned)units, (unsigned)nsplit);
+    if (s.D == 64)
+      hipLaunchKernelGGL(decode_attn_mfma_kernel<64>, grid, dim3(NWM * 64), 0, st, a);
+    else
+      hipLaunchKernelGGL(decode_attn_mfma_kernel<128>, grid, dim3(NWM * 64), 0, st, a);
+    MINITP_LAUNCH_CHECK();
+    if (nsplit > 1) {
+      const dim3 mg((unsigned)units, (unsigned)cdiv(s.Hq / s.Hkv * s.D, MERGE_T));
+      if (s.D == 64)
+        hipLaunchKernelGGL((decode_merge_kernel<bf16, 64>), mg, dim3(MERGE_T), 0, st, a, nsplit);
+      else
+        hipLaunchKernelGGL((decode_merge_kernel<bf16, 128>), mg, dim3(MERGE_T), 0, st, a, nsplit);
+      MINITP_LAUNCH_CHECK();
+    }
+    return MINITP_OK;
+  }
   return dtype == MINITP_F32 ? decode_by_d<float>(st, a, nsplit) : decode_by_d<bf16>(st, a, nsplit);
 }
 

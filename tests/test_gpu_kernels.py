@@ -295,6 +295,32 @@ def test_decode_attention_bf16(ctx, b, hq, hkv, d):
     assert ((got - ref).abs() <= ref.abs() * 2 ** -8 + 1e-6).all(), (got - ref).abs().max().item()
 
 
+@pytest.mark.parametrize("ctx", [1, 5, 31, 32, 33, 130, 767, 2304, 2559])
+@pytest.mark.parametrize("b,hq,hkv,d", [(32, 14, 2, 64), (16, 28, 4, 128), (64, 16, 2, 64)])
+def test_decode_attention_bf16_grouped_mfma(ctx, b, hq, hkv, d):
+    """The grouped MFMA form (bf16, batch rows x KV heads >= 64): P is
+    rounded to bf16 (unit roundoff 2^-8) for its product with V, so the bar
+    adds 2^-8 of the attention-weighted mean of |V| (the bound of that
+    rounding) to the output rounding's |ref| 2^-8; cache rows past the
+    context poisoned. (A float64 emulation of exactly these two roundings
+    reaches 0.0079 at context 5 for the first shape, inside this bar and
+    outside a 2^-9 one.)"""
+    g = torch.Generator().manual_seed(ctx * 17 + d + b)
+    q = torch.randn(b, 1, hq, d, generator=g).bfloat16()
+    kc = torch.randn(b, hkv, ctx + 2, d, generator=g).bfloat16()
+    kc[:, :, ctx:] = float("nan")
+    vc = torch.randn(b, hkv, ctx + 2, d, generator=g).bfloat16()
+    vc[:, :, ctx:] = float("nan")
+    got = _k().attention(q.to(DEV), kc.to(DEV), vc.to(DEV), cache_len=ctx - 1).cpu().double()
+    ref = _ref_attention(q, kc, vc, ctx - 1)
+    vabs = vc.abs()
+    vabs[:, :, ctx:] = 0
+    ref_abs = _ref_attention(q, kc, vabs, ctx - 1)
+    err = (got - ref).abs()
+    assert torch.isfinite(got).all()
+    assert (err <= (ref.abs() + ref_abs) * 2 ** -8 + 1e-6).all(), err.max().item()
+
+
 def test_decode_attention_single_key_returns_v_and_zero_q_averages():
     b, hq, hkv, d, s = 1, 14, 2, 64, 10
     kc = torch.randn(b, hkv, s, d)
