@@ -86,10 +86,11 @@ int minitp_cast_f32_bf16(void* stream, const float* in, void* out, int64_t n);
  * fused.py:57-61, 102-104), result rounded to dtype, then the epilogue.
  * x: [M, K] (row stride ldx), W: [N, K] (or [2N, K] for SWIGLU), bias: [N]
  * or NULL, y: [M, N] (row stride ldy), aux: [M, N] (stride ldy) for RESID
- * (may alias y). Small M streams W once as a GEMV; larger M runs an MFMA
- * GEMM. K must be a multiple of 8; pointers 16-byte aligned. SWIGLU is
- * served for decode rows (M <= 4) and for bf16 products of at least 96
- * output tiles of 256 rows x 128 columns (no bias). */
+ * (may alias y). Small M streams W once as a GEMV (M <= 4; bf16 up to 32
+ * rows on MFMA); larger M runs an MFMA GEMM. K must be a multiple of 8;
+ * pointers 16-byte aligned. SWIGLU is served for the GEMV shapes and for
+ * bf16 products of at least 96 output tiles of 256 rows x 128 columns (no
+ * bias). */
 int minitp_linear(void* stream, int dtype, const void* x, int64_t ldx, const void* w,
                   const void* bias, void* y, int64_t ldy, int64_t M, int64_t N, int64_t K,
                   int epilogue, const void* aux);
@@ -98,7 +99,8 @@ int minitp_linear(void* stream, int dtype, const void* x, int64_t ldx, const voi
  * layer.py:60-67) in one pass over W: every block normalises the x rows it
  * needs (fp32, rounded to dtype) and streams its share of W. Arguments as
  * minitp_linear plus norm_w [K] and eps. Serves the decode shapes only
- * (M <= 4 rows, or M == 1 up to K = 20480); others return
+ * (M <= 4 rows, M == 1 up to K = 20480; bf16 5..32 rows up to K = 1024);
+ * others return
  * MINITP_ERR_UNSUPPORTED (use minitp_rmsnorm, then minitp_linear). The norm
  * sums x^2 in a different order than minitp_rmsnorm, so the two agree to
  * rounding, not bitwise. */

@@ -191,8 +191,8 @@ int minitp_linear(void* stream, int dtype, const void* x, int64_t ldx, const voi
     if (dtype == MINITP_BF16 && bias == nullptr && aligned16(x) && aligned16(w) &&
         gemm_tile_supported(M, N, K, ldx, ldy, true))
       return launch_gemm_tile(st, x, ldx, w, nullptr, y, ldy, M, N, K, true);
-    set_error("linear: SWIGLU epilogue is served for decode rows (M <= 4) and bf16 prompts of at least 96 "
-              "256 x 128 output tiles; use NONE + minitp_silu_mul");
+    set_error("linear: SWIGLU epilogue is served for decode rows (M <= 4, bf16 up to 32) and bf16 prompts of at "
+              "least 96 256 x 128 output tiles; use NONE + minitp_silu_mul");
     return MINITP_ERR_UNSUPPORTED;
   }
   return launch_gemm(st, dtype, x, ldx, w, bias, y, ldy, M, N, K, epilogue, aux);
