@@ -924,6 +924,23 @@ __device__ __forceinline__ uint4 norm_chunk(const uint4& xb, const uint4& wb, fl
   return pack_bf16x8(o);
 }
 
+// Single-batch staging: a wave's K range is at most MF_ONE steps, i.e. 32
+// 16-byte chunks per row. Rows are loaded coalesced (lane l takes chunk
+// l % 32 of row l / 32 + 2 t: 512 contiguous bytes per row instead of the
+// operand layout's 64) and stored to wave-private LDS with chunk c of row r
+// at slot c ^ (r & 15), so the 16 lanes that read one operand column (16
+// rows, one chunk) hit 16 different bank groups. The weights pass first,
+// then the input rows, through the same 16 KiB per wave (two blocks per CU
+// stay resident).
+constexpr int MF_STAGE_CH = 32;
+constexpr int MF_X_STAGE = 32 * MF_STAGE_CH * 16;   // the 32 input rows of a wave's K range
+constexpr int MF_W_STAGE = 16 * MF_STAGE_CH * 16;   // one tuple's 16 weight rows
+__device__ __forceinline__ uint32_t mf_slot(int r, int c) { return (uint32_t)((r * MF_STAGE_CH + (c ^ (r & 15))) * 16); }
+template <int NT>
+constexpr int mf_wave_stage() { return MF_X_STAGE > NT * MF_W_STAGE ? MF_X_STAGE : NT * MF_W_STAGE; }
+template <int NT>
+constexpr int mf_stage_bytes() { return 4 * mf_wave_stage<NT>(); }
+
 template <int PRO, int EPI, int KSPLIT, int NT, int NB, bool MULTI>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
   // A wave owns NT tuples that share each A fragment it loads, over a K
@@ -1002,7 +1019,37 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
   };
 
   Batch b0;
-  issue(b0, s_begin);
+  // !MULTI: the wave's whole K range staged through LDS (coalesced loads)
+  extern __shared__ __attribute__((aligned(16))) char mf_stage[];
+  char* xs_lds = mf_stage + wave * mf_wave_stage<NT>();
+  char* ws_lds = xs_lds;
+  uint4 wl[NT][8], xl[16];
+  const int64_t kb = s_begin * 32;
+  const int nch = (int)std::max<int64_t>(0, std::min<int64_t>((s_end - s_begin) * 4, (K - kb) / 8));
+  if constexpr (!MULTI) {
+    // input rows first (the norm prologue needs them first), then weights
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int q = lane + 64 * t, r = q >> 5, c = q & 31;
+      const bool ok = r < M && c < nch;
+      xl[t] = span_load16<0>(xr, ok ? (uint32_t)(((int64_t)r * a.ldx + kb + 8 * c) * 2) : OOBW);
+    }
+    if constexpr (PRO == PRO_NORM) {
+#pragma unroll
+      for (int i = 0; i < NB; ++i) b0.nw[i] = span_load16<0>(nr, off(0u, s_begin + i));
+    }
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int q = lane + 64 * t, r = q >> 5, c = q & 31;
+        const int64_t wrow = r < P16 ? ra[j] + r : rb[j] + (r - P16);
+        const bool ok = t0 + j < ntup && row_valid<EPI>(wrow, a) && c < nch;
+        wl[j][t] = span_load16<W_AUX>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
+      }
+  } else {
+    issue(b0, s_begin);
+  }
   // the epilogue's side inputs (residual, QKV bias, the single-token RoPE
   // rows) load now, underneath the weights, not after the products: lane
   // l < 8 of a K-split leader finishes pair l of each tuple for rows
@@ -1040,6 +1087,37 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
     }
   }
   if constexpr (!MULTI) {
+    // coalesced rows -> swizzled LDS -> operand fragments: the input rows,
+    // then (same wave-private buffer) the weights
+    auto wave_sync = []() {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int q = lane + 64 * t;
+      *(uint4*)(xs_lds + mf_slot(q >> 5, q & 31)) = xl[t];
+    }
+    wave_sync();
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      b0.xa[i] = *(const uint4*)(xs_lds + mf_slot(m0, 4 * i + kq));
+      b0.xc[i] = *(const uint4*)(xs_lds + mf_slot(m1, 4 * i + kq));
+    }
+    wave_sync();
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int q = lane + 64 * t;
+        *(uint4*)(ws_lds + j * MF_W_STAGE + mf_slot(q >> 5, q & 31)) = wl[j][t];
+      }
+    wave_sync();
+#pragma unroll
+    for (int i = 0; i < NB; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) b0.w[i][j] = *(const uint4*)(ws_lds + j * MF_W_STAGE + mf_slot(nidx, 4 * i + kq));
     if constexpr (PRO == PRO_NORM) {
       // sums of squares of this wave's K range (packed dots: exact products,
       // fp32 sums), over the four lanes of a row (l, l + 16, l + 32, l + 48),
@@ -1090,14 +1168,17 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
       red[wave][j][1][lane] = acc[j][1];
     }
     __syncthreads();
-    if (kw == 0) {
-      for (int k = 1; k < KSPLIT; ++k)
+    // every wave adds the K-split tiles in wave order (the same sums in
+    // every wave) and finishes accumulator register r = kw of each tile, so
+    // the epilogue's work is spread over the block
 #pragma unroll
-        for (int j = 0; j < NT; ++j) {
-          acc[j][0] += red[wave + k][j][0][lane];
-          acc[j][1] += red[wave + k][j][1][lane];
-        }
-    }
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        f32x4_m v = red[slot * KSPLIT][j][h][lane];
+        for (int k = 1; k < KSPLIT; ++k) v += red[slot * KSPLIT + k][j][h][lane];
+        acc[j][h] = v;
+      }
   }
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
@@ -1107,7 +1188,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
       pa0[r] = __shfl_xor(acc[j][0][r], 8);
       pa1[r] = __shfl_xor(acc[j][1][r], 8);
     }
-    if (kw != 0 || t0 + j >= ntup || nidx >= P16) continue;
+    if (t0 + j >= ntup || nidx >= P16) continue;
     const int p = nidx;
     const int64_t row_a = ra[j] + p, row_b = rb[j] + p;
     const bool oka = row_valid<EPI>(row_a, a), okb = row_valid<EPI>(row_b, a);
@@ -1126,6 +1207,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
     for (int h = 0; h < 2; ++h)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
+        if (KSPLIT > 1 && r % KSPLIT != kw) continue;
         const int m = h * 16 + 4 * kq + r;
         if (m >= M) continue;
         const float va = acc[j][h][r], vb = h ? pa1[r] : pa0[r];
@@ -1213,16 +1295,32 @@ __global__ __launch_bounds__(256) void gemv_mfma_split_kernel(GemvArgs a, int ns
     const int64_t k = s * 32 + kq * 8;
     return (base != OOBW && s < s_end && k < K) ? base + (uint32_t)(k * 2) : OOBW;
   };
-  uint4 w[MF_ONE][NT], xa[MF_ONE], xc[MF_ONE];
+  (void)off;
+  (void)wbase;
+  (void)xb0;
+  (void)xb1;
+  // the wave's K range staged through LDS as in gemv_mfma_kernel:
+  // coalesced loads (input rows first), swizzled wave-private tiles
+  extern __shared__ __attribute__((aligned(16))) char mf_stage[];
+  char* st_lds = mf_stage + kw * mf_wave_stage<NT>();
+  const int64_t kb = s_begin * 32;
+  const int nch = (int)std::max<int64_t>(0, std::min<int64_t>((s_end - s_begin) * 4, (K - kb) / 8));
+  uint4 wl[NT][8], xl[16];
 #pragma unroll
-  for (int i = 0; i < MF_ONE; ++i)
-#pragma unroll
-    for (int j = 0; j < NT; ++j) w[i][j] = span_load16<W_AUX>(wr, off(wbase[j], s_begin + i));
-#pragma unroll
-  for (int i = 0; i < MF_ONE; ++i) {
-    xa[i] = span_load16<0>(xr, off(xb0, s_begin + i));
-    xc[i] = span_load16<0>(xr, off(xb1, s_begin + i));
+  for (int t = 0; t < 16; ++t) {
+    const int q = lane + 64 * t, r = q >> 5, c = q & 31;
+    const bool ok = r < M && c < nch;
+    xl[t] = span_load16<0>(xr, ok ? (uint32_t)(((int64_t)r * a.ldx + kb + 8 * c) * 2) : OOBW);
   }
+#pragma unroll
+  for (int j = 0; j < NT; ++j)
+#pragma unroll
+    for (int t = 0; t < 8; ++t) {
+      const int q = lane + 64 * t, r = q >> 5, c = q & 31;
+      const int64_t wrow = r < P16 ? ra[j] + r : rb[j] + (r - P16);
+      const bool ok = t0 + j < ntup && row_valid<EPI>(wrow, a) && c < nch;
+      wl[j][t] = span_load16<W_AUX>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
+    }
   // the epilogue's side inputs, loaded underneath the weights (only the
   // block that finishes a group uses them)
   constexpr int NSIDE = EPI == EPI_RESID ? 16 : (EPI == EPI_QKV_ROPE1 ? 6 : (EPI == EPI_QKV_ROPE ? 2 : 1));
@@ -1256,6 +1354,38 @@ __global__ __launch_bounds__(256) void gemv_mfma_split_kernel(GemvArgs a, int ns
         sv[j][5] = a.st->rope_sin[i + D / 2];
       }
     }
+  }
+  uint4 w[MF_ONE][NT], xa[MF_ONE], xc[MF_ONE];
+  {
+    auto wave_sync = []() {
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+#pragma unroll
+    for (int t = 0; t < 16; ++t) {
+      const int q = lane + 64 * t;
+      *(uint4*)(st_lds + mf_slot(q >> 5, q & 31)) = xl[t];
+    }
+    wave_sync();
+#pragma unroll
+    for (int i = 0; i < MF_ONE; ++i) {
+      xa[i] = *(const uint4*)(st_lds + mf_slot(m0, 4 * i + kq));
+      xc[i] = *(const uint4*)(st_lds + mf_slot(m1, 4 * i + kq));
+    }
+    wave_sync();
+#pragma unroll
+    for (int j = 0; j < NT; ++j)
+#pragma unroll
+      for (int t = 0; t < 8; ++t) {
+        const int q = lane + 64 * t;
+        *(uint4*)(st_lds + j * MF_W_STAGE + mf_slot(q >> 5, q & 31)) = wl[j][t];
+      }
+    wave_sync();
+#pragma unroll
+    for (int i = 0; i < MF_ONE; ++i)
+#pragma unroll
+      for (int j = 0; j < NT; ++j) w[i][j] = *(const uint4*)(st_lds + j * MF_W_STAGE + mf_slot(nidx, 4 * i + kq));
   }
   f32x4_m acc[NT][2];
 #pragma unroll
@@ -1303,8 +1433,10 @@ __global__ __launch_bounds__(256) void gemv_mfma_split_kernel(GemvArgs a, int ns
     }
   }
   __syncthreads();
-  if (last && kw == 0) {
-    // ---- the group's last block: segments in order, then the epilogue ----
+  if (!last) return;
+  {
+    // ---- the group's last block: segments in order (every wave the same
+    // sums), then the epilogue, accumulator register r = kw per wave ----
     // (SB segments' loads in flight at a time; past nseg they read zeros)
     constexpr int SB = 8 / NT;
 #pragma unroll
@@ -1353,6 +1485,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_split_kernel(GemvArgs a, int ns
       for (int h = 0; h < 2; ++h)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
+          if (r != kw) continue;
           const int m = h * 16 + 4 * kq + r;
           if (m >= M) continue;
           const float va = acc[j][h][r], vb = h ? pa1[r] : pa0[r];
@@ -1417,7 +1550,11 @@ bool mf_split_ok(const GemvArgs& a) {
 template <int EPI, int NT>
 int launch_mfma_split_nt(hipStream_t st, const GemvArgs& a, const MfSplit& g) {
   const dim3 grid((unsigned)g.groups, (unsigned)g.nseg);
-  hipLaunchKernelGGL((gemv_mfma_split_kernel<EPI, NT>), grid, dim3(256), 0, st, a, g.nseg, g.seg_steps);
+  auto kern = gemv_mfma_split_kernel<EPI, NT>;
+  const int lds = mf_stage_bytes<NT>();
+  const int rc = ensure_lds_limit((const void*)kern, lds);
+  if (rc) return rc;
+  hipLaunchKernelGGL(kern, grid, dim3(256), lds, st, a, g.nseg, g.seg_steps);
   MINITP_LAUNCH_CHECK();
   return MINITP_OK;
 }
@@ -1438,7 +1575,11 @@ int launch_mfma_nt(hipStream_t st, const GemvArgs& a, int64_t ntup) {
   const unsigned grid = (unsigned)cdiv(ntup, NT);
   const int64_t per_wave = cdiv(cdiv(a.K, 32), 4);
   if (per_wave <= MF_ONE) {
-    hipLaunchKernelGGL((gemv_mfma_kernel<PRO, EPI, 4, NT, MF_ONE, false>), dim3(grid), dim3(256), 0, st, a);
+    auto kern = gemv_mfma_kernel<PRO, EPI, 4, NT, MF_ONE, false>;
+    const int lds = mf_stage_bytes<NT>();
+    const int rc = ensure_lds_limit((const void*)kern, lds);
+    if (rc) return rc;
+    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, a);
   } else if constexpr (PRO == PRO_NORM) {
     set_error("gemv: the RMSNorm prologue on MFMA serves K <= %d", 4 * 32 * MF_ONE);
     return MINITP_ERR_UNSUPPORTED;
@@ -1459,10 +1600,10 @@ int launch_mfma(hipStream_t st, const GemvArgs& a) {
     if constexpr (PRO == PRO_NONE) {
       if (mf_split_ok<EPI>(a)) return launch_mfma_split<EPI>(st, a);
     }
-    // K split over the block's 4 waves; many tuples: 2 per wave (the input
-    // rows read once per 32 weight rows), few: 1 per wave (more blocks)
+    // K split over the block's 4 waves, one tuple per block (two per block
+    // measured slower at every shape once the loads were staged: 13.0
+    // against 12.2 us for the batch-32 gate/up)
     const int64_t ntup = num_tuples16<EPI>(a);
-    if (ntup >= 512) return launch_mfma_nt<PRO, EPI, 2>(st, a, ntup);
     return launch_mfma_nt<PRO, EPI, 1>(st, a, ntup);
   }
 }

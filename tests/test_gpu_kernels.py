@@ -93,7 +93,7 @@ def _ref_linear(x, w, b=None):
     return F.linear(x.double(), w.double(), None if b is None else b.double())
 
 
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 33, 130])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 5, 8, 16, 32, 33, 130])
 @pytest.mark.parametrize("n,k", [(64, 64), (1152, 896), (1000, 64), (896, 4864), (300, 136)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_linear_shapes(m, n, k, dtype):
@@ -110,7 +110,7 @@ def test_linear_shapes(m, n, k, dtype):
         assert ((got - ref).abs() <= ref.abs() * 2 ** -8 + 1e-3 * scale).all()
 
 
-@pytest.mark.parametrize("m", [1, 3, 40])
+@pytest.mark.parametrize("m", [1, 3, 19, 32, 40])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_linear_residual_epilogue(m, dtype):
     from minitp import _native as N
@@ -126,12 +126,12 @@ def test_linear_residual_epilogue(m, dtype):
     torch.testing.assert_close(y.cpu(), (r.float() + lin.float()).to(dtype), atol=0, rtol=0)
 
 
-@pytest.mark.parametrize("m", [1, 2, 4])
+@pytest.mark.parametrize("m", [1, 2, 4, 7, 32])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_linear_swiglu_epilogue_equals_split(m, dtype):
     from minitp import _native as N
 
-    if dtype == torch.float32 and m == 4:
+    if dtype == torch.float32 and m >= 4:
         pytest.skip("fp32 rows of K=896 take the GEMV register path only up to M=2; SWIGLU is GEMV-only")
     g = torch.Generator().manual_seed(7 + m)
     inter, k = 256, 896
@@ -145,7 +145,7 @@ def test_linear_swiglu_epilogue_equals_split(m, dtype):
     torch.testing.assert_close(split.cpu().float(), ref.float(), atol=1e-6, rtol=2 ** -7)
 
 
-@pytest.mark.parametrize("m,k", [(1, 896), (2, 896), (4, 896), (1, 4864), (2, 4864)])
+@pytest.mark.parametrize("m,k", [(1, 896), (2, 896), (4, 896), (1, 4864), (2, 4864), (7, 896), (32, 896), (32, 1024)])
 @pytest.mark.parametrize("epilogue", ["none", "bias", "swiglu", "resid"])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_rmsnorm_linear_matches_two_step_reference(m, k, epilogue, dtype):
@@ -153,7 +153,7 @@ def test_rmsnorm_linear_matches_two_step_reference(m, k, epilogue, dtype):
     output (layer.py:39-42 then linear.py:57-58)."""
     from minitp import _native as N
 
-    if dtype == torch.float32 and (m == 4 or k == 4864) and m > 1:
+    if dtype == torch.float32 and (m >= 4 or k == 4864) and m > 1:
         pytest.skip("fp32 rows this long take the register GEMV path only for fewer rows")
     g = torch.Generator().manual_seed(m * 31 + k + len(epilogue))
     n = 512
