@@ -390,7 +390,10 @@ __global__ __launch_bounds__(MERGE_T) void decode_merge_kernel(DecodeArgs a, int
 // round robin, each tile's K and V loads issued before the previous tile's
 // math. Waves and splits merge as in decode_attn_kernel (same workspace
 // layout and merge kernel).
-constexpr int NWM = 4;
+#ifndef MINITP_DEC_MF_WAVES
+#define MINITP_DEC_MF_WAVES 8
+#endif
+constexpr int NWM = MINITP_DEC_MF_WAVES;
 typedef __bf16 bf16x8_a __attribute__((ext_vector_type(8)));
 typedef float f32x4_a __attribute__((ext_vector_type(4)));
 
@@ -409,7 +412,7 @@ __global__ __launch_bounds__(NWM * 64) void decode_attn_mfma_kernel(DecodeArgs a
   constexpr int DB = D / 16;   // 16-column blocks of the output
   constexpr int VL = Geo::VL;
   constexpr uint32_t OOB = 0xffffffffu;
-  __shared__ __attribute__((aligned(16))) char lds[NWM * Geo::WAVE_LDS];
+  extern __shared__ __attribute__((aligned(16))) char lds[];  // NWM * Geo::WAVE_LDS
   __shared__ float pm[NWM][GMAX], pl[NWM][GMAX];
 
   const AttnShape& s = a.s;
@@ -1205,10 +1208,16 @@ int prefill_by_d(hipStream_t st, const void* q, const void* k, const void* v, vo
 // tokens per second; one chunk per wave (5 splits) measured 8 % fewer.
 // Splits of the MFMA form: about 2 blocks per CU, each wave at least two
 // 32-position tiles.
+#ifndef MINITP_DEC_MF_BLOCKS
+#define MINITP_DEC_MF_BLOCKS 256
+#endif
+#ifndef MINITP_DEC_MF_TILES
+#define MINITP_DEC_MF_TILES 2
+#endif
 int64_t decode_mfma_nsplit(int64_t units, int64_t ctx) {
   const int64_t tiles = cdiv(std::max<int64_t>(ctx, 1), 32);
-  const int64_t by_tiles = std::max<int64_t>(1, tiles / (2 * NWM));
-  return std::max<int64_t>(1, std::min<int64_t>(cdiv(512, std::max<int64_t>(units, 1)), by_tiles));
+  const int64_t by_tiles = std::max<int64_t>(1, tiles / (MINITP_DEC_MF_TILES * NWM));
+  return std::max<int64_t>(1, std::min<int64_t>(cdiv(MINITP_DEC_MF_BLOCKS, std::max<int64_t>(units, 1)), by_tiles));
 }
 
 // The MFMA form serves bf16 groups of 2..GMAX heads at D = 64 / 128 once
@@ -1268,10 +1277,14 @@ int launch_decode_attention(hipStream_t st, int dtype, const void* q, const void
   a.ws_o = a.ws_ml + units * nsplit * GMAX * 2;
   if (mf) {
     const dim3 grid((unsigned)units, (unsigned)nsplit);
+    const void* kern = s.D == 64 ? (const void*)decode_attn_mfma_kernel<64> : (const void*)decode_attn_mfma_kernel<128>;
+    const int lds = NWM * (s.D == 64 ? MfDec<64>::WAVE_LDS : MfDec<128>::WAVE_LDS);
+    int rc = ensure_lds_limit(kern, lds);
+    if (rc) return rc;
     if (s.D == 64)
-      hipLaunchKernelGGL(decode_attn_mfma_kernel<64>, grid, dim3(NWM * 64), 0, st, a);
+      hipLaunchKernelGGL(decode_attn_mfma_kernel<64>, grid, dim3(NWM * 64), lds, st, a);
     else
-      hipLaunchKernelGGL(decode_attn_mfma_kernel<128>, grid, dim3(NWM * 64), 0, st, a);
+      hipLaunchKernelGGL(decode_attn_mfma_kernel<128>, grid, dim3(NWM * 64), lds, st, a);
     MINITP_LAUNCH_CHECK();
     if (nsplit > 1) {
       const dim3 mg((unsigned)units, (unsigned)cdiv(s.Hq / s.Hkv * s.D, MERGE_T));

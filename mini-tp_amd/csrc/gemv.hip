@@ -1515,7 +1515,7 @@ struct MfSplit {
   int64_t groups, part_bytes;
 };
 #ifndef MINITP_MF_TARGET_BLOCKS
-#define MINITP_MF_TARGET_BLOCKS 512
+#define MINITP_MF_TARGET_BLOCKS 256
 #endif
 #ifndef MINITP_MF_MIN_STEPS
 #define MINITP_MF_MIN_STEPS 1
