@@ -184,7 +184,8 @@ template <typename T, int EPI>
 __device__ __forceinline__ void finish_pair(const GemvArgs& a, int m, int64_t row_a, int64_t row_b, bool oka,
                                             bool okb, float va, float vb, const float* side, int64_t pos) {
   if constexpr (EPI == EPI_STORE) {
-    T* y = (T*)a.y;
+    // no output pointer: the step's logits buffer (the LM head in a forward)
+    T* y = (T*)(a.y != nullptr ? a.y : a.st->args.logits);
     const T* bias = (const T*)a.bias;
     if (oka) store_f32<T>(y, m * a.ldy + row_a, va + (bias ? load_f32<T>(bias, row_a) : 0.f));
     if (okb) store_f32<T>(y, m * a.ldy + row_b, vb + (bias ? load_f32<T>(bias, row_b) : 0.f));
@@ -1235,6 +1236,206 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
 constexpr int MF_ONE = 8;
 
 // ---------------------------------------------------------------------------
+// gemv_mfma_loop_kernel: the single-batch MFMA GEMV for products with many
+// tuples (the batch-32 gate/up: 608, the LM head: 9,496). A block's input
+// fragments, normalized once, serve several tuples in turn (t = blockIdx.x,
+// + gridDim.x, ...): the RMSNorm prologue, about 650 of the 1,130 VALU
+// instructions per wave when every tuple has a block of its own, is paid
+// once per block. Each tuple's weights are staged like gemv_mfma_kernel's;
+// the loads of the tuples MF_LOOP_PD on go out before the current tuple's
+// products (register buffers in rotation), and the K-split partial tiles
+// alternate between two LDS buffers, so a tuple costs one block barrier.
+// The two buffers (8 KB each) sit in the second halves of waves 0 and 1's
+// input stages, which the weight stages leave free: 64.5 KB of LDS a block,
+// two blocks a CU.
+#ifndef MINITP_MF_LOOP_PD
+#define MINITP_MF_LOOP_PD 2
+#endif
+template <int PRO, int EPI>
+__global__ __launch_bounds__(256) void gemv_mfma_loop_kernel(GemvArgs a) {
+  static_assert(EPI == EPI_STORE || EPI == EPI_SWIGLU, "the tuple loop serves the store and SwiGLU epilogues");
+  constexpr int MF_LOOP_PD = MINITP_MF_LOOP_PD;  // tuples whose weight loads are in flight
+  constexpr int NB = 8;  // steps of 32 per wave (the single-batch form)
+  constexpr uint32_t OOBW = 0xffffffffu;
+  static_assert(4 * 2 * 64 * (int)sizeof(f32x4_m) == MF_W_STAGE && 2 * MF_W_STAGE == MF_X_STAGE, "LDS plan");
+  __shared__ float nrm[4][32];
+  extern __shared__ __attribute__((aligned(16))) char mf_stage[];
+  const int tid = threadIdx.x, lane = tid & 63, kw = tid >> 6;
+  const int M = (int)a.M;
+  const int64_t K = a.K;
+  const int64_t ntup = num_tuples16<EPI>(a);
+  const int nidx = lane & 15, kq = lane >> 4;
+  const int64_t w_rows = EPI == EPI_SWIGLU ? 2 * a.N : a.N;
+  const __amdgpu_buffer_rsrc_t wr = span_rsrc(a.w, (uint32_t)(w_rows * K * 2));
+  const __amdgpu_buffer_rsrc_t xr = span_rsrc(a.x, (uint32_t)(((int64_t)(M - 1) * a.ldx + K) * 2));
+  const __amdgpu_buffer_rsrc_t nr = span_rsrc(a.norm_w, PRO == PRO_NORM ? (uint32_t)(K * 2) : 0u);
+  const int m0 = nidx, m1 = 16 + nidx;
+  const int64_t nsteps = cdiv(K, 32), per = cdiv(nsteps, 4);
+  const int64_t s_begin = kw * per, s_end = std::min(nsteps, s_begin + per);
+  const int64_t kb = s_begin * 32;
+  const int nch = (int)std::max<int64_t>(0, std::min<int64_t>((s_end - s_begin) * 4, (K - kb) / 8));
+  char* st_lds = mf_stage + kw * MF_X_STAGE;
+  auto wave_sync = []() {
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+  };
+  auto load_w = [&](int64_t t, uint4 (&wl)[8]) {
+    int64_t ra = 0, rb = 0;
+    const bool live = t < ntup;
+    if (live) tuple16_rows<EPI>(t, a, ra, rb);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int q = lane + 64 * u, r = q >> 5, c = q & 31;
+      const int64_t wrow = r < P16 ? ra + r : rb + (r - P16);
+      const bool ok = live && row_valid<EPI>(wrow, a) && c < nch;
+      wl[u] = span_load16<W_AUX>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
+    }
+  };
+
+  // ---- input rows (and norm weight), then the first tuple's weights -------
+  uint4 xl[16], nw[NB], wl[MF_LOOP_PD][8];
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int q = lane + 64 * u, r = q >> 5, c = q & 31;
+    const bool ok = r < M && c < nch;
+    xl[u] = span_load16<0>(xr, ok ? (uint32_t)(((int64_t)r * a.ldx + kb + 8 * c) * 2) : OOBW);
+  }
+  if constexpr (PRO == PRO_NORM) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int64_t s = s_begin + i, k = s * 32 + kq * 8;
+      nw[i] = span_load16<0>(nr, s < s_end && k < K ? (uint32_t)(k * 2) : OOBW);
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < MF_LOOP_PD; ++j) load_w(blockIdx.x + j * (int64_t)gridDim.x, wl[j]);
+
+  // ---- A fragments through the wave's LDS stage, normalized once ----------
+  uint4 xa[NB], xc[NB];
+#pragma unroll
+  for (int u = 0; u < 16; ++u) {
+    const int q = lane + 64 * u;
+    *(uint4*)(st_lds + mf_slot(q >> 5, q & 31)) = xl[u];
+  }
+  wave_sync();
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    xa[i] = *(const uint4*)(st_lds + mf_slot(m0, 4 * i + kq));
+    xc[i] = *(const uint4*)(st_lds + mf_slot(m1, 4 * i + kq));
+  }
+  wave_sync();
+  if constexpr (PRO == PRO_NORM) {
+    float ss0 = 0.f, ss1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      ss0 = dot_chunk<bf16>(xa[i], nullptr, xa[i], ss0);
+      ss1 = dot_chunk<bf16>(xc[i], nullptr, xc[i], ss1);
+    }
+    ss0 += __shfl_xor(ss0, 16);
+    ss0 += __shfl_xor(ss0, 32);
+    ss1 += __shfl_xor(ss1, 16);
+    ss1 += __shfl_xor(ss1, 32);
+    if (kq == 0) {
+      nrm[kw][m0] = ss0;
+      nrm[kw][m1] = ss1;
+    }
+    __syncthreads();  // also: every wave is done with its input stage
+    float u0 = 0.f, u1 = 0.f;
+    for (int k = 0; k < 4; ++k) {
+      u0 += nrm[k][m0];
+      u1 += nrm[k][m1];
+    }
+    const float r0 = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(u0, (float)K), a.eps)));
+    const float r1 = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(u1, (float)K), a.eps)));
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      xa[i] = norm_chunk(xa[i], nw[i], r0);
+      xc[i] = norm_chunk(xc[i], nw[i], r1);
+    }
+  } else {
+    __syncthreads();  // every wave is done with its input stage (the sum buffers overlay them)
+  }
+
+  // ---- tuples ---------------------------------------------------------------
+  // Outputs go out through a buffer resource, every lane issuing the same
+  // stores each tuple (an offset past the end drops one): with no store
+  // behind a branch, the compiler's count of memory operations in flight
+  // stays exact across the loop, and the wait before a tuple's weights are
+  // staged lets the loads of the tuples after it stay in flight.
+  bf16* yp = (bf16*)(a.y != nullptr ? a.y : a.st->args.logits);
+  const __amdgpu_buffer_rsrc_t yr = span_rsrc(yp, (uint32_t)(((int64_t)(M - 1) * a.ldy + a.N) * 2));
+  const __amdgpu_buffer_rsrc_t br = span_rsrc(a.bias, a.bias != nullptr ? (uint32_t)(a.N * 2) : 0u);
+  const int kwu = __builtin_amdgcn_readfirstlane(kw);
+  auto tuple = [&](const int64_t t, const int it, uint4 (&wl)[8]) {
+    int64_t ra = 0, rb = 0;
+    tuple16_rows<EPI>(t, a, ra, rb);
+    const int p = nidx & (P16 - 1);
+    const int64_t row_a = ra + p, row_b = rb + p;
+    const bool oka = nidx < P16 && row_valid<EPI>(row_a, a), okb = nidx < P16 && row_valid<EPI>(row_b, a);
+    float bias_a = 0.f, bias_b = 0.f;
+    if constexpr (EPI == EPI_STORE) {  // a zero-length resource reads zeros
+      bias_a = bf16_to_f32((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(br, oka ? (uint32_t)(row_a * 2) : OOBW, 0, 0));
+      bias_b = bf16_to_f32((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(br, okb ? (uint32_t)(row_b * 2) : OOBW, 0, 0));
+    }
+    // this tuple's weights -> fragments; those MF_LOOP_PD tuples on go out
+    uint4 w[NB];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int q = lane + 64 * u;
+      *(uint4*)(st_lds + mf_slot(q >> 5, q & 31)) = wl[u];
+    }
+    wave_sync();
+#pragma unroll
+    for (int i = 0; i < NB; ++i) w[i] = *(const uint4*)(st_lds + mf_slot(nidx, 4 * i + kq));
+    wave_sync();
+    load_w(t + MF_LOOP_PD * (int64_t)gridDim.x, wl);
+    f32x4_m acc[2] = {f32x4_m{0.f, 0.f, 0.f, 0.f}, f32x4_m{0.f, 0.f, 0.f, 0.f}};
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const bf16x8_m bw = __builtin_bit_cast(bf16x8_m, w[i]);
+      acc[0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_m, xa[i]), bw, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_m, xc[i]), bw, acc[1], 0, 0, 0);
+    }
+    // K-split sum (two alternating buffers: one barrier per tuple): every
+    // wave the same sums in wave order, wave kw finishing register kw
+    f32x4_m (*rb_buf)[2][64] = (f32x4_m(*)[2][64])(mf_stage + (it & 1) * MF_X_STAGE + MF_W_STAGE);
+    rb_buf[kw][0][lane] = acc[0];
+    rb_buf[kw][1][lane] = acc[1];
+    __syncthreads();
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      f32x4_m v = rb_buf[0][h][lane];
+      for (int k = 1; k < 4; ++k) v += rb_buf[k][h][lane];
+      // register kw of the sum (row 16 h + 4 kq + kw, column nidx), and the
+      // partner column nidx ^ 8 (row_ror:8 within each 16-lane row)
+      const float va = kwu == 0 ? v[0] : kwu == 1 ? v[1] : kwu == 2 ? v[2] : v[3];
+      const float vb = dpp_f32<0x128>(0.f, va);
+      const int m = h * 16 + 4 * kq + kwu;
+      const bool okm = m < M;
+      if constexpr (EPI == EPI_STORE) {
+        const uint16_t ya = f32_to_bf16(va + bias_a), yb = f32_to_bf16(vb + bias_b);
+        __builtin_amdgcn_raw_buffer_store_b16(ya, yr, okm && oka ? (uint32_t)((m * a.ldy + row_a) * 2) : OOBW, 0, 0);
+        __builtin_amdgcn_raw_buffer_store_b16(yb, yr, okm && okb ? (uint32_t)((m * a.ldy + row_b) * 2) : OOBW, 0, 0);
+      } else {
+        const uint16_t ya = f32_to_bf16(swiglu<bf16>(round_to<bf16>(va), round_to<bf16>(vb)));
+        __builtin_amdgcn_raw_buffer_store_b16(ya, yr, okm && oka ? (uint32_t)((m * a.ldy + row_a) * 2) : OOBW, 0, 0);
+      }
+    }
+  };
+  int it = 0;
+  for (int64_t tb = blockIdx.x; tb < ntup; tb += MF_LOOP_PD * (int64_t)gridDim.x) {
+#pragma unroll
+    for (int j = 0; j < MF_LOOP_PD; ++j) {
+      const int64_t t = tb + j * (int64_t)gridDim.x;
+      if (t >= ntup) break;
+      tuple(t, it++, wl[j]);
+    }
+  }
+}
+
+
+// ---------------------------------------------------------------------------
 // gemv_mfma_split_kernel: decode rows 5..32 (bf16) with K split over blocks
 // as well as over a block's 4 waves, no RMSNorm prologue. The grid is groups
 // of NT tuples (x) by K segments of seg_steps steps of 32 (y): the few-tuple
@@ -1570,10 +1771,39 @@ int launch_mfma_split(hipStream_t st, const GemvArgs& a) {
   }
 }
 
+// The tuple-loop form from MINITP_MF_LOOP_MIN tuples: at least
+// MINITP_MF_LOOP_PER tuples a block, and at most MINITP_MF_LOOP_BLOCKS blocks
+// (two a CU). Measured on the batch-32 decode (kernel trace): gate/up (608
+// tuples) 10.3 us at 2 a block, 8.9-9.3 at 3, 9.9 at 4; the LM head (9,496
+// tuples) 56 us on 500 blocks, 60 on 256, 100 on 128. Two tuples' loads in
+// flight against one: LM head 56 against 59 us, gate/up within noise; three:
+// slower (1.167 against 1.143 ms a step).
+#ifndef MINITP_MF_LOOP_MIN
+#define MINITP_MF_LOOP_MIN 512
+#endif
+#ifndef MINITP_MF_LOOP_PER
+#define MINITP_MF_LOOP_PER 3
+#endif
+#ifndef MINITP_MF_LOOP_BLOCKS
+#define MINITP_MF_LOOP_BLOCKS 512
+#endif
 template <int PRO, int EPI, int NT>
 int launch_mfma_nt(hipStream_t st, const GemvArgs& a, int64_t ntup) {
   const unsigned grid = (unsigned)cdiv(ntup, NT);
   const int64_t per_wave = cdiv(cdiv(a.K, 32), 4);
+  if constexpr (EPI == EPI_STORE || EPI == EPI_SWIGLU) {
+    if (per_wave <= MF_ONE && NT == 1 && ntup >= MINITP_MF_LOOP_MIN) {
+      // many tuples: several a block, the input rows' prologue shared
+      auto kern = gemv_mfma_loop_kernel<PRO, EPI>;
+      const int lds = 4 * MF_X_STAGE;
+      const int rc = ensure_lds_limit((const void*)kern, lds);
+      if (rc) return rc;
+      const int64_t per = std::max<int64_t>(MINITP_MF_LOOP_PER, cdiv(ntup, (int64_t)MINITP_MF_LOOP_BLOCKS));
+      hipLaunchKernelGGL(kern, dim3((unsigned)cdiv(ntup, per)), dim3(256), lds, st, a);
+      MINITP_LAUNCH_CHECK();
+      return MINITP_OK;
+    }
+  }
   if (per_wave <= MF_ONE) {
     auto kern = gemv_mfma_kernel<PRO, EPI, 4, NT, MF_ONE, false>;
     const int lds = mf_stage_bytes<NT>();

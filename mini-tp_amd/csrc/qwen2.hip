@@ -375,6 +375,25 @@ struct Qwen2Program {
       g.part_idx = w.part_idx;
       return launch_gemv(st, c.dtype, PRO_NORM, EPI_ARGMAX, g);
     }
+    if (!s.logits_all && B > 4 && gemv_norm_supported(c.dtype, B, H)) {
+      // batched rows (bf16, 5..32): the final norm and the LM head in one
+      // MFMA GEMV whose blocks each normalize the rows once for many tuples,
+      // storing the step's logits (read from the step state), then the argmax
+      GemvArgs g{};
+      g.x = (const char*)w.x + (T - 1) * H * es();
+      g.ldx = T * H;
+      g.norm_w = final_norm;
+      g.eps = c.eps;
+      g.w = lm_head;
+      g.ldy = V;
+      g.M = B;
+      g.N = V;
+      g.K = H;
+      g.st = w.st;
+      if ((rc = launch_gemv(st, c.dtype, PRO_NORM, EPI_STORE, g))) return rc;
+      if (s.next_tok) return launch_argmax(st, c.dtype, nullptr, V, B, V, nullptr, 0, w.amax_ws, w.amax_ws_bytes, w.st, 0);
+      return MINITP_OK;
+    }
     if (s.logits_all && fz) {  // same kernel family as the module path at this M
       GemvArgs g{};
       g.x = w.x;

@@ -189,6 +189,58 @@ def test_rmsnorm_linear_matches_two_step_reference(m, k, epilogue, dtype):
     assert ((got - ref).abs() <= tol).all(), (got - ref).abs().max().item()
 
 
+@pytest.mark.parametrize("m,n,k,epilogue", [(32, 4864, 896, "swiglu"), (5, 4104, 896, "swiglu"), (17, 8272, 1024, "none"),
+                                             (32, 151936, 896, "none"), (9, 9000, 136, "none"), (32, 8200, 896, "resid")])
+@pytest.mark.parametrize("norm", [True, False])
+def test_mfma_gemv_many_tuples_equals_column_blocks(m, n, k, epilogue, norm):
+    """Products with 512 or more 16-row tuples run the tuple-loop MFMA form
+    (each block normalizes the input rows once for several tuples); the same
+    product cut into column blocks of under 512 tuples runs one tuple per
+    block. Every output is the same fixed-order sum, so the two agree
+    bitwise; the float64 check bounds both."""
+    from minitp import _native as N
+
+    g = torch.Generator().manual_seed(m + n + k)
+    eps = 1e-6
+    x = torch.randn(m, k, generator=g).to(torch.bfloat16).to(DEV)
+    nw = (1 + 0.1 * torch.randn(k, generator=g)).to(torch.bfloat16).to(DEV)
+    w = (torch.randn(2 * n if epilogue == "swiglu" else n, k, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
+    r = torch.randn(m, n, generator=g).to(torch.bfloat16).to(DEV)
+    epi = {"none": N.EPI_NONE, "swiglu": N.EPI_SWIGLU, "resid": N.EPI_RESID}[epilogue]
+
+    def run(wb, rb):
+        kw = {"out": rb.clone(), "aux": rb.clone()} if epilogue == "resid" else {}
+        if norm:
+            return _k().rmsnorm_linear(x, nw, eps, wb, None, epilogue=epi, **kw)
+        return _k().linear(x, wb, None, epilogue=epi, **kw)
+
+    whole = run(w, r)
+    step = 4096 if epilogue != "swiglu" else 2048  # under 512 tuples a block of columns
+    parts = []
+    for c0 in range(0, n, step):
+        c1 = min(n, c0 + step)
+        wb = torch.cat([w[c0:c1], w[n + c0:n + c1]]) if epilogue == "swiglu" else w[c0:c1]
+        parts.append(run(wb.contiguous(), r[:, c0:c1].contiguous()))
+    assert torch.equal(whole, torch.cat(parts, dim=1))
+    # and against float64
+    xf = x.cpu().float()
+    xn = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * nw.cpu().float()).to(torch.bfloat16) if norm \
+        else x.cpu()
+    lin = xn.double() @ w.cpu().double().T
+    scale = (xn.double().abs() @ w.cpu().double().abs().T).max().item()
+    got = whole.cpu().double()
+    if epilogue == "swiglu":
+        gate, up = lin[:, :n].to(torch.bfloat16).double(), lin[:, n:].to(torch.bfloat16).double()
+        ref = F.silu(gate.float()).to(torch.bfloat16).double() * up
+        tol = ref.abs() * 2 ** -7 + 2e-3 * scale
+    elif epilogue == "resid":
+        ref = r.cpu().double() + lin
+        tol = ref.abs() * 2 ** -7 + 2e-3 * (scale + r.abs().max().item())
+    else:
+        ref, tol = lin, lin.abs() * 2 ** -8 + 2e-3 * scale
+    assert ((got - ref).abs() <= tol).all(), (got - ref).abs().max().item()
+
+
 def test_rmsnorm_linear_refuses_prefill_shapes():
     x = torch.randn(8, 896, device=DEV)
     nw = torch.ones(896, device=DEV)
