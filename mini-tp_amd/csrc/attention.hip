@@ -4,6 +4,8 @@
 // gives (attention.py:89-90), so no K/V copy is ever made. Scale 1/sqrt(D)
 // (SDPA default). Softmax and accumulation in fp32; the output is rounded to
 // the model dtype once.
+#include <cstddef>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -52,6 +54,10 @@ struct DecodeArgs {
   float scale;
   float* ws_ml;  // [B * Hkv][nsplit][GMAX][2]  (split partials, nsplit > 1)
   float* ws_o;   // [B * Hkv][nsplit][GMAX][D]
+  // Arrival words, one per (batch row, KV head), zero between launches
+  // (the forward's step state holds them): when set, the MFMA kernel's last
+  // split block of a unit merges the splits itself (no merge launch).
+  uint32_t* count;
 };
 
 // Value held by lane j ^ (2 * MK - 1) (rows of 16 lanes, DPP). Used for a
@@ -335,14 +341,15 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(DecodeArgs a) {
 constexpr int MERGE_T = 128;
 constexpr int MERGE_NS = 8;
 
-template <typename T, int D>
-__global__ __launch_bounds__(MERGE_T) void decode_merge_kernel(DecodeArgs a, int nsplit) {
-  const AttnShape& s = a.s;
-  const int G = s.Hq / s.Hkv;
-  const int bh = blockIdx.x, b = bh / s.Hkv, g = bh % s.Hkv;
-  const int i = blockIdx.y * MERGE_T + threadIdx.x;
-  if (i >= G * D) return;
-  const int h = i / D, d = i % D;
+// Output (h, d) of unit bh from its nsplit partials. DEV: the partials were
+// stored by other blocks of the same launch (device-coherent loads).
+template <bool DEV>
+__device__ __forceinline__ float ws_load(const float* p) {
+  if constexpr (DEV) return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return *p;
+}
+template <int D, bool DEV>
+__device__ __forceinline__ float merge_splits(const DecodeArgs& a, int bh, int nsplit, int h, int d) {
   float mx = -__builtin_inff(), l = 0.f, o = 0.f;
   for (int sp0 = 0; sp0 < nsplit; sp0 += MERGE_NS) {
     float ms[MERGE_NS], ls[MERGE_NS], os[MERGE_NS];
@@ -350,9 +357,9 @@ __global__ __launch_bounds__(MERGE_T) void decode_merge_kernel(DecodeArgs a, int
     for (int u = 0; u < MERGE_NS; ++u) {
       const int sp = sp0 + u < nsplit ? sp0 + u : sp0;
       const int64_t slot = ((int64_t)bh * nsplit + sp) * GMAX + h;
-      ms[u] = sp0 + u < nsplit ? a.ws_ml[slot * 2] : -__builtin_inff();
-      ls[u] = a.ws_ml[slot * 2 + 1];
-      os[u] = a.ws_o[slot * D + d];
+      ms[u] = sp0 + u < nsplit ? ws_load<DEV>(a.ws_ml + slot * 2) : -__builtin_inff();
+      ls[u] = ws_load<DEV>(a.ws_ml + slot * 2 + 1);
+      os[u] = ws_load<DEV>(a.ws_o + slot * D + d);
     }
     float cm = mx;
 #pragma unroll
@@ -370,7 +377,18 @@ __global__ __launch_bounds__(MERGE_T) void decode_merge_kernel(DecodeArgs a, int
     }
     mx = cm;
   }
-  store_f32<T>((T*)a.out, ((int64_t)b * s.Hq + g * G + h) * D + d, o / l);
+  return o / l;
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(MERGE_T) void decode_merge_kernel(DecodeArgs a, int nsplit) {
+  const AttnShape& s = a.s;
+  const int G = s.Hq / s.Hkv;
+  const int bh = blockIdx.x, b = bh / s.Hkv, g = bh % s.Hkv;
+  const int i = blockIdx.y * MERGE_T + threadIdx.x;
+  if (i >= G * D) return;
+  const int h = i / D, d = i % D;
+  store_f32<T>((T*)a.out, ((int64_t)b * s.Hq + g * G + h) * D + d, merge_splits<D, false>(a, bh, nsplit, h, d));
 }
 
 // ---------------------------------------------------------------------------
@@ -388,8 +406,13 @@ __global__ __launch_bounds__(MERGE_T) void decode_merge_kernel(DecodeArgs a, int
 // P is rounded to bf16 for its MFMA.
 // Block = NWM waves over one split's position range, 32-position tiles
 // round robin, each tile's K and V loads issued before the previous tile's
-// math. Waves and splits merge as in decode_attn_kernel (same workspace
-// layout and merge kernel).
+// math. Waves merge in LDS; splits merge as in decode_attn_kernel (same
+// workspace layout and merge arithmetic), inside a forward by the unit's
+// last split block (arrival words in the step state), else by the merge
+// kernel. Measured at batch 32 (0.5B shape, context about 2,300): 4 splits
+// of 8 waves 13.3 us a layer with the in-kernel merge (10.5 + 4.8 us with
+// the merge kernel); 1, 2, 6 or 8 splits, 16 waves, or three tiles of
+// loads in flight per wave were all slower or no faster.
 #ifndef MINITP_DEC_MF_WAVES
 #define MINITP_DEC_MF_WAVES 8
 #endif
@@ -420,7 +443,9 @@ __global__ __launch_bounds__(NWM * 64) void decode_attn_mfma_kernel(DecodeArgs a
   const int bh = blockIdx.x, b = bh / s.Hkv, g = bh % s.Hkv;
   const int split = blockIdx.y, nsplit = gridDim.y;
   const int64_t ctx = (a.st ? a.st->args.cache_len : a.cache_len) + 1;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // the wave index made explicitly uniform: the tile loop then runs on scalar
+  // branches, and the compiler counts the loads in flight across it exactly
+  const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n16 = lane & 15, q4 = lane >> 4;
   char* vs = lds + w * Geo::WAVE_LDS;
   char* ps = vs + 32 * Geo::VS;
@@ -583,14 +608,44 @@ __global__ __launch_bounds__(NWM * 64) void decode_attn_mfma_kernel(DecodeArgs a
     if (nsplit == 1) {
       store_f32<bf16>(out, ((int64_t)b * s.Hq + g * G + h) * D + d, acc / lsum);
     } else {
-      // the merge kernel works in natural-log units
+      // the merge works in natural-log units
       const int64_t slot = ((int64_t)bh * nsplit + split) * GMAX + h;
-      a.ws_o[slot * D + d] = acc;
-      if (d == 0) {
-        a.ws_ml[slot * 2] = mx == -__builtin_inff() ? mx : mx * 0.6931471805599453f;
-        a.ws_ml[slot * 2 + 1] = lsum;
+      const float mln = mx == -__builtin_inff() ? mx : mx * 0.6931471805599453f;
+      if (a.count != nullptr) {  // device-coherent (sc1): read by the unit's last block
+        __hip_atomic_store(a.ws_o + slot * D + d, acc, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (d == 0) {
+          __hip_atomic_store(a.ws_ml + slot * 2, mln, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          __hip_atomic_store(a.ws_ml + slot * 2 + 1, lsum, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      } else {
+        a.ws_o[slot * D + d] = acc;
+        if (d == 0) {
+          a.ws_ml[slot * 2] = mln;
+          a.ws_ml[slot * 2 + 1] = lsum;
+        }
       }
     }
+  }
+  if (nsplit == 1 || a.count == nullptr) return;
+
+  // ---- in-kernel merge: the unit's last split block to arrive -------------
+  // Every wave's partial stores complete (vmcnt(0) expcnt(7) lgkmcnt(15))
+  // before the block is counted in: an agent-scope release without its
+  // whole-L2 write-back. The last block merges in split order (the same
+  // result whatever the arrival order) and puts the word back to 0.
+  __shared__ int last_blk;
+  __builtin_amdgcn_s_waitcnt(0x0F70);
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t old = __hip_atomic_fetch_add(a.count + bh, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    last_blk = old == (uint32_t)(nsplit - 1);
+    if (last_blk) __hip_atomic_store(a.count + bh, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+  __syncthreads();
+  if (!last_blk) return;
+  for (int i = tid; i < G * D; i += NWM * 64) {
+    const int h = i / D, d = i % D;
+    store_f32<bf16>(out, ((int64_t)b * s.Hq + g * G + h) * D + d, merge_splits<D, true>(a, bh, nsplit, h, d));
   }
 }
 
@@ -1275,6 +1330,10 @@ int launch_decode_attention(hipStream_t st, int dtype, const void* q, const void
   const int nsplit = (int)(mf ? decode_mfma_nsplit(units, ctx) : decode_nsplit(units, ctx, s.D));
   a.ws_ml = (float*)workspace;
   a.ws_o = a.ws_ml + units * nsplit * GMAX * 2;
+  // inside a forward: the step state's arrival words, the merge in-kernel
+  a.count = state != nullptr && units <= SPLIT_MAX_TUPLES
+                ? (uint32_t*)((char*)const_cast<StepState*>(state) + offsetof(StepState, split_count))
+                : nullptr;
   if (mf) {
     const dim3 grid((unsigned)units, (unsigned)nsplit);
     const void* kern = s.D == 64 ? (const void*)decode_attn_mfma_kernel<64> : (const void*)decode_attn_mfma_kernel<128>;
@@ -1286,7 +1345,7 @@ int launch_decode_attention(hipStream_t st, int dtype, const void* q, const void
     else
       hipLaunchKernelGGL(decode_attn_mfma_kernel<128>, grid, dim3(NWM * 64), lds, st, a);
     MINITP_LAUNCH_CHECK();
-    if (nsplit > 1) {
+    if (nsplit > 1 && a.count == nullptr) {
       const dim3 mg((unsigned)units, (unsigned)cdiv(s.Hq / s.Hkv * s.D, MERGE_T));
       if (s.D == 64)
         hipLaunchKernelGGL((decode_merge_kernel<bf16, 64>), mg, dim3(MERGE_T), 0, st, a, nsplit);
