@@ -32,12 +32,45 @@ __global__ __launch_bounds__(256) void argmax_slice_kernel(const T* logits, int6
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   float v = -__builtin_inff();
   int64_t i = INT64_MAX;
-  const int64_t end = std::min<int64_t>(V, ((int64_t)blockIdx.x + 1) * SLICE);
-  for (int64_t j = (int64_t)blockIdx.x * SLICE + tid; j < end; j += 256) {
-    const float x = load_f32<T>(lr, j);
-    if (argmax_better(x, j, v, i)) {
-      v = x;
-      i = j;
+  const int64_t start = (int64_t)blockIdx.x * SLICE, end = std::min<int64_t>(V, start + SLICE);
+  if ((((uint64_t)lr) & 15) == 0 && V * (int64_t)sizeof(T) < (1LL << 31)) {
+    // 16 consecutive elements per thread, every 16-byte load issued before
+    // the first comparison (past the row's end: zeros, dropped by index)
+    constexpr int VE = 16 / (int)sizeof(T), NV = 16 / VE;
+    const __amdgpu_buffer_rsrc_t r = span_rsrc(lr, (uint32_t)(V * (int64_t)sizeof(T)));
+    const int64_t j0 = start + 16 * tid;
+    uint4 raw[NV];
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int64_t j = j0 + u * VE;
+      const u32x4 w = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, j < end ? (uint32_t)(j * (int64_t)sizeof(T)) : 0xffffffffu, 0, 0));
+      raw[u] = make_uint4(w.x, w.y, w.z, w.w);
+    }
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const uint32_t wd[4] = {raw[u].x, raw[u].y, raw[u].z, raw[u].w};
+#pragma unroll
+      for (int e = 0; e < VE; ++e) {
+        const int64_t j = j0 + u * VE + e;
+        float x;
+        if constexpr (sizeof(T) == 2)
+          x = bf16_to_f32((uint16_t)(wd[e / 2] >> (16 * (e % 2))));
+        else
+          x = __builtin_bit_cast(float, wd[e]);
+        if (j < end && argmax_better(x, j, v, i)) {
+          v = x;
+          i = j;
+        }
+      }
+    }
+  } else {
+    for (int64_t j = start + tid; j < end; j += 256) {
+      const float x = load_f32<T>(lr, j);
+      if (argmax_better(x, j, v, i)) {
+        v = x;
+        i = j;
+      }
     }
   }
   wave_argmax(v, i);

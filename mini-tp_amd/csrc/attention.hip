@@ -16,15 +16,6 @@ namespace {
 constexpr int GMAX = 8;  // max q heads per KV head served
 constexpr int NW = 8;    // waves per decode block
 
-// Buffer resource over [base, base + bytes), wave-uniform (scalar registers);
-// loads at lane offsets past the end return zeros.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t attn_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t p = (uint64_t)base;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
-  const int n = (int)__builtin_amdgcn_readfirstlane(bytes);
-  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
-}
 __device__ __forceinline__ uint4 attn_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
   return make_uint4(v.x, v.y, v.z, v.w);
@@ -458,13 +449,13 @@ __global__ __launch_bounds__(NWM * 64) void decode_attn_mfma_kernel(DecodeArgs a
   const bf16* kc = (const bf16*)(a.st ? a.st->args.k_cache : a.k) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
   const bf16* vc = (const bf16*)(a.st ? a.st->args.v_cache : a.v) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
   const uint32_t kv_bytes = (uint32_t)(ctx * D * 2);  // rows past the context read zeros
-  const __amdgpu_buffer_rsrc_t kr = attn_rsrc(kc, kv_bytes), vr = attn_rsrc(vc, kv_bytes);
+  const __amdgpu_buffer_rsrc_t kr = span_rsrc(kc, kv_bytes), vr = span_rsrc(vc, kv_bytes);
 
   // q heads of the group as the A operand (rows G..15 zero)
   bf16x8_a qa[KS];
   {
     const bf16* qp = (const bf16*)a.q + ((int64_t)b * s.Hq + (int64_t)g * G) * D;
-    const __amdgpu_buffer_rsrc_t qr = attn_rsrc(qp, (uint32_t)(G * D * 2));
+    const __amdgpu_buffer_rsrc_t qr = span_rsrc(qp, (uint32_t)(G * D * 2));
 #pragma unroll
     for (int k = 0; k < KS; ++k)
       qa[k] = __builtin_bit_cast(bf16x8_a, attn_load16(qr, n16 < G ? (uint32_t)((n16 * D + 32 * k + 8 * q4) * 2) : OOB));
@@ -804,7 +795,7 @@ __global__ __launch_bounds__(PW * 64) void prefill_attn_mfma_kernel(const bf16* 
   const int kqv = tid % (KT / KQ), pcv = tid / (KT / KQ);
   const bool stager = tid < NPC / KQ;
   const uint32_t kv_bytes = (uint32_t)(key_end * D * 2);
-  const __amdgpu_buffer_rsrc_t krs = attn_rsrc(kbase, kv_bytes), vrs = attn_rsrc(vbase, kv_bytes);
+  const __amdgpu_buffer_rsrc_t krs = span_rsrc(kbase, kv_bytes), vrs = span_rsrc(vbase, kv_bytes);
   uint4 kr[KQ], vr[KQ];
   auto load_tile = [&](int64_t k0) {
 #pragma unroll
@@ -1029,7 +1020,7 @@ __global__ __launch_bounds__(256, 2) void prefill_attn_fa_kernel(const bf16* q, 
   static_assert(NPC / KQ == 256, "every thread stages");
   // pieces of keys past key_end lie past the buffer's size and read as zeros
   const uint32_t kv_bytes = (uint32_t)(key_end * D * 2);
-  const __amdgpu_buffer_rsrc_t krs = attn_rsrc(kbase, kv_bytes), vrs = attn_rsrc(vbase, kv_bytes);
+  const __amdgpu_buffer_rsrc_t krs = span_rsrc(kbase, kv_bytes), vrs = span_rsrc(vbase, kv_bytes);
   const uint32_t koff = (uint32_t)((kq * KQ * D + pc * 8) * 2), voff = (uint32_t)((kqv * KQ * D + pcv * 8) * 2);
   uint4 kr[KQ], vr[KQ];
   auto load_tile = [&](int64_t k0) {

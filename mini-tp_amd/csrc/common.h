@@ -214,4 +214,18 @@ void set_error(const char* fmt, ...);
 inline bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 __host__ __device__ inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// Buffer resource over [base, base + bytes): a load at a lane offset past
+// the end returns zeros without touching memory, so kernels issue their
+// loads unconditionally (a load behind a branch leaves a value to merge with
+// the branch-free default, and the compiler places that merge, and the wait
+// it implies, before the next loads it issues). Built from wave-uniform
+// values made explicitly uniform, so the resource lives in scalar registers.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t span_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  const int n = (int)__builtin_amdgcn_readfirstlane(bytes);
+  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
+}
+
 }  // namespace minitp

@@ -248,13 +248,7 @@ typedef uint32_t u32x4v __attribute__((ext_vector_type(4)));
 // The buffer resource, built from wave-uniform values made explicitly
 // uniform (otherwise the compiler may keep it in vector registers and wrap
 // every load in a loop over distinct lane values).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const Rows& q) {
-  const uint64_t a = (uint64_t)q.base;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
-  const int bytes = __builtin_amdgcn_readfirstlane(q.bytes);
-  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, bytes, 0x00020000);
-}
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_rsrc(const Rows& q) { return span_rsrc(q.base, (uint32_t)q.bytes); }
 
 // Issue loads [T0, T1) of the batch of slots [sb, sb + S) x columns
 // [jb, jb + J), load t being (slot t / J, column t % J): a batch can go out

@@ -32,14 +32,6 @@ namespace {
 constexpr int OUT_PARTIAL = 100;  // epilogue: fp32 split-K partials
 constexpr uint32_t OOB = 0xffffffffu;  // lane offset that reads zeros
 
-// Buffer resource over [base, base + bytes), wave-uniform (scalar registers).
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t gemm_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t p = (uint64_t)base;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
-  const int n = (int)__builtin_amdgcn_readfirstlane(bytes);
-  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
-}
 template <int AUX>
 __device__ __forceinline__ uint4 gemm_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
@@ -135,8 +127,8 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ x, int6
   constexpr int ES = (int)sizeof(T);
   // x rows [0, M) and W rows [0, N) as buffers; a lane's piece is read only
   // when its row exists and its K lies inside this block's split
-  const __amdgpu_buffer_rsrc_t xr = gemm_rsrc(x, (uint32_t)(((M - 1) * ldx + K) * ES));
-  const __amdgpu_buffer_rsrc_t wr = gemm_rsrc(w, (uint32_t)(N * K * ES));
+  const __amdgpu_buffer_rsrc_t xr = span_rsrc(x, (uint32_t)(((M - 1) * ldx + K) * ES));
+  const __amdgpu_buffer_rsrc_t wr = span_rsrc(w, (uint32_t)(N * K * ES));
   uint4 ra[DEPTH][LA], rb[DEPTH][LB];
   auto load = [&](int64_t k0, uint4(&a)[LA], uint4(&bb)[LB]) {
 #pragma unroll

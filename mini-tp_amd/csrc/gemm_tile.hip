@@ -54,14 +54,6 @@ constexpr int GROUP_M = 8;  // row tiles per group (4 and 16 measured no better)
 #endif
 constexpr uint32_t OOB_OFF = 0xffffffffu;
 
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t tile_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t p = (uint64_t)base;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
-  const int n = (int)__builtin_amdgcn_readfirstlane(bytes);
-  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
-}
-
 __device__ __forceinline__ uint4 tile_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
   return make_uint4(v.x, v.y, v.z, v.w);
@@ -119,9 +111,9 @@ __global__ __launch_bounds__(128 * WAVES_N) void gemm_tile_kernel(const bf16* __
     return n < N ? n : -1;
   };
 
-  const __amdgpu_buffer_rsrc_t xr = tile_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
+  const __amdgpu_buffer_rsrc_t xr = span_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
   const int64_t w_rows = EPI == TILE_SWIGLU ? 2LL * N : (int64_t)N;
-  const __amdgpu_buffer_rsrc_t wr = tile_rsrc(w, (uint32_t)(w_rows * K * 2));
+  const __amdgpu_buffer_rsrc_t wr = span_rsrc(w, (uint32_t)(w_rows * K * 2));
 
   // per-thread load slots: chunk q = tid + i * 512 -> row q / CPR, chunk q % CPR
   uint32_t a_base[LPT_A], b_base[LPT_B];

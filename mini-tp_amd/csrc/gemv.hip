@@ -51,21 +51,9 @@ constexpr bool is_qkv() {
   return EPI == EPI_QKV_ROPE || EPI == EPI_QKV_ROPE1;
 }
 
-// Buffer resource over [base, base + bytes): a load at a lane offset past
-// the end returns zeros without touching memory. The register path issues
-// all of its input and weight loads through these, unconditionally: a load
-// behind a branch leaves a value that has to be merged with the branch-free
-// default, and the compiler places that merge (and the wait for the load it
-// implies) before the next loads it issues, which would hold the weight
-// stream back by a full memory round trip. Built from wave-uniform values
-// made explicitly uniform, so the resource lives in scalar registers.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t span_rsrc(const void* base, uint32_t bytes) {
-  const uint64_t p = (uint64_t)base;
-  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
-  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
-  const int n = (int)__builtin_amdgcn_readfirstlane(bytes);
-  return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
-}
+// The register path issues every input and weight load through span_rsrc
+// resources, unconditionally.
+
 // Cache-policy bits of the weight loads: nt (read once per step) when
 // MINITP_NT_LOADS is set.
 constexpr int W_AUX = MINITP_NT_LOADS ? 2 : 0;
@@ -1251,6 +1239,10 @@ constexpr int MF_ONE = 8;
 #ifndef MINITP_MF_LOOP_PD
 #define MINITP_MF_LOOP_PD 2
 #endif
+// weights through the wave's LDS stage (1) or loaded in the operand layout (0)
+#ifndef MINITP_MF_LOOP_STAGE
+#define MINITP_MF_LOOP_STAGE 1
+#endif
 template <int PRO, int EPI>
 __global__ __launch_bounds__(256) void gemv_mfma_loop_kernel(GemvArgs a) {
   static_assert(EPI == EPI_STORE || EPI == EPI_SWIGLU, "the tuple loop serves the store and SwiGLU epilogues");
@@ -1280,17 +1272,45 @@ __global__ __launch_bounds__(256) void gemv_mfma_loop_kernel(GemvArgs a) {
     __builtin_amdgcn_wave_barrier();
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
   };
+  // staged weight loads: lane l, load u takes chunk l % 32 of tuple row
+  // l / 32 + 2 u (rows 0..7: ra + r, 8..15: rb + r - 8)
+  const uint32_t wstep = (uint32_t)((EPI == EPI_SWIGLU ? P16 : 2 * P16) * K * 2);
+  uint32_t wbase[8];
+  bool wok[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int q = lane + 64 * u, r = q >> 5, c = q & 31;
+    const int64_t row0 = r < P16 ? r : (EPI == EPI_SWIGLU ? a.N : P16) + (r - P16);
+    wbase[u] = (uint32_t)((row0 * K + kb + 8 * c) * 2);
+    wok[u] = c < nch;
+  }
   auto load_w = [&](int64_t t, uint4 (&wl)[8]) {
     int64_t ra = 0, rb = 0;
     const bool live = t < ntup;
+#if !MINITP_MF_LOOP_STAGE
     if (live) tuple16_rows<EPI>(t, a, ra, rb);
+#endif
+#if MINITP_MF_LOOP_STAGE
+    // tuple t's rows are tuple 0's moved by t x (rows a tuple) x K: the
+    // offsets are a per-lane base plus one uniform step. Rows past the
+    // product read zeros (past the buffer's end) or, for SwiGLU gate rows
+    // past N, up rows whose outputs are never stored.
+    (void)ra;
+    (void)rb;
+    (void)live;
+    const uint32_t tof = (uint32_t)t * wstep;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int q = lane + 64 * u, r = q >> 5, c = q & 31;
-      const int64_t wrow = r < P16 ? ra + r : rb + (r - P16);
-      const bool ok = live && row_valid<EPI>(wrow, a) && c < nch;
-      wl[u] = span_load16<W_AUX>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
+    for (int u = 0; u < 8; ++u) wl[u] = span_load16<W_AUX>(wr, wok[u] ? wbase[u] + tof : OOBW);
+#else
+    // straight into the operand layout: row nidx, chunk 4 i + kq
+    const int64_t wrow = nidx < P16 ? ra + nidx : rb + (nidx - P16);
+    const bool rok = live && row_valid<EPI>(wrow, a);
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int c = 4 * i + kq;
+      wl[i] = span_load16<W_AUX>(wr, rok && c < nch ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
     }
+#endif
   };
 
   // ---- input rows (and norm weight), then the first tuple's weights -------
@@ -1370,16 +1390,17 @@ __global__ __launch_bounds__(256) void gemv_mfma_loop_kernel(GemvArgs a) {
   auto tuple = [&](const int64_t t, const int it, uint4 (&wl)[8]) {
     int64_t ra = 0, rb = 0;
     tuple16_rows<EPI>(t, a, ra, rb);
+    // SwiGLU: lane nidx < 8 finishes gate row ra + nidx with its up partner
+    // (lane nidx + 8); plain store: every lane finishes its own column
     const int p = nidx & (P16 - 1);
-    const int64_t row_a = ra + p, row_b = rb + p;
-    const bool oka = nidx < P16 && row_valid<EPI>(row_a, a), okb = nidx < P16 && row_valid<EPI>(row_b, a);
-    float bias_a = 0.f, bias_b = 0.f;
-    if constexpr (EPI == EPI_STORE) {  // a zero-length resource reads zeros
+    const int64_t row_a = EPI == EPI_STORE ? (nidx < P16 ? ra + p : rb + p) : ra + p;
+    const bool oka = (EPI == EPI_STORE || nidx < P16) && row_valid<EPI>(row_a, a);
+    float bias_a = 0.f;
+    if constexpr (EPI == EPI_STORE)  // a zero-length resource reads zeros
       bias_a = bf16_to_f32((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(br, oka ? (uint32_t)(row_a * 2) : OOBW, 0, 0));
-      bias_b = bf16_to_f32((uint16_t)__builtin_amdgcn_raw_buffer_load_b16(br, okb ? (uint32_t)(row_b * 2) : OOBW, 0, 0));
-    }
     // this tuple's weights -> fragments; those MF_LOOP_PD tuples on go out
     uint4 w[NB];
+#if MINITP_MF_LOOP_STAGE
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int q = lane + 64 * u;
@@ -1389,6 +1410,10 @@ __global__ __launch_bounds__(256) void gemv_mfma_loop_kernel(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) w[i] = *(const uint4*)(st_lds + mf_slot(nidx, 4 * i + kq));
     wave_sync();
+#else
+#pragma unroll
+    for (int i = 0; i < NB; ++i) w[i] = wl[i];
+#endif
     load_w(t + MF_LOOP_PD * (int64_t)gridDim.x, wl);
     f32x4_m acc[2] = {f32x4_m{0.f, 0.f, 0.f, 0.f}, f32x4_m{0.f, 0.f, 0.f, 0.f}};
 #pragma unroll
@@ -1399,25 +1424,27 @@ __global__ __launch_bounds__(256) void gemv_mfma_loop_kernel(GemvArgs a) {
     }
     // K-split sum (two alternating buffers: one barrier per tuple): every
     // wave the same sums in wave order, wave kw finishing register kw
-    f32x4_m (*rb_buf)[2][64] = (f32x4_m(*)[2][64])(mf_stage + (it & 1) * MF_X_STAGE + MF_W_STAGE);
-    rb_buf[kw][0][lane] = acc[0];
-    rb_buf[kw][1][lane] = acc[1];
+    // (planes [register][wave][h][lane]: a wave reads only its register's
+    // plane, 2 KiB instead of 8, every read conflict-free)
+    float* rb_buf = (float*)(mf_stage + (it & 1) * MF_X_STAGE + MF_W_STAGE);
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) rb_buf[((r * 4 + kw) * 2 + h) * 64 + lane] = acc[h][r];
     __syncthreads();
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      f32x4_m v = rb_buf[0][h][lane];
-      for (int k = 1; k < 4; ++k) v += rb_buf[k][h][lane];
       // register kw of the sum (row 16 h + 4 kq + kw, column nidx), and the
       // partner column nidx ^ 8 (row_ror:8 within each 16-lane row)
-      const float va = kwu == 0 ? v[0] : kwu == 1 ? v[1] : kwu == 2 ? v[2] : v[3];
-      const float vb = dpp_f32<0x128>(0.f, va);
+      const float* pl = rb_buf + (kwu * 4 * 2 + h) * 64 + lane;
+      const float va = ((pl[0] + pl[2 * 64]) + pl[4 * 64]) + pl[6 * 64];
       const int m = h * 16 + 4 * kq + kwu;
       const bool okm = m < M;
       if constexpr (EPI == EPI_STORE) {
-        const uint16_t ya = f32_to_bf16(va + bias_a), yb = f32_to_bf16(vb + bias_b);
+        const uint16_t ya = f32_to_bf16(va + bias_a);
         __builtin_amdgcn_raw_buffer_store_b16(ya, yr, okm && oka ? (uint32_t)((m * a.ldy + row_a) * 2) : OOBW, 0, 0);
-        __builtin_amdgcn_raw_buffer_store_b16(yb, yr, okm && okb ? (uint32_t)((m * a.ldy + row_b) * 2) : OOBW, 0, 0);
       } else {
+        const float vb = dpp_f32<0x128>(0.f, va);
         const uint16_t ya = f32_to_bf16(swiglu<bf16>(round_to<bf16>(va), round_to<bf16>(vb)));
         __builtin_amdgcn_raw_buffer_store_b16(ya, yr, okm && oka ? (uint32_t)((m * a.ldy + row_a) * 2) : OOBW, 0, 0);
       }
@@ -1792,7 +1819,9 @@ int launch_mfma_nt(hipStream_t st, const GemvArgs& a, int64_t ntup) {
   const unsigned grid = (unsigned)cdiv(ntup, NT);
   const int64_t per_wave = cdiv(cdiv(a.K, 32), 4);
   if constexpr (EPI == EPI_STORE || EPI == EPI_SWIGLU) {
-    if (per_wave <= MF_ONE && NT == 1 && ntup >= MINITP_MF_LOOP_MIN) {
+    // (32-bit weight offsets: at most 1 GiB of weights)
+    const int64_t w_bytes = (EPI == EPI_SWIGLU ? 2 : 1) * a.N * a.K * 2;
+    if (per_wave <= MF_ONE && NT == 1 && ntup >= MINITP_MF_LOOP_MIN && w_bytes < (1LL << 30)) {
       // many tuples: several a block, the input rows' prologue shared
       auto kern = gemv_mfma_loop_kernel<PRO, EPI>;
       const int lds = 4 * MF_X_STAGE;

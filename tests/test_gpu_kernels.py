@@ -190,7 +190,8 @@ def test_rmsnorm_linear_matches_two_step_reference(m, k, epilogue, dtype):
 
 
 @pytest.mark.parametrize("m,n,k,epilogue", [(32, 4864, 896, "swiglu"), (5, 4104, 896, "swiglu"), (17, 8272, 1024, "none"),
-                                             (32, 151936, 896, "none"), (9, 9000, 136, "none"), (32, 8200, 896, "resid")])
+                                             (32, 151936, 896, "none"), (9, 9000, 136, "none"), (32, 8200, 896, "resid"),
+                                             (13, 8232, 896, "bias")])
 @pytest.mark.parametrize("norm", [True, False])
 def test_mfma_gemv_many_tuples_equals_column_blocks(m, n, k, epilogue, norm):
     """Products with 512 or more 16-row tuples run the tuple-loop MFMA form
@@ -206,27 +207,30 @@ def test_mfma_gemv_many_tuples_equals_column_blocks(m, n, k, epilogue, norm):
     nw = (1 + 0.1 * torch.randn(k, generator=g)).to(torch.bfloat16).to(DEV)
     w = (torch.randn(2 * n if epilogue == "swiglu" else n, k, generator=g) * 0.02).to(torch.bfloat16).to(DEV)
     r = torch.randn(m, n, generator=g).to(torch.bfloat16).to(DEV)
-    epi = {"none": N.EPI_NONE, "swiglu": N.EPI_SWIGLU, "resid": N.EPI_RESID}[epilogue]
+    b = (torch.randn(n, generator=g) * 0.02).to(torch.bfloat16).to(DEV) if epilogue == "bias" else None
+    epi = {"none": N.EPI_NONE, "bias": N.EPI_NONE, "swiglu": N.EPI_SWIGLU, "resid": N.EPI_RESID}[epilogue]
 
-    def run(wb, rb):
+    def run(wb, rb, bb):
         kw = {"out": rb.clone(), "aux": rb.clone()} if epilogue == "resid" else {}
         if norm:
-            return _k().rmsnorm_linear(x, nw, eps, wb, None, epilogue=epi, **kw)
-        return _k().linear(x, wb, None, epilogue=epi, **kw)
+            return _k().rmsnorm_linear(x, nw, eps, wb, bb, epilogue=epi, **kw)
+        return _k().linear(x, wb, bb, epilogue=epi, **kw)
 
-    whole = run(w, r)
+    whole = run(w, r, b)
     step = 4096 if epilogue != "swiglu" else 2048  # under 512 tuples a block of columns
     parts = []
     for c0 in range(0, n, step):
         c1 = min(n, c0 + step)
         wb = torch.cat([w[c0:c1], w[n + c0:n + c1]]) if epilogue == "swiglu" else w[c0:c1]
-        parts.append(run(wb.contiguous(), r[:, c0:c1].contiguous()))
+        parts.append(run(wb.contiguous(), r[:, c0:c1].contiguous(), None if b is None else b[c0:c1].contiguous()))
     assert torch.equal(whole, torch.cat(parts, dim=1))
     # and against float64
     xf = x.cpu().float()
     xn = (xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + eps) * nw.cpu().float()).to(torch.bfloat16) if norm \
         else x.cpu()
     lin = xn.double() @ w.cpu().double().T
+    if b is not None:
+        lin = lin + b.cpu().double()
     scale = (xn.double().abs() @ w.cpu().double().abs().T).max().item()
     got = whole.cpu().double()
     if epilogue == "swiglu":
@@ -443,7 +447,7 @@ def test_prefill_attention_causal_bf16_long(b, t, cache_len, hq, hkv, d):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("v", [8, 1000, 151936, 200000])
+@pytest.mark.parametrize("v", [8, 1000, 1001, 151936, 200000])  # 1001: rows off 16-byte alignment
 def test_argmax_matches_torch(dtype, v):
     g = torch.Generator().manual_seed(v)
     x = torch.randn(5, v, generator=g).to(dtype)
