@@ -285,7 +285,7 @@ int gemm_typed(hipStream_t st, const void* x, int64_t ldx, const void* w, const 
 
 int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
                 int64_t ldy, int64_t M, int64_t N, int64_t K, int epi, const void* aux, const StepState* state,
-                void* ws, int64_t ws_bytes) {
+                void* ws, int64_t ws_bytes, TileTail tail) {
   if (M == 0 || N == 0) return MINITP_OK;
   if (epi != MINITP_EPI_NONE && epi != MINITP_EPI_RESID) {
     set_error("gemm: epilogue %d not supported (split SwiGLU runs as its own kernel)", epi);
@@ -294,7 +294,7 @@ int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const voi
   // bf16 products large enough to fill the chip with 256 x 256 tiles
   if (dtype == MINITP_BF16 && epi == MINITP_EPI_NONE && state == nullptr && aligned16(x) && aligned16(w) &&
       gemm_tile_supported(M, N, K, ldx, ldy, false))
-    return launch_gemm_tile(st, x, ldx, w, bias, y, ldy, M, N, K, false);
+    return launch_gemm_tile(st, x, ldx, w, bias, y, ldy, M, N, K, false, tail);
   return dtype == MINITP_F32 ? gemm_typed<float>(st, x, ldx, w, bias, y, ldy, M, N, K, epi, aux, state, ws, ws_bytes)
                              : gemm_typed<bf16>(st, x, ldx, w, bias, y, ldy, M, N, K, epi, aux, state, ws, ws_bytes);
 }

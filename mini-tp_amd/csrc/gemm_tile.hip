@@ -38,8 +38,6 @@ typedef __bf16 bf16x8_g __attribute__((ext_vector_type(8)));
 typedef float f32x16_g __attribute__((ext_vector_type(16)));
 
 constexpr int TM = 256, TN = 256, TK = 64;
-constexpr int WTM = 128;  // wave tile rows (2 waves along M)
-constexpr int FM = WTM / 32;
 constexpr int ROWB = TK * 2;  // bytes per row per stage
 constexpr int A_BYTES = TM * ROWB, B_BYTES = TN * ROWB;
 constexpr int STAGE_BYTES = A_BYTES + B_BYTES;  // 64 KiB
@@ -51,6 +49,11 @@ constexpr int GROUP_M = 8;  // row tiles per group (4 and 16 measured no better)
 // slower at the 7B prefill shapes, one wave per SIMD hiding no latency)
 #ifndef MINITP_TILE_WAVES_N
 #define MINITP_TILE_WAVES_N 4
+#endif
+// waves along M: 2 (128-row wave tiles; the default) or 4 (64 x 64 wave
+// tiles, 16 waves, four per SIMD)
+#ifndef MINITP_TILE_WAVES_M
+#define MINITP_TILE_WAVES_M 2
 #endif
 constexpr uint32_t OOB_OFF = 0xffffffffu;
 
@@ -73,20 +76,35 @@ __device__ __forceinline__ int lds_off(int r, int c) {
 
 enum { TILE_STORE = 0, TILE_SWIGLU = 1 };
 
-template <int EPI, int WAVES_N>
-__global__ __launch_bounds__(128 * WAVES_N) void gemm_tile_kernel(const bf16* __restrict__ x, int64_t ldx,
+template <int EPI, int WAVES_M, int WAVES_N>
+__global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_tile_kernel(const bf16* __restrict__ x, int64_t ldx,
                                                              const bf16* __restrict__ w, const bf16* __restrict__ bias,
                                                              bf16* __restrict__ y, int64_t ldy, int M, int N, int K,
-                                                             int tiles_m, int tiles_n, int per_xcd) {
-  constexpr int TTHREADS = 128 * WAVES_N;
+                                                             int tiles_m, int tiles_n, int per_xcd, int full_tiles,
+                                                             int tail_split, float* __restrict__ tail_part,
+                                                             uint32_t* __restrict__ tail_cnt) {
+  constexpr int TTHREADS = 64 * WAVES_M * WAVES_N;
+  constexpr int WTM = TM / WAVES_M, FM = WTM / 32;  // wave tile rows
   constexpr int WTN = TN / WAVES_N, FN = WTN / 32;
   constexpr int LPT_A = TM * CPR / TTHREADS;  // chunks per thread per stage (x)
   constexpr int LPT_B = TN * CPR / TTHREADS;  // (W)
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int b = blockIdx.x;
-  const int local = b >> 3;
-  const int t = (b & 7) * per_xcd + local;
-  if (local >= per_xcd || t >= tiles_m * tiles_n) return;
+  // blocks [0, 8 per_xcd): tiles [0, full_tiles), one each, in
+  // XCD-contiguous ranges; past that (the split last round, where
+  // 8 per_xcd == full_tiles) tail_split blocks per remaining tile, block part
+  // p taking the p-th share of the K steps
+  const bool split_blk = b >= 8 * per_xcd;
+  int t, part = 0;
+  if (!split_blk) {
+    const int local = b >> 3;
+    t = (b & 7) * per_xcd + local;
+    if (t >= full_tiles) return;
+  } else {
+    t = full_tiles + (b - 8 * per_xcd) / tail_split;
+    part = (b - 8 * per_xcd) % tail_split;
+    if (t >= tiles_m * tiles_n) return;
+  }
   const int group = t / (GROUP_M * tiles_n);
   const int first_m = group * GROUP_M;
   const int gsz = min(tiles_m - first_m, GROUP_M);
@@ -172,13 +190,16 @@ __global__ __launch_bounds__(128 * WAVES_N) void gemm_tile_kernel(const bf16* __
   // stage writes and global loads sit between the two halves of a substep's
   // MFMAs, so the matrix pipe has work queued while they issue; one barrier
   // per step.
-  const int nk = (K + TK - 1) / TK;
+  const int nk_all = (K + TK - 1) / TK;
+  const int kper = (nk_all + tail_split - 1) / tail_split;
+  const int kb = split_blk ? part * kper : 0;
+  const int nk = split_blk ? min(nk_all, kb + kper) - kb : nk_all;  // steps of this block
 #pragma unroll
-  for (int i = 0; i < NCH; ++i) load_chunk(i, 0);
+  for (int i = 0; i < NCH; ++i) load_chunk(i, kb);
 #pragma unroll
   for (int i = 0; i < NCH; ++i) stash_chunk(i, lds);
 #pragma unroll
-  for (int i = 0; i < NCH; ++i) load_chunk(i, 1);
+  for (int i = 0; i < NCH; ++i) load_chunk(i, kb + 1);
   __syncthreads();
   constexpr int KS = TK / 16;              // MFMA k substeps per step
   constexpr int CH_PER_KS = NCH / KS;      // chunks moved per substep
@@ -211,7 +232,7 @@ __global__ __launch_bounds__(128 * WAVES_N) void gemm_tile_kernel(const bf16* __
 #pragma unroll
       for (int q = 0; q < CH_PER_KS; ++q) stash_chunk(ks * CH_PER_KS + q, nxt);
 #pragma unroll
-      for (int q = 0; q < CH_PER_KS; ++q) load_chunk(ks * CH_PER_KS + q, kt + 2);
+      for (int q = 0; q < CH_PER_KS; ++q) load_chunk(ks * CH_PER_KS + q, kb + kt + 2);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = FM / 2; i < FM; ++i)
@@ -220,6 +241,70 @@ __global__ __launch_bounds__(128 * WAVES_N) void gemm_tile_kernel(const bf16* __
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[ks & 1][i], bv[ks & 1][j], acc[i][j], 0, 0, 0);
     }
     __syncthreads();
+  }
+
+  // ---- the split last round: partials, the last block adds them ----------
+  // Each block stores its fp32 tile device-coherent ([register quad][thread]
+  // 16-byte pieces: a wave's stores are 1 KiB contiguous), waits for their
+  // completion, and counts itself in on the tile's arrival word; the block
+  // that brings the word to tail_split adds the parts in part order (the
+  // same bits whatever the arrival order), resets the word and runs the
+  // epilogue. Sums over K come out in two or more runs instead of one: a
+  // different but equally fixed order.
+  if (split_blk) {
+    __shared__ int last_blk;
+    constexpr int QUADS = FM * FN * 4;
+    const int slot = t - full_tiles;
+    const __amdgpu_buffer_rsrc_t pr =
+        span_rsrc(tail_part, (uint32_t)((int64_t)(slot + 1) * tail_split * QUADS * TTHREADS * 16));
+    auto poff = [&](int p, int qd) -> uint32_t {
+      return (uint32_t)(((((int64_t)slot * tail_split + p) * QUADS + qd) * TTHREADS + tid) * 16);
+    };
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          const u32x4 v = {__float_as_uint(acc[i][j][4 * r4]), __float_as_uint(acc[i][j][4 * r4 + 1]),
+                           __float_as_uint(acc[i][j][4 * r4 + 2]), __float_as_uint(acc[i][j][4 * r4 + 3])};
+          __builtin_amdgcn_raw_buffer_store_b128(v, pr, poff(part, (i * FN + j) * 4 + r4), 0, 16 /* sc1 */);
+        }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0): the partials are out
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t old = __hip_atomic_fetch_add(tail_cnt + slot, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      last_blk = old == (uint32_t)(tail_split - 1);
+      if (last_blk) __hip_atomic_store(tail_cnt + slot, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();
+    if (!last_blk) return;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          float v[4] = {0.f, 0.f, 0.f, 0.f};
+          for (int p = 0; p < tail_split; ++p) {
+            float x4[4];
+            if (p == part) {
+#pragma unroll
+              for (int e = 0; e < 4; ++e) x4[e] = acc[i][j][4 * r4 + e];
+            } else {
+              const u32x4 w4 = __builtin_bit_cast(
+                  u32x4, __builtin_amdgcn_raw_buffer_load_b128(pr, poff(p, (i * FN + j) * 4 + r4), 0, 16 /* sc1 */));
+              x4[0] = __uint_as_float(w4.x);
+              x4[1] = __uint_as_float(w4.y);
+              x4[2] = __uint_as_float(w4.z);
+              x4[3] = __uint_as_float(w4.w);
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = p == 0 ? x4[e] : v[e] + x4[e];
+          }
+#pragma unroll
+          for (int e = 0; e < 4; ++e) acc[i][j][4 * r4 + e] = v[e];
+        }
   }
 
   // epilogue: lane holds column (lane % 32) of rows 8 (r / 4) + 4 half + r % 4
@@ -258,19 +343,46 @@ __global__ __launch_bounds__(128 * WAVES_N) void gemm_tile_kernel(const bf16* __
   }
 }
 
+// CUs of the current device (the tile rounds' width)
+int device_cus() {
+  static int cached[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cached[dev] == 0) {
+    int cus = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus <= 0) cus = 256;
+    cached[dev] = cus;
+  }
+  return cached[dev];
+}
+
 template <int EPI>
 int launch_tile(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy,
-                int64_t M, int64_t N, int64_t K) {
-  constexpr int WN = MINITP_TILE_WAVES_N;
-  const void* kern = (const void*)gemm_tile_kernel<EPI, WN>;
+                int64_t M, int64_t N, int64_t K, TileTail tail) {
+  constexpr int WM = MINITP_TILE_WAVES_M, WN = MINITP_TILE_WAVES_N;
+  constexpr int64_t PART_BYTES = (int64_t)TM * TN * 4;  // one fp32 tile
+  const void* kern = (const void*)gemm_tile_kernel<EPI, WM, WN>;
   if (const int rc = ensure_lds_limit(kern, LDS_TILE_BYTES)) return rc;
   const int tiles_m = (int)cdiv(M, TM);
   const int tiles_n = (int)cdiv(N, EPI == TILE_SWIGLU ? TN / 2 : TN);
   const int tiles = tiles_m * tiles_n;
-  const int per_xcd = (tiles + 7) / 8;
-  hipLaunchKernelGGL((gemm_tile_kernel<EPI, WN>), dim3((unsigned)(8 * per_xcd)), dim3(128 * WN), LDS_TILE_BYTES, st,
+  // One block per CU at a time (128 KiB of LDS): tiles run in rounds of
+  // `cus`. A last round at most half full is split over K into S parts
+  // (S rem <= cus blocks), so that it takes about 1/S of a round; it needs
+  // the workspace and S <= the K steps.
+  const int cus = device_cus();
+  const int rem = tiles % cus, nk = (int)cdiv(K, TK);
+  int split = 1;
+  if (tail.part != nullptr && tail.count != nullptr && tiles >= cus && rem > 0 && 2 * rem <= cus) {
+    split = std::min(std::min(cus / rem, 4), nk);
+    if ((int64_t)rem * split * PART_BYTES > TILE_TAIL_BYTES || rem > SPLIT_MAX_TUPLES) split = 1;
+  }
+  const int full = split > 1 ? tiles - rem : tiles;
+  const int per_xcd = (full + 7) / 8;
+  const int grid = 8 * per_xcd + (split > 1 ? rem * split : 0);
+  hipLaunchKernelGGL((gemm_tile_kernel<EPI, WM, WN>), dim3((unsigned)grid), dim3(64 * WM * WN), LDS_TILE_BYTES, st,
                      (const bf16*)x, ldx, (const bf16*)w, (const bf16*)bias, (bf16*)y, ldy, (int)M, (int)N, (int)K,
-                     tiles_m, tiles_n, per_xcd);
+                     tiles_m, tiles_n, per_xcd, full, split, tail.part, tail.count);
   MINITP_LAUNCH_CHECK();
   return MINITP_OK;
 }
@@ -285,14 +397,14 @@ bool gemm_tile_supported(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t l
 }
 
 int launch_gemm_tile(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy,
-                     int64_t M, int64_t N, int64_t K, bool swiglu) {
+                     int64_t M, int64_t N, int64_t K, bool swiglu, TileTail tail) {
   if (!gemm_tile_supported(M, N, K, ldx, ldy, swiglu) || !aligned16(x) || !aligned16(w)) {
     set_error("gemm_tile: shape M=%lld N=%lld K=%lld (ldx %lld) not served", (long long)M, (long long)N, (long long)K,
               (long long)ldx);
     return MINITP_ERR_UNSUPPORTED;
   }
-  if (swiglu) return launch_tile<TILE_SWIGLU>(st, x, ldx, w, nullptr, y, ldy, M, N, K);
-  return launch_tile<TILE_STORE>(st, x, ldx, w, bias, y, ldy, M, N, K);
+  if (swiglu) return launch_tile<TILE_SWIGLU>(st, x, ldx, w, nullptr, y, ldy, M, N, K, tail);
+  return launch_tile<TILE_STORE>(st, x, ldx, w, bias, y, ldy, M, N, K, tail);
 }
 
 }  // namespace minitp

@@ -107,11 +107,21 @@ bool gemv_norm_supported(int dtype, int64_t M, int64_t K);
 // GEMM workspace of a forward: hipBLASLt's (its heuristics find solutions
 // for the 7B prefill shapes only with tens of MiB), of which the split-K
 // partials of launch_gemm use the first GEMM_SPLIT_BYTES.
-constexpr int64_t GEMM_WS_BYTES = 64LL << 20;
+// The tile GEMM's split of its last, partial round over K (TileTail) takes
+// the next TILE_TAIL_BYTES.
 constexpr int64_t GEMM_SPLIT_BYTES = 8LL << 20;
+constexpr int64_t TILE_TAIL_BYTES = 64LL << 20;
+constexpr int64_t GEMM_WS_BYTES = GEMM_SPLIT_BYTES + TILE_TAIL_BYTES;
+// fp32 partials and arrival words (zero between launches) for the tile
+// GEMM's split last round; null members: no split
+struct TileTail {
+  float* part;
+  uint32_t* count;
+};
 int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
                 int64_t ldy, int64_t M, int64_t N, int64_t K, int epi, const void* aux,
-                const StepState* state = nullptr, void* ws = nullptr, int64_t ws_bytes = 0);
+                const StepState* state = nullptr, void* ws = nullptr, int64_t ws_bytes = 0,
+                TileTail tail = TileTail{nullptr, nullptr});
 
 // gemm_tile.hip: 256 x 256 MFMA tiles (32x32x16 bf16) for prompt-sized
 // bf16 products; swiglu: W is [2N, K] = [gate; up] and y = silu(gate) * up
@@ -119,7 +129,7 @@ int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const voi
 // tiles, operands past 4 GiB, unaligned rows).
 bool gemm_tile_supported(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, bool swiglu);
 int launch_gemm_tile(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy,
-                     int64_t M, int64_t N, int64_t K, bool swiglu);
+                     int64_t M, int64_t N, int64_t K, bool swiglu, TileTail tail = TileTail{nullptr, nullptr});
 
 // elementwise.hip
 int launch_fill_normal(hipStream_t st, int dtype, void* dst, int64_t count, uint64_t seed, uint64_t sid,

@@ -220,13 +220,16 @@ struct Qwen2Program {
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     const bool use_blaslt = blas && blaslt_requested() && hipStreamIsCapturing(st, &cap) == hipSuccess &&
                             cap == hipStreamCaptureStatusNone;
+    // the tile GEMM's split last round: partials after the split-K region,
+    // arrival words in the step state (zeroed by the embedding kernel)
+    const TileTail tail{(float*)((char*)w.gemm_ws + GEMM_SPLIT_BYTES), w.split_count};
     auto lin = [&](const void* xin, int64_t ldx, const void* wt, const void* b, void* y, int64_t ldy, int64_t n,
                    int64_t k) -> int {
       int r = use_blaslt ? blaslt_linear_bf16(st, xin, ldx, wt, b, y, ldy, M, n, k, w.gemm_ws, GEMM_WS_BYTES)
                          : MINITP_ERR_UNSUPPORTED;
       if (r == MINITP_ERR_UNSUPPORTED)
         r = launch_gemm(st, c.dtype, xin, ldx, wt, b, y, ldy, M, n, k, MINITP_EPI_NONE, nullptr, nullptr, w.gemm_ws,
-                        GEMM_SPLIT_BYTES);
+                        GEMM_SPLIT_BYTES, tail);
       return r;
     };
     if (blas && (rc = launch_rmsnorm(st, c.dtype, w.x, L(0, MINITP_W_LN1), w.h, M, H, c.eps))) return rc;
@@ -249,7 +252,8 @@ struct Qwen2Program {
         if ((rc = lin(w.attn, q_rows(), L(l, MINITP_W_O), nullptr, w.h, H, H, q_rows()))) return rc;
         if ((rc = launch_add_rmsnorm(st, c.dtype, w.x, w.h, L(l, MINITP_W_LN2), w.h, M, H, c.eps))) return rc;
         if (!use_blaslt && gemm_tile_supported(M, I, H, H, I, true)) {
-          if ((rc = launch_gemm_tile(st, w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.act, I, M, I, H, true))) return rc;
+          if ((rc = launch_gemm_tile(st, w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.act, I, M, I, H, true, tail)))
+            return rc;
         } else {
           if ((rc = lin(w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.gu, 2 * I, 2 * I, H))) return rc;
           const char* up = (const char*)w.gu + I * es();
@@ -417,7 +421,7 @@ struct Qwen2Program {
       rc = use_blaslt ? blaslt_linear_bf16(st, w.h, H, lm_head, nullptr, s.logits, V, M, V, H, w.gemm_ws, GEMM_WS_BYTES)
                       : MINITP_ERR_UNSUPPORTED;
       if (rc == MINITP_ERR_UNSUPPORTED && blas && gemm_tile_supported(M, V, H, H, V, false))
-        rc = launch_gemm_tile(st, w.h, H, lm_head, nullptr, s.logits, V, M, V, H, false);
+        rc = launch_gemm_tile(st, w.h, H, lm_head, nullptr, s.logits, V, M, V, H, false, tail);
       if (rc == MINITP_ERR_UNSUPPORTED)
         rc = launch_gemm(st, c.dtype, w.h, H, lm_head, nullptr, nullptr, V, M, V, H, MINITP_EPI_NONE, nullptr, w.st);
       if (rc) return rc;
