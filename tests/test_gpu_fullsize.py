@@ -11,6 +11,9 @@ exercise exactly the full-size path:
 * the whole-prompt prefill's last-position logits equal those of a prefill of
   the first 4,095 tokens followed by one decode step of the last token (the
   decode attention and GEMV path over the 4,095 cached rows);
+* layer 0's K and V cache rows against float64 (embedding, the oracle's
+  RMSNorm and RoPE, the QKV product in float64), on rows computed by split
+  and by unsplit GEMM tiles;
 * a prefill in two chunks of 2,048 (the second attending over the first
   through the cache offset, positions 2,048 .. 4,095 given explicitly) gives
   the same last-position logits and the same cache rows as the whole prompt;
@@ -74,6 +77,40 @@ def test_full_prompt_last_row_equals_prefill_then_decode(model_prompt):
     err = (whole - step).abs().max().item()
     print(f"4 x 4096: whole-prompt vs prefill(4095) + decode: max |logit diff| {err:.4f}")
     assert err <= BF16_LOGIT_ATOL
+
+
+@pytest.mark.parametrize("b,p0", [(3, 3968), (0, 0)])
+def test_layer0_cache_rows_match_float64(model_prompt, b, p0):
+    """Layer 0's K and V cache rows of 128 positions after the whole-prompt
+    prefill, against embedding -> RMSNorm (the oracle's, bf16) -> the QKV
+    product in float64 + bias, rounded to bf16 -> RoPE (the oracle's cached
+    tables) for K. At M = 16,384 the QKV GEMM has 1,152 tiles: 4 full rounds
+    of 256 and 128 tiles split over K in two parts. Batch row 3's last
+    positions sit in split tiles, row 0's first in unsplit ones. Bar: a few
+    bf16 steps (the GEMM's fp32 sums round to bf16 differently from float64's
+    in the last bit, and RoPE multiplies that)."""
+    from oracle.qwen2_ref import rms_norm, rope_apply, rope_tables
+
+    model, prompt = model_prompt
+    _, kv = _whole(model, prompt)
+    sd = model.state_dict()
+    hq, hkv, hd = 28, 4, 128
+    emb = sd["model.embed_tokens.weight"]
+    x = emb[prompt[b, p0:p0 + 128]]
+    xn = rms_norm(x, sd["model.layers.0.input_layernorm.weight"], 1e-6)
+    y = torch.nn.functional.linear(xn.double(), sd["model.layers.0.self_attn.qkv_proj.weight"].double(),
+                                   sd["model.layers.0.self_attn.qkv_proj.bias"].double()).to(torch.bfloat16)
+    k = y[:, hq * hd:(hq + hkv) * hd].view(128, hkv, hd).transpose(0, 1)[None]
+    v = y[:, (hq + hkv) * hd:].view(128, hkv, hd).transpose(0, 1)[None]
+    cos, sin = rope_tables(hd, 1e6, 4096)
+    _, k = rope_apply(cos.to(DEV), sin.to(DEV), k, k, torch.arange(p0, p0 + 128, device=DEV))
+    for name, got, ref in (("k", kv.k[0], k), ("v", kv.v[0], v)):
+        g = got[b:b + 1, :, p0:p0 + 128].float()
+        r = ref.float()
+        d = (g - r).abs()
+        print(f"row {b}, positions {p0}..{p0 + 127}, {name}: max |ref| {r.abs().max().item():.3f}, "
+              f"max |diff| {d.max().item():.4f}")
+        assert torch.isfinite(g).all() and (d <= 3e-2 + r.abs() / 32).all()
 
 
 def test_two_chunk_prefill_equals_whole_prompt(model_prompt):
