@@ -66,19 +66,21 @@ constexpr int chunk_bytes() {
 }
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
-typedef short s16x4 __attribute__((ext_vector_type(4)));
 
 template <typename T>
 struct Mfma;
 
+typedef __bf16 bf16x8_k __attribute__((ext_vector_type(8)));
+// gfx950's 32x32x16: lane l holds A[l % 32][8 (l / 32) .. + 7] and the same
+// k range of B column l % 32, one 16-byte LDS read each
 template <>
 struct Mfma<bf16> {
-  static constexpr int KSTEP = 8;  // k per instruction
+  static constexpr int KSTEP = 16;  // k per instruction
   __device__ static f32x16 step(const char* a_row, const char* b_row, int ks, int lane, f32x16 c) {
-    const int off = (ks * KSTEP + (lane >> 5) * 4) * 2;
-    s16x4 a = *reinterpret_cast<const s16x4*>(a_row + off);
-    s16x4 b = *reinterpret_cast<const s16x4*>(b_row + off);
-    return __builtin_amdgcn_mfma_f32_32x32x8bf16_1k(a, b, c, 0, 0, 0);
+    const int off = (ks * KSTEP + (lane >> 5) * 8) * 2;
+    const bf16x8_k a = *reinterpret_cast<const bf16x8_k*>(a_row + off);
+    const bf16x8_k b = *reinterpret_cast<const bf16x8_k*>(b_row + off);
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
   }
 };
 
