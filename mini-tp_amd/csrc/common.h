@@ -228,4 +228,47 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t span_rsrc(const void* base, ui
   return __builtin_amdgcn_make_buffer_rsrc((void*)(((uint64_t)hi << 32) | lo), (short)0, n, 0x00020000);
 }
 
+// Split-K partial products, fp32 [S][M][N] in the forward's GEMM workspace
+// (launch_gemm_partials), handed to the kernel that consumes the product.
+struct Partials {
+  const float* p;
+  int S;
+  int64_t M, N;
+};
+
+// Sum over the splits of elements (row, col .. col + 7), added in split
+// order (the order gemm_reduce_kernel uses), the loads of four splits in
+// flight at a time. col and N multiples of 4.
+__device__ __forceinline__ void sum_partials8(const Partials& q, int64_t row, int64_t col, float* v) {
+  const int64_t mn = q.M * q.N, off = row * q.N + col;
+  auto ld = [&](int s, float* o) {
+    const float4 a = *(const float4*)(q.p + s * mn + off), b = *(const float4*)(q.p + s * mn + off + 4);
+    o[0] = a.x;
+    o[1] = a.y;
+    o[2] = a.z;
+    o[3] = a.w;
+    o[4] = b.x;
+    o[5] = b.y;
+    o[6] = b.z;
+    o[7] = b.w;
+  };
+  ld(0, v);
+  int s = 1;
+  for (; s + 4 <= q.S; s += 4) {
+    float t[4][8];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) ld(s + u, t[u]);
+#pragma unroll
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] += t[u][e];
+  }
+  for (; s < q.S; ++s) {
+    float t[8];
+    ld(s, t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] += t[e];
+  }
+}
+
 }  // namespace minitp

@@ -204,8 +204,12 @@ __global__ __launch_bounds__(256) void add_rmsnorm_kernel(T* x, const T* delta, 
 
 // bf16 rows of hidden % 8 == 0: the same math in 16-byte pieces (8 elements per
 // load and store; a thread's elements are whole pieces).
-__global__ __launch_bounds__(256) void add_rmsnorm8_kernel(bf16* x, const bf16* delta, const bf16* __restrict__ w,
-                                                           bf16* out, int64_t hidden, float eps) {
+// PART: delta is the split-K partial product itself (the sum over the splits
+// rounded to bf16 as gemm_reduce_kernel stores it), not a bf16 row.
+template <bool PART>
+__global__ __launch_bounds__(256) void add_rmsnorm8_kernel(bf16* x, const bf16* delta, Partials dp,
+                                                           const bf16* __restrict__ w, bf16* out, int64_t hidden,
+                                                           float eps) {
   __shared__ float red[4];
   uint4* xr = reinterpret_cast<uint4*>(x + blockIdx.x * hidden);
   const uint4* dr = reinterpret_cast<const uint4*>(delta + blockIdx.x * hidden);
@@ -216,7 +220,14 @@ __global__ __launch_bounds__(256) void add_rmsnorm8_kernel(bf16* x, const bf16* 
   for (int64_t c = threadIdx.x; c < n8; c += 256) {
     float a[8], d[8];
     unpack16(xr[c], a, (bf16*)nullptr);
-    unpack16(dr[c], d, (bf16*)nullptr);
+    if constexpr (PART) {
+      float v[8];
+      sum_partials8(dp, blockIdx.x, c * 8, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) d[e] = round_to<bf16>(v[e] + 0.f);
+    } else {
+      unpack16(dr[c], d, (bf16*)nullptr);
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       a[e] = round_to<bf16>(add_rn(a[e], d[e]));
@@ -245,8 +256,8 @@ int launch_add_rmsnorm(hipStream_t st, int dtype, void* x, const void* delta, co
                        int64_t hidden, float eps) {
   if (rows == 0) return MINITP_OK;
   if (dtype == MINITP_BF16 && hidden % 8 == 0 && aligned16(x) && aligned16(delta) && aligned16(w) && aligned16(out)) {
-    add_rmsnorm8_kernel<<<(unsigned)rows, 256, 0, st>>>((bf16*)x, (const bf16*)delta, (const bf16*)w, (bf16*)out,
-                                                        hidden, eps);
+    add_rmsnorm8_kernel<false><<<(unsigned)rows, 256, 0, st>>>((bf16*)x, (const bf16*)delta, Partials{}, (const bf16*)w,
+                                                               (bf16*)out, hidden, eps);
     MINITP_LAUNCH_CHECK();
     return MINITP_OK;
   }
@@ -295,17 +306,31 @@ __global__ void silu_mul_kernel(const T* gate, const T* up, int64_t ld_in, T* ou
 
 // bf16, 8 elements per thread through 16-byte loads and stores (rows of n % 8
 // == 0 elements, 16-byte aligned row starts); same math as silu_mul_kernel.
-__global__ void silu_mul8_kernel(const bf16* gate, const bf16* up, int64_t ld_in, bf16* out, int64_t ld_out,
-                                 int64_t rows, int64_t n) {
+// PART: gate and up are the split-K partial product of the [gate; up]
+// weight ([S][rows][2 n]), each sum rounded to bf16 as the GEMM stores it.
+template <bool PART>
+__global__ void silu_mul8_kernel(const bf16* gate, const bf16* up, int64_t ld_in, Partials gp, bf16* out,
+                                 int64_t ld_out, int64_t rows, int64_t n) {
   const int64_t n8 = n / 8, total = rows * n8;
   const int64_t stride = (int64_t)gridDim.x * blockDim.x;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < total; i += stride) {
     const int64_t r = i / n8, c = (i % n8) * 8;
-    const uint4 gv = *reinterpret_cast<const uint4*>(gate + r * ld_in + c);
-    const uint4 uv = *reinterpret_cast<const uint4*>(up + r * ld_in + c);
     float g[8], u[8], o[8];
-    unpack16(gv, g, (bf16*)nullptr);
-    unpack16(uv, u, (bf16*)nullptr);
+    if constexpr (PART) {
+      float vg[8], vu[8];
+      sum_partials8(gp, r, c, vg);
+      sum_partials8(gp, r, n + c, vu);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        g[e] = round_to<bf16>(vg[e] + 0.f);
+        u[e] = round_to<bf16>(vu[e] + 0.f);
+      }
+    } else {
+      const uint4 gv = *reinterpret_cast<const uint4*>(gate + r * ld_in + c);
+      const uint4 uv = *reinterpret_cast<const uint4*>(up + r * ld_in + c);
+      unpack16(gv, g, (bf16*)nullptr);
+      unpack16(uv, u, (bf16*)nullptr);
+    }
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = swiglu<bf16>(g[e], u[e]);
     *reinterpret_cast<uint4*>(out + r * ld_out + c) =
@@ -320,7 +345,8 @@ int launch_silu_mul(hipStream_t st, int dtype, const void* gate, const void* up,
                    aligned16(up) && aligned16(out);
   if (vec) {
     const int grid8 = (int)std::min<int64_t>(cdiv(rows * (n / 8), 256), 65536);
-    silu_mul8_kernel<<<grid8, 256, 0, st>>>((const bf16*)gate, (const bf16*)up, ld_in, (bf16*)out, ld_out, rows, n);
+    silu_mul8_kernel<false><<<grid8, 256, 0, st>>>((const bf16*)gate, (const bf16*)up, ld_in, Partials{}, (bf16*)out,
+                                                   ld_out, rows, n);
     MINITP_LAUNCH_CHECK();
     return MINITP_OK;
   }
@@ -331,6 +357,32 @@ int launch_silu_mul(hipStream_t st, int dtype, const void* gate, const void* up,
   else
     silu_mul_kernel<bf16><<<grid, 256, 0, st>>>((const bf16*)gate, (const bf16*)up, ld_in, (bf16*)out, ld_out, rows,
                                                 n);
+  MINITP_LAUNCH_CHECK();
+  return MINITP_OK;
+}
+
+int launch_add_rmsnorm_partials(hipStream_t st, void* x, const Partials& delta, const void* w, void* out,
+                                int64_t hidden, float eps) {
+  if (delta.M == 0) return MINITP_OK;
+  if (delta.N != hidden || hidden % 8 != 0 || delta.S < 1 || !aligned16(x) || !aligned16(delta.p) || !aligned16(w) ||
+      !aligned16(out)) {
+    set_error("add_rmsnorm from partials: hidden %lld, partial width %lld", (long long)hidden, (long long)delta.N);
+    return MINITP_ERR_UNSUPPORTED;
+  }
+  add_rmsnorm8_kernel<true><<<(unsigned)delta.M, 256, 0, st>>>((bf16*)x, nullptr, delta, (const bf16*)w, (bf16*)out,
+                                                              hidden, eps);
+  MINITP_LAUNCH_CHECK();
+  return MINITP_OK;
+}
+
+int launch_silu_mul_partials(hipStream_t st, const Partials& gu, void* out, int64_t ld_out, int64_t n) {
+  if (gu.M * n == 0) return MINITP_OK;
+  if (gu.N != 2 * n || n % 8 != 0 || ld_out % 8 != 0 || gu.S < 1 || !aligned16(gu.p) || !aligned16(out)) {
+    set_error("silu_mul from partials: n %lld, partial width %lld", (long long)n, (long long)gu.N);
+    return MINITP_ERR_UNSUPPORTED;
+  }
+  const int grid8 = (int)std::min<int64_t>(cdiv(gu.M * (n / 8), 256), 65536);
+  silu_mul8_kernel<true><<<grid8, 256, 0, st>>>(nullptr, nullptr, 0, gu, (bf16*)out, ld_out, gu.M, n);
   MINITP_LAUNCH_CHECK();
   return MINITP_OK;
 }

@@ -228,25 +228,37 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restric
   }
 }
 
+// Splits of K (and K elements per split) for an M x N x K product on BM x BN
+// tiles: enough blocks to fill the CUs twice, each at least one chunk deep,
+// and partials that fit the workspace.
 template <typename T, int BM, int BN>
-int gemm_launch(hipStream_t st, const T* x, int64_t ldx, const T* w, const T* bias, T* y, int64_t ldy, int64_t M,
-                int64_t N, int64_t K, int epi, const T* aux, const StepState* state, float* ws, int64_t ws_bytes) {
+int64_t split_plan(int64_t M, int64_t N, int64_t K, const float* ws, int64_t ws_bytes, int64_t* kper_out) {
   constexpr int64_t KCE = chunk_bytes<BM>() / sizeof(T);
-  if (N * K * (int64_t)sizeof(T) > 0xffffffffLL || ((M - 1) * ldx + K) * (int64_t)sizeof(T) > 0xffffffffLL) {
-    set_error("gemm: operands over 4 GiB (M=%lld N=%lld K=%lld)", (long long)M, (long long)N, (long long)K);
-    return MINITP_ERR_UNSUPPORTED;
-  }
   const int64_t tiles = cdiv(N, BN) * cdiv(M, BM);
   const int64_t nchunk = cdiv(K, KCE);
-  // splits: enough blocks to fill the CUs twice, each at least one chunk deep,
-  // and partials that fit the workspace
   int64_t S = 1;
   if (ws != nullptr) {
     S = std::min<int64_t>(cdiv(512, tiles), nchunk);
     while (S > 1 && S * M * N * (int64_t)sizeof(float) > ws_bytes) --S;
   }
   const int64_t kper = cdiv(nchunk, S) * KCE;
-  S = cdiv(K, kper);
+  *kper_out = kper;
+  return cdiv(K, kper);
+}
+
+inline bool gemm_operands_fit(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t es) {
+  return N * K * es <= 0xffffffffLL && ((M - 1) * ldx + K) * es <= 0xffffffffLL;
+}
+
+template <typename T, int BM, int BN>
+int gemm_launch(hipStream_t st, const T* x, int64_t ldx, const T* w, const T* bias, T* y, int64_t ldy, int64_t M,
+                int64_t N, int64_t K, int epi, const T* aux, const StepState* state, float* ws, int64_t ws_bytes) {
+  if (!gemm_operands_fit(M, N, K, ldx, sizeof(T))) {
+    set_error("gemm: operands over 4 GiB (M=%lld N=%lld K=%lld)", (long long)M, (long long)N, (long long)K);
+    return MINITP_ERR_UNSUPPORTED;
+  }
+  int64_t kper = 0;
+  const int64_t S = split_plan<T, BM, BN>(M, N, K, ws, ws_bytes, &kper);
   const dim3 grid((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM), (unsigned)S);
   if (S > 1) {
     hipLaunchKernelGGL((gemm_kernel<T, BM, BN, OUT_PARTIAL>), grid, dim3(256), 0, st, x, ldx, w, bias, y, ldy, aux,
@@ -284,6 +296,35 @@ int gemm_typed(hipStream_t st, const void* x, int64_t ldx, const void* w, const 
 }
 
 }  // namespace
+
+int launch_gemm_partials(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, int64_t M, int64_t N,
+                         int64_t K, void* ws, int64_t ws_bytes, Partials* out) {
+  // the product launch_gemm would split (bf16, not on the tile kernel)
+  if (dtype != MINITP_BF16 || M <= 0 || N % 8 != 0 || ws == nullptr || !aligned16(ws) || !aligned16(x) ||
+      !aligned16(w) || gemm_tile_supported(M, N, K, ldx, N, false) || !gemm_operands_fit(M, N, K, ldx, 2))
+    return MINITP_ERR_UNSUPPORTED;
+  int64_t kper = 0, S;
+  dim3 grid;
+  const bf16 *xb = (const bf16*)x, *wb = (const bf16*)w;
+  float* part = (float*)ws;
+  if (M >= 512) {
+    S = split_plan<bf16, 128, 128>(M, N, K, part, ws_bytes, &kper);
+    if (S < 2) return MINITP_ERR_UNSUPPORTED;
+    grid = dim3((unsigned)cdiv(N, 128), (unsigned)cdiv(M, 128), (unsigned)S);
+    hipLaunchKernelGGL((gemm_kernel<bf16, 128, 128, OUT_PARTIAL>), grid, dim3(256), 0, st, xb, ldx, wb, nullptr,
+                       nullptr, N, nullptr, part, M, N, K, kper, nullptr);
+  } else {
+    constexpr int BM = MINITP_GEMM_SMALL_BM, BN = MINITP_GEMM_SMALL_BN;
+    S = split_plan<bf16, BM, BN>(M, N, K, part, ws_bytes, &kper);
+    if (S < 2) return MINITP_ERR_UNSUPPORTED;
+    grid = dim3((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM), (unsigned)S);
+    hipLaunchKernelGGL((gemm_kernel<bf16, BM, BN, OUT_PARTIAL>), grid, dim3(256), 0, st, xb, ldx, wb, nullptr, nullptr,
+                       N, nullptr, part, M, N, K, kper, nullptr);
+  }
+  MINITP_LAUNCH_CHECK();
+  *out = Partials{part, (int)S, M, N};
+  return MINITP_OK;
+}
 
 int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
                 int64_t ldy, int64_t M, int64_t N, int64_t K, int epi, const void* aux, const StepState* state,

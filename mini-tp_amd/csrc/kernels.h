@@ -122,6 +122,13 @@ int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const voi
                 int64_t ldy, int64_t M, int64_t N, int64_t K, int epi, const void* aux,
                 const StepState* state = nullptr, void* ws = nullptr, int64_t ws_bytes = 0,
                 TileTail tail = TileTail{nullptr, nullptr});
+// The first half of a bf16 product that launch_gemm would split over K: the
+// split GEMM alone, its fp32 partials [S][M][N] in ws (described in *out),
+// for a consumer kernel to add up in split order with its own epilogue
+// (the *_partials launchers). MINITP_ERR_UNSUPPORTED when the product is
+// not split (tile kernel, one split, fp32): the caller runs launch_gemm.
+int launch_gemm_partials(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, int64_t M, int64_t N,
+                         int64_t K, void* ws, int64_t ws_bytes, Partials* out);
 
 // gemm_tile.hip: 256 x 256 MFMA tiles (32x32x16 bf16) for prompt-sized
 // bf16 products; swiglu: W is [2N, K] = [gate; up] and y = silu(gate) * up
@@ -146,6 +153,12 @@ int launch_silu_mul(hipStream_t st, int dtype, const void* gate, const void* up,
 int launch_cast_f32_bf16(hipStream_t st, const float* in, void* out, int64_t n);
 int launch_add_rmsnorm(hipStream_t st, int dtype, void* x, const void* delta, const void* w, void* out, int64_t rows,
                        int64_t hidden, float eps);
+// bf16 launch_add_rmsnorm / launch_silu_mul whose delta / [gate, up] input is
+// a split product's partials (the sums rounded to bf16 as launch_gemm
+// stores them, so the results are the same bits)
+int launch_add_rmsnorm_partials(hipStream_t st, void* x, const Partials& delta, const void* w, void* out,
+                                int64_t hidden, float eps);
+int launch_silu_mul_partials(hipStream_t st, const Partials& gu, void* out, int64_t ld_out, int64_t n);
 // MINITP_GEMM=blaslt in the environment: prompt GEMMs on hipBLASLt (a
 // benchmark comparison; the product path runs the library's own kernels)
 bool blaslt_requested();
@@ -165,6 +178,11 @@ int launch_rope_kv_write(hipStream_t st, int dtype, const void* qkv, int64_t ld_
                          int64_t max_pos, int64_t B, int64_t T, int64_t Hq, int64_t Hkv, int64_t D, int64_t S,
                          int64_t cache_len, int32_t* error_flag, const StepState* state = nullptr,
                          int layer = 0);
+// bf16 launch_rope_kv_write of a QKV projection given as its split partials
+// plus the bias (positions, cache length and caches from the step state)
+int launch_rope_kv_write_partials(hipStream_t st, const Partials& qkv, const void* bias, void* q_out,
+                                  const float* cos_tab, const float* sin_tab, int64_t max_pos, int64_t B, int64_t T,
+                                  int64_t Hq, int64_t Hkv, int64_t D, int64_t S, const StepState* state, int layer);
 
 // attention.hip. Decode (T == 1) may read cache_len and the cache bases
 // from a StepState (graph replay); prefill takes them by value.

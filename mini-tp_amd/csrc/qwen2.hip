@@ -233,6 +233,17 @@ struct Qwen2Program {
       return r;
     };
     if (blas && (rc = launch_rmsnorm(st, c.dtype, w.x, L(0, MINITP_W_LN1), w.h, M, H, c.eps))) return rc;
+    // Prompt products that the split-K GEMM serves hand their partials to
+    // the kernel after them (RoPE + KV write, residual add + RMSNorm,
+    // SwiGLU), which adds them up in split order: no reduction launch, and
+    // the same bits as reduce-then-consume. The partials may take the whole
+    // GEMM workspace (nothing else in it is live between the two launches).
+    const bool fuse_split = blas && !use_blaslt && D % 16 == 0 && H % 8 == 0 && I % 8 == 0 &&
+                            aligned16(cos_tab) && aligned16(sin_tab);
+    auto partials = [&](const void* xin, int64_t ldx, const void* wt, int64_t n, int64_t k, Partials* p) -> int {
+      if (!fuse_split) return MINITP_ERR_UNSUPPORTED;
+      return launch_gemm_partials(st, c.dtype, xin, ldx, wt, M, n, k, w.gemm_ws, GEMM_WS_BYTES, p);
+    };
     auto split_bufs = [&](GemvArgs& g) {
       g.split_part = w.split_part;
       g.split_part_bytes = w.split_part_bytes;
@@ -241,27 +252,54 @@ struct Qwen2Program {
     for (int l = 0; l < c.num_layers; ++l) {
       if (blas) {
         // h holds input_layernorm(x) of this layer
-        if ((rc = lin(w.h, H, L(l, MINITP_W_QKV), L(l, MINITP_W_QKV_BIAS), w.qkv, qkv_rows(), qkv_rows(), H)))
-          return rc;
-        if ((rc = launch_rope_kv_write(st, c.dtype, w.qkv, qkv_rows(), w.q, nullptr, nullptr, cos_tab, sin_tab, nullptr,
-                                       c.max_pos, B, T, c.heads, c.kv_heads, D, s.max_seq, 0, nullptr, w.st, l)))
-          return rc;
+        Partials pp{};
+        rc = partials(w.h, H, L(l, MINITP_W_QKV), qkv_rows(), H, &pp);
+        if (rc == MINITP_OK) {
+          rc = launch_rope_kv_write_partials(st, pp, L(l, MINITP_W_QKV_BIAS), w.q, cos_tab, sin_tab, c.max_pos, B, T,
+                                             c.heads, c.kv_heads, D, s.max_seq, w.st, l);
+        } else if (rc == MINITP_ERR_UNSUPPORTED) {
+          rc = lin(w.h, H, L(l, MINITP_W_QKV), L(l, MINITP_W_QKV_BIAS), w.qkv, qkv_rows(), qkv_rows(), H);
+          if (!rc)
+            rc = launch_rope_kv_write(st, c.dtype, w.qkv, qkv_rows(), w.q, nullptr, nullptr, cos_tab, sin_tab, nullptr,
+                                      c.max_pos, B, T, c.heads, c.kv_heads, D, s.max_seq, 0, nullptr, w.st, l);
+        }
+        if (rc) return rc;
         const char* kc = (const char*)s.k_cache + l * layer_elems * es();
         const char* vc = (const char*)s.v_cache + l * layer_elems * es();
         if ((rc = launch_prefill_attention(st, c.dtype, w.q, kc, vc, w.attn, as, s.cache_len))) return rc;
-        if ((rc = lin(w.attn, q_rows(), L(l, MINITP_W_O), nullptr, w.h, H, H, q_rows()))) return rc;
-        if ((rc = launch_add_rmsnorm(st, c.dtype, w.x, w.h, L(l, MINITP_W_LN2), w.h, M, H, c.eps))) return rc;
+        // x += o_proj(attn), h = post_attention_layernorm(x)
+        rc = partials(w.attn, q_rows(), L(l, MINITP_W_O), H, q_rows(), &pp);
+        if (rc == MINITP_OK) {
+          rc = launch_add_rmsnorm_partials(st, w.x, pp, L(l, MINITP_W_LN2), w.h, H, c.eps);
+        } else if (rc == MINITP_ERR_UNSUPPORTED) {
+          rc = lin(w.attn, q_rows(), L(l, MINITP_W_O), nullptr, w.h, H, H, q_rows());
+          if (!rc) rc = launch_add_rmsnorm(st, c.dtype, w.x, w.h, L(l, MINITP_W_LN2), w.h, M, H, c.eps);
+        }
+        if (rc) return rc;
         if (!use_blaslt && gemm_tile_supported(M, I, H, H, I, true)) {
           if ((rc = launch_gemm_tile(st, w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.act, I, M, I, H, true, tail)))
             return rc;
         } else {
-          if ((rc = lin(w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.gu, 2 * I, 2 * I, H))) return rc;
-          const char* up = (const char*)w.gu + I * es();
-          if ((rc = launch_silu_mul(st, c.dtype, w.gu, up, 2 * I, w.act, I, M, I))) return rc;
+          rc = partials(w.h, H, L(l, MINITP_W_GATE_UP), 2 * I, H, &pp);
+          if (rc == MINITP_OK) {
+            rc = launch_silu_mul_partials(st, pp, w.act, I, I);
+          } else if (rc == MINITP_ERR_UNSUPPORTED) {
+            rc = lin(w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.gu, 2 * I, 2 * I, H);
+            const char* up = (const char*)w.gu + I * es();
+            if (!rc) rc = launch_silu_mul(st, c.dtype, w.gu, up, 2 * I, w.act, I, M, I);
+          }
+          if (rc) return rc;
         }
-        if ((rc = lin(w.act, I, L(l, MINITP_W_DOWN), nullptr, w.h, H, H, I))) return rc;
+        // x += down(act), h = the next layer's input_layernorm(x) (the final norm after the last)
         const void* next_norm = l + 1 < c.num_layers ? L(l + 1, MINITP_W_LN1) : final_norm;
-        if ((rc = launch_add_rmsnorm(st, c.dtype, w.x, w.h, next_norm, w.h, M, H, c.eps))) return rc;
+        rc = partials(w.act, I, L(l, MINITP_W_DOWN), H, I, &pp);
+        if (rc == MINITP_OK) {
+          rc = launch_add_rmsnorm_partials(st, w.x, pp, next_norm, w.h, H, c.eps);
+        } else if (rc == MINITP_ERR_UNSUPPORTED) {
+          rc = lin(w.act, I, L(l, MINITP_W_DOWN), nullptr, w.h, H, H, I);
+          if (!rc) rc = launch_add_rmsnorm(st, c.dtype, w.x, w.h, next_norm, w.h, M, H, c.eps);
+        }
+        if (rc) return rc;
         continue;
       }
       // ---- attention block --------------------------------------------------

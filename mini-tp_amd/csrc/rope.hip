@@ -142,11 +142,14 @@ __device__ __forceinline__ void store8_bf16(bf16* dst, const float* v) {
 // The same as rope_kv_write_kernel<bf16> for D / 2 % 8 == 0, eight pairs per
 // thread: 16-byte loads of the qkv row (the caller checks its alignment) and
 // of the fp32 tables, 16-byte stores wherever the destination allows them.
-__global__ void rope_kv_write8_kernel(const bf16* qkv, int64_t ld, bf16* q_out, bf16* k_cache, bf16* v_cache,
-                                      const float* cos_tab, const float* sin_tab, const int64_t* positions,
-                                      int64_t max_pos, int64_t B, int64_t T_, int64_t Hq, int64_t Hkv, int64_t D,
-                                      int64_t S, int64_t cache_len, int32_t* error_flag, const StepState* state,
-                                      int layer) {
+// PART: the projection is the split-K partial product (qp) plus the bias,
+// rounded to bf16 as gemm_reduce_kernel stores it, instead of a qkv row.
+template <bool PART>
+__global__ void rope_kv_write8_kernel(const bf16* qkv, int64_t ld, Partials qp, const bf16* bias, bf16* q_out,
+                                      bf16* k_cache, bf16* v_cache, const float* cos_tab, const float* sin_tab,
+                                      const int64_t* positions, int64_t max_pos, int64_t B, int64_t T_, int64_t Hq,
+                                      int64_t Hkv, int64_t D, int64_t S, int64_t cache_len, int32_t* error_flag,
+                                      const StepState* state, int layer) {
   if (state != nullptr) {
     const int64_t layer_off = (int64_t)layer * B * Hkv * S * D;
     positions = state->args.positions;
@@ -163,10 +166,24 @@ __global__ void rope_kv_write8_kernel(const bf16* qkv, int64_t ld, bf16* q_out, 
   if (state != nullptr && state->halted && head >= Hq) return;
   const int64_t n = idx / (groups * heads);
   const int64_t b = n / T_, t = n % T_;
-  const bf16* src = qkv + n * ld + head * D;
   float xa[8], xb[8], oa[8], ob[8];
-  unpack16(*reinterpret_cast<const uint4*>(src + i), xa, (bf16*)nullptr);
-  unpack16(*reinterpret_cast<const uint4*>(src + i + half), xb, (bf16*)nullptr);
+  if constexpr (PART) {
+    const int64_t col = head * D + i;
+    float va[8], vb[8], ba[8], bb[8];
+    sum_partials8(qp, n, col, va);
+    sum_partials8(qp, n, col + half, vb);
+    unpack16(*reinterpret_cast<const uint4*>(bias + col), ba, (bf16*)nullptr);
+    unpack16(*reinterpret_cast<const uint4*>(bias + col + half), bb, (bf16*)nullptr);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      xa[e] = round_to<bf16>(va[e] + ba[e]);
+      xb[e] = round_to<bf16>(vb[e] + bb[e]);
+    }
+  } else {
+    const bf16* src = qkv + n * ld + head * D;
+    unpack16(*reinterpret_cast<const uint4*>(src + i), xa, (bf16*)nullptr);
+    unpack16(*reinterpret_cast<const uint4*>(src + i + half), xb, (bf16*)nullptr);
+  }
   bf16* dst;
   if (head < Hq + Hkv) {
     const int64_t pos = positions[t];
@@ -210,9 +227,9 @@ int launch_rope_kv_write(hipStream_t st, int dtype, const void* qkv, int64_t ld_
   if (n == 0) return MINITP_OK;
   if (dtype == MINITP_BF16 && D % 16 == 0 && ld_qkv % 8 == 0 && aligned16(qkv) && aligned16(cos_tab) &&
       aligned16(sin_tab)) {
-    rope_kv_write8_kernel<<<(unsigned)cdiv(n / 8, 256), 256, 0, st>>>(
-        (const bf16*)qkv, ld_qkv, (bf16*)q_out, (bf16*)k_cache, (bf16*)v_cache, cos_tab, sin_tab, positions, max_pos,
-        B, T_, Hq, Hkv, D, S, cache_len, error_flag, state, layer);
+    rope_kv_write8_kernel<false><<<(unsigned)cdiv(n / 8, 256), 256, 0, st>>>(
+        (const bf16*)qkv, ld_qkv, Partials{}, nullptr, (bf16*)q_out, (bf16*)k_cache, (bf16*)v_cache, cos_tab, sin_tab,
+        positions, max_pos, B, T_, Hq, Hkv, D, S, cache_len, error_flag, state, layer);
     MINITP_LAUNCH_CHECK();
     return MINITP_OK;
   }
@@ -225,6 +242,23 @@ int launch_rope_kv_write(hipStream_t st, int dtype, const void* qkv, int64_t ld_
     rope_kv_write_kernel<bf16><<<grid, 256, 0, st>>>((const bf16*)qkv, ld_qkv, (bf16*)q_out, (bf16*)k_cache,
                                                      (bf16*)v_cache, cos_tab, sin_tab, positions, max_pos, B, T_, Hq,
                                                      Hkv, D, S, cache_len, error_flag, state, layer);
+  MINITP_LAUNCH_CHECK();
+  return MINITP_OK;
+}
+
+int launch_rope_kv_write_partials(hipStream_t st, const Partials& qkv, const void* bias, void* q_out,
+                                  const float* cos_tab, const float* sin_tab, int64_t max_pos, int64_t B, int64_t T_,
+                                  int64_t Hq, int64_t Hkv, int64_t D, int64_t S, const StepState* state, int layer) {
+  const int64_t n = B * T_ * (Hq + 2 * Hkv) * (D / 2);
+  if (n == 0) return MINITP_OK;
+  if (state == nullptr || bias == nullptr || D % 16 != 0 || qkv.M != B * T_ || qkv.N != (Hq + 2 * Hkv) * D ||
+      qkv.S < 1 || !aligned16(qkv.p) || !aligned16(bias) || !aligned16(cos_tab) || !aligned16(sin_tab)) {
+    set_error("rope_kv_write from partials: D %lld, partial width %lld", (long long)D, (long long)qkv.N);
+    return MINITP_ERR_UNSUPPORTED;
+  }
+  rope_kv_write8_kernel<true><<<(unsigned)cdiv(n / 8, 256), 256, 0, st>>>(
+      nullptr, 0, qkv, (const bf16*)bias, (bf16*)q_out, nullptr, nullptr, cos_tab, sin_tab, nullptr, max_pos, B, T_, Hq,
+      Hkv, D, S, 0, nullptr, state, layer);
   MINITP_LAUNCH_CHECK();
   return MINITP_OK;
 }
