@@ -356,9 +356,18 @@ int device_cus() {
   return cached[dev];
 }
 
+// K steps each part of a tile split over K runs at least (so that the
+// pipeline fills and the fp32 partials stay small against the work)
+constexpr int SPLIT_MIN_STEPS = 16;
+// at most this many parts (7B down projection at 512 tokens, TTFT: 4 or 6
+// parts 12.43-12.55 ms, 8 parts 12.63-12.66 ms, the split-K GEMM 12.82-12.84)
+#ifndef MINITP_TILE_SPLIT_MAX
+#define MINITP_TILE_SPLIT_MAX 4
+#endif
+
 template <int EPI>
 int launch_tile(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy,
-                int64_t M, int64_t N, int64_t K, TileTail tail) {
+                int64_t M, int64_t N, int64_t K, TileTail tail, bool split_all = false) {
   constexpr int WM = MINITP_TILE_WAVES_M, WN = MINITP_TILE_WAVES_N;
   constexpr int64_t PART_BYTES = (int64_t)TM * TN * 4;  // one fp32 tile
   const void* kern = (const void*)gemm_tile_kernel<EPI, WM, WN>;
@@ -373,13 +382,21 @@ int launch_tile(hipStream_t st, const void* x, int64_t ldx, const void* w, const
   const int cus = device_cus();
   const int rem = tiles % cus, nk = (int)cdiv(K, TK);
   int split = 1;
-  if (tail.part != nullptr && tail.count != nullptr && tiles >= cus && rem > 0 && 2 * rem <= cus) {
+  if (split_all) {
+    // fewer tiles than half the CUs: every tile split over K
+    split = std::min(std::min(cus / tiles, MINITP_TILE_SPLIT_MAX), nk / SPLIT_MIN_STEPS);
+    while (split > 1 && (int64_t)tiles * split * PART_BYTES > TILE_TAIL_BYTES) --split;
+    if (split < 2 || tiles > SPLIT_MAX_TUPLES || tail.part == nullptr || tail.count == nullptr) {
+      set_error("gemm_tile: %d tiles of %d K steps do not split", tiles, nk);
+      return MINITP_ERR_UNSUPPORTED;
+    }
+  } else if (tail.part != nullptr && tail.count != nullptr && tiles >= cus && rem > 0 && 2 * rem <= cus) {
     split = std::min(std::min(cus / rem, 4), nk);
     if ((int64_t)rem * split * PART_BYTES > TILE_TAIL_BYTES || rem > SPLIT_MAX_TUPLES) split = 1;
   }
-  const int full = split > 1 ? tiles - rem : tiles;
+  const int full = split_all ? 0 : split > 1 ? tiles - rem : tiles;
   const int per_xcd = (full + 7) / 8;
-  const int grid = 8 * per_xcd + (split > 1 ? rem * split : 0);
+  const int grid = split_all ? tiles * split : 8 * per_xcd + (split > 1 ? rem * split : 0);
   hipLaunchKernelGGL((gemm_tile_kernel<EPI, WM, WN>), dim3((unsigned)grid), dim3(64 * WM * WN), LDS_TILE_BYTES, st,
                      (const bf16*)x, ldx, (const bf16*)w, (const bf16*)bias, (bf16*)y, ldy, (int)M, (int)N, (int)K,
                      tiles_m, tiles_n, per_xcd, full, split, tail.part, tail.count);
@@ -388,6 +405,28 @@ int launch_tile(hipStream_t st, const void* x, int64_t ldx, const void* w, const
 }
 
 }  // namespace
+
+// Whole rows of tiles (M a multiple of 256) but fewer tiles than half the
+// CUs, and K long enough for two parts of SPLIT_MIN_STEPS: every tile split
+// over K, its parts added by the tile's last block (the split-last-round
+// machinery applied to all tiles).
+bool gemm_tile_split_supported(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, bool swiglu) {
+  const int64_t w_rows = swiglu ? 2 * N : N;
+  const int64_t tiles = cdiv(M, TM) * cdiv(N, swiglu ? TN / 2 : TN);
+  return M >= TM && M % TM == 0 && 2 * tiles <= device_cus() && cdiv(K, TK) >= 2 * SPLIT_MIN_STEPS && K % 8 == 0 &&
+         ldx % 8 == 0 && ldx >= K && ldy >= N && M < (1LL << 31) && N < (1LL << 30) &&
+         ((M - 1) * ldx + K) * 2 < (1LL << 32) && w_rows * K * 2 < (1LL << 32);
+}
+
+int launch_gemm_tile_split(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
+                           int64_t ldy, int64_t M, int64_t N, int64_t K, bool swiglu, TileTail tail) {
+  if (!gemm_tile_split_supported(M, N, K, ldx, ldy, swiglu) || !aligned16(x) || !aligned16(w)) {
+    set_error("gemm_tile: split shape M=%lld N=%lld K=%lld not served", (long long)M, (long long)N, (long long)K);
+    return MINITP_ERR_UNSUPPORTED;
+  }
+  if (swiglu) return launch_tile<TILE_SWIGLU>(st, x, ldx, w, nullptr, y, ldy, M, N, K, tail, true);
+  return launch_tile<TILE_STORE>(st, x, ldx, w, bias, y, ldy, M, N, K, tail, true);
+}
 
 bool gemm_tile_supported(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, bool swiglu) {
   const int64_t w_rows = swiglu ? 2 * N : N;

@@ -137,6 +137,12 @@ int launch_gemm_partials(hipStream_t st, int dtype, const void* x, int64_t ldx, 
 bool gemm_tile_supported(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, bool swiglu);
 int launch_gemm_tile(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy,
                      int64_t M, int64_t N, int64_t K, bool swiglu, TileTail tail = TileTail{nullptr, nullptr});
+// The same tiles for products with too few of them (M a multiple of 256,
+// fewer tiles than half the CUs) and a long K: every tile split over K into
+// parts that its last block adds (needs the forward's tail buffers)
+bool gemm_tile_split_supported(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t ldy, bool swiglu);
+int launch_gemm_tile_split(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
+                           int64_t ldy, int64_t M, int64_t N, int64_t K, bool swiglu, TileTail tail);
 
 // elementwise.hip
 int launch_fill_normal(hipStream_t st, int dtype, void* dst, int64_t count, uint64_t seed, uint64_t sid,

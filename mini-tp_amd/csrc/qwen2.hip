@@ -23,6 +23,10 @@
 #include "decode_loop.h"
 #include "kernels.h"
 
+#ifndef MINITP_DOWN_TILE_SPLIT
+#define MINITP_DOWN_TILE_SPLIT 1
+#endif
+
 namespace minitp {
 
 namespace {
@@ -292,6 +296,14 @@ struct Qwen2Program {
         }
         // x += down(act), h = the next layer's input_layernorm(x) (the final norm after the last)
         const void* next_norm = l + 1 < c.num_layers ? L(l + 1, MINITP_W_LN1) : final_norm;
+        // (a long K over too few tiles, e.g. 7B at 512 tokens: the tile kernel
+        // with every tile split over K, then the residual add + norm)
+        if (MINITP_DOWN_TILE_SPLIT && !use_blaslt && gemm_tile_split_supported(M, H, I, I, H, false)) {
+          rc = launch_gemm_tile_split(st, w.act, I, L(l, MINITP_W_DOWN), nullptr, w.h, H, M, H, I, false, tail);
+          if (!rc) rc = launch_add_rmsnorm(st, c.dtype, w.x, w.h, next_norm, w.h, M, H, c.eps);
+          if (rc) return rc;
+          continue;
+        }
         rc = partials(w.act, I, L(l, MINITP_W_DOWN), H, I, &pp);
         if (rc == MINITP_OK) {
           rc = launch_add_rmsnorm_partials(st, w.x, pp, next_norm, w.h, H, c.eps);
