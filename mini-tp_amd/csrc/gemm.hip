@@ -228,17 +228,29 @@ __global__ __launch_bounds__(256) void gemm_reduce_kernel(const float* __restric
   }
 }
 
+// blocks a split-K product aims at: the reduce-kernel form (fp32, direct
+// calls) fills the CUs twice; the form whose partials the next kernel adds
+// (bf16 prompt forwards) once: 128-token 0.5B TTFT 1.62 ms at 512 blocks,
+// 1.49 at 256 (128: 1.53, 192: 1.51, 384: 1.56; per-product mixes of 192-1024
+// no better), 512-token 7B 12.67 -> 12.16 ms
+#ifndef MINITP_SPLIT_BLOCKS
+#define MINITP_SPLIT_BLOCKS 512
+#endif
+#ifndef MINITP_PARTIALS_SPLIT_BLOCKS
+#define MINITP_PARTIALS_SPLIT_BLOCKS 256
+#endif
 // Splits of K (and K elements per split) for an M x N x K product on BM x BN
 // tiles: enough blocks to fill the CUs twice, each at least one chunk deep,
 // and partials that fit the workspace.
 template <typename T, int BM, int BN>
-int64_t split_plan(int64_t M, int64_t N, int64_t K, const float* ws, int64_t ws_bytes, int64_t* kper_out) {
+int64_t split_plan(int64_t M, int64_t N, int64_t K, const float* ws, int64_t ws_bytes, int64_t* kper_out,
+                   int64_t target = MINITP_SPLIT_BLOCKS) {
   constexpr int64_t KCE = chunk_bytes<BM>() / sizeof(T);
   const int64_t tiles = cdiv(N, BN) * cdiv(M, BM);
   const int64_t nchunk = cdiv(K, KCE);
   int64_t S = 1;
   if (ws != nullptr) {
-    S = std::min<int64_t>(cdiv(512, tiles), nchunk);
+    S = std::min<int64_t>(cdiv(target, tiles), nchunk);
     while (S > 1 && S * M * N * (int64_t)sizeof(float) > ws_bytes) --S;
   }
   const int64_t kper = cdiv(nchunk, S) * KCE;
@@ -298,7 +310,8 @@ int gemm_typed(hipStream_t st, const void* x, int64_t ldx, const void* w, const 
 }  // namespace
 
 int launch_gemm_partials(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, int64_t M, int64_t N,
-                         int64_t K, void* ws, int64_t ws_bytes, Partials* out) {
+                         int64_t K, void* ws, int64_t ws_bytes, Partials* out, int64_t target_blocks) {
+  if (target_blocks <= 0) target_blocks = MINITP_PARTIALS_SPLIT_BLOCKS;
   // the product launch_gemm would split (bf16, not on the tile kernel)
   if (dtype != MINITP_BF16 || M <= 0 || N % 8 != 0 || ws == nullptr || !aligned16(ws) || !aligned16(x) ||
       !aligned16(w) || gemm_tile_supported(M, N, K, ldx, N, false) || !gemm_operands_fit(M, N, K, ldx, 2))
@@ -308,14 +321,14 @@ int launch_gemm_partials(hipStream_t st, int dtype, const void* x, int64_t ldx, 
   const bf16 *xb = (const bf16*)x, *wb = (const bf16*)w;
   float* part = (float*)ws;
   if (M >= 512) {
-    S = split_plan<bf16, 128, 128>(M, N, K, part, ws_bytes, &kper);
+    S = split_plan<bf16, 128, 128>(M, N, K, part, ws_bytes, &kper, target_blocks);
     if (S < 2) return MINITP_ERR_UNSUPPORTED;
     grid = dim3((unsigned)cdiv(N, 128), (unsigned)cdiv(M, 128), (unsigned)S);
     hipLaunchKernelGGL((gemm_kernel<bf16, 128, 128, OUT_PARTIAL>), grid, dim3(256), 0, st, xb, ldx, wb, nullptr,
                        nullptr, N, nullptr, part, M, N, K, kper, nullptr);
   } else {
     constexpr int BM = MINITP_GEMM_SMALL_BM, BN = MINITP_GEMM_SMALL_BN;
-    S = split_plan<bf16, BM, BN>(M, N, K, part, ws_bytes, &kper);
+    S = split_plan<bf16, BM, BN>(M, N, K, part, ws_bytes, &kper, target_blocks);
     if (S < 2) return MINITP_ERR_UNSUPPORTED;
     grid = dim3((unsigned)cdiv(N, BN), (unsigned)cdiv(M, BM), (unsigned)S);
     hipLaunchKernelGGL((gemm_kernel<bf16, BM, BN, OUT_PARTIAL>), grid, dim3(256), 0, st, xb, ldx, wb, nullptr, nullptr,

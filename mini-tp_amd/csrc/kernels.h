@@ -128,7 +128,7 @@ int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const voi
 // (the *_partials launchers). MINITP_ERR_UNSUPPORTED when the product is
 // not split (tile kernel, one split, fp32): the caller runs launch_gemm.
 int launch_gemm_partials(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, int64_t M, int64_t N,
-                         int64_t K, void* ws, int64_t ws_bytes, Partials* out);
+                         int64_t K, void* ws, int64_t ws_bytes, Partials* out, int64_t target_blocks = 0);
 
 // gemm_tile.hip: 256 x 256 MFMA tiles (32x32x16 bf16) for prompt-sized
 // bf16 products; swiglu: W is [2N, K] = [gate; up] and y = silu(gate) * up
