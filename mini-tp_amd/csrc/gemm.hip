@@ -30,6 +30,10 @@ namespace minitp {
 namespace {
 
 constexpr int OUT_PARTIAL = 100;  // epilogue: fp32 split-K partials
+// epilogue: SwiGLU of a [gate; up] weight (2N rows): tile column bx holds
+// outputs [bx BN / 2, + BN / 2), its first BN / 2 B rows the gate rows and
+// the rest the matching up rows, so waves wn = 0 hold gate and wn = 1 up
+constexpr int OUT_SWIGLU = 101;
 constexpr uint32_t OOB = 0xffffffffu;  // lane offset that reads zeros
 
 template <int AUX>
@@ -130,7 +134,7 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ x, int6
   // x rows [0, M) and W rows [0, N) as buffers; a lane's piece is read only
   // when its row exists and its K lies inside this block's split
   const __amdgpu_buffer_rsrc_t xr = span_rsrc(x, (uint32_t)(((M - 1) * ldx + K) * ES));
-  const __amdgpu_buffer_rsrc_t wr = span_rsrc(w, (uint32_t)(N * K * ES));
+  const __amdgpu_buffer_rsrc_t wr = span_rsrc(w, (uint32_t)((OUT == OUT_SWIGLU ? 2 : 1) * N * K * ES));
   uint4 ra[DEPTH][LA], rb[DEPTH][LB];
   auto load = [&](int64_t k0, uint4(&a)[LA], uint4(&bb)[LB]) {
 #pragma unroll
@@ -144,8 +148,14 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ x, int6
     for (int i = 0; i < LB; ++i) {
       const int c = tid + i * 256, row = c / CPR, pc = c % CPR;
       const int64_t k = k0 + pc * V;
-      const bool ok = n0 + row < N && k < ke;
-      bb[i] = gemm_load16<GEMM_W_AUX>(wr, ok ? (uint32_t)(((n0 + row) * K + k) * ES) : OOB);
+      int64_t wrow = n0 + row;
+      bool ok = wrow < N && k < ke;
+      if constexpr (OUT == OUT_SWIGLU) {
+        const int64_t j = (int64_t)blockIdx.x * (BN / 2) + row % (BN / 2);
+        wrow = row < BN / 2 ? j : N + j;
+        ok = j < N && k < ke;
+      }
+      bb[i] = gemm_load16<GEMM_W_AUX>(wr, ok ? (uint32_t)((wrow * K + k) * ES) : OOB);
     }
   };
   auto stash = [&](const uint4(&a)[LA], const uint4(&bb)[LB]) {
@@ -188,6 +198,38 @@ __global__ __launch_bounds__(256) void gemm_kernel(const T* __restrict__ x, int6
     }
   }
 
+  if constexpr (OUT == OUT_SWIGLU) {
+    // the up waves hand their accumulators to the gate waves through LDS
+    // (free after the last chunk's barrier): [wm][i][j][r][lane]
+    float* xch = reinterpret_cast<float*>(As);
+    static_assert(2 * FM * FN * 16 * 64 * 4 <= BM * ROWB, "exchange fits the A tile");
+    if (wn == 1) {
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+#pragma unroll
+        for (int j = 0; j < FN; ++j)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) xch[(((wm * FM + i) * FN + j) * 16 + r) * 64 + lane] = acc[i][j][r];
+    }
+    __syncthreads();
+    if (wn == 1) return;
+#pragma unroll
+    for (int i = 0; i < FM; ++i)
+#pragma unroll
+      for (int j = 0; j < FN; ++j) {
+        const int64_t col = (int64_t)blockIdx.x * (BN / 2) + j * 32 + (lane & 31);
+        if (col >= N) continue;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int64_t row = m0 + wm * (BM / 2) + i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+          if (row >= M) continue;
+          const float g = round_to<T>(acc[i][j][r] + 0.f);
+          const float u = round_to<T>(xch[(((wm * FM + i) * FN + j) * 16 + r) * 64 + lane] + 0.f);
+          store_f32<T>(y, row * ldy + col, swiglu<T>(g, u));
+        }
+      }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < FM; ++i)
 #pragma unroll
@@ -308,6 +350,22 @@ int gemm_typed(hipStream_t st, const void* x, int64_t ldx, const void* w, const 
 }
 
 }  // namespace
+
+int launch_gemm_swiglu(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, void* y, int64_t ldy,
+                       int64_t M, int64_t N, int64_t K) {
+  if (M == 0 || N == 0) return MINITP_OK;
+  if (dtype != MINITP_BF16 || M >= 512 || ldy < N || !aligned16(x) || !aligned16(w) ||
+      !gemm_operands_fit(M, 2 * N, K, ldx, 2)) {
+    set_error("gemm: SwiGLU form M=%lld N=%lld K=%lld not served", (long long)M, (long long)N, (long long)K);
+    return MINITP_ERR_UNSUPPORTED;
+  }
+  constexpr int BM = MINITP_GEMM_SMALL_BM, BN = MINITP_GEMM_SMALL_BN;
+  const dim3 grid((unsigned)cdiv(N, BN / 2), (unsigned)cdiv(M, BM), 1u);
+  hipLaunchKernelGGL((gemm_kernel<bf16, BM, BN, OUT_SWIGLU>), grid, dim3(256), 0, st, (const bf16*)x, ldx,
+                     (const bf16*)w, nullptr, (bf16*)y, ldy, nullptr, nullptr, M, N, K, K, nullptr);
+  MINITP_LAUNCH_CHECK();
+  return MINITP_OK;
+}
 
 int launch_gemm_partials(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, int64_t M, int64_t N,
                          int64_t K, void* ws, int64_t ws_bytes, Partials* out, int64_t target_blocks) {

@@ -129,6 +129,11 @@ int launch_gemm(hipStream_t st, int dtype, const void* x, int64_t ldx, const voi
 // not split (tile kernel, one split, fp32): the caller runs launch_gemm.
 int launch_gemm_partials(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, int64_t M, int64_t N,
                          int64_t K, void* ws, int64_t ws_bytes, Partials* out, int64_t target_blocks = 0);
+// bf16 y[M, N] = swiglu(x W_gate^T, x W_up^T) for W = [gate; up] ([2N, K]) on
+// the small tiles, unsplit (M < 512), gate and up rounded to bf16 first as
+// launch_gemm + launch_silu_mul would store and read them
+int launch_gemm_swiglu(hipStream_t st, int dtype, const void* x, int64_t ldx, const void* w, void* y, int64_t ldy,
+                       int64_t M, int64_t N, int64_t K);
 
 // gemm_tile.hip: 256 x 256 MFMA tiles (32x32x16 bf16) for prompt-sized
 // bf16 products; swiglu: W is [2N, K] = [gate; up] and y = silu(gate) * up

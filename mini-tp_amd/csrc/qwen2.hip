@@ -26,6 +26,9 @@
 #ifndef MINITP_DOWN_TILE_SPLIT
 #define MINITP_DOWN_TILE_SPLIT 1
 #endif
+#ifndef MINITP_GEMM_SWIGLU_EPI
+#define MINITP_GEMM_SWIGLU_EPI 1
+#endif
 
 namespace minitp {
 
@@ -287,7 +290,11 @@ struct Qwen2Program {
           rc = partials(w.h, H, L(l, MINITP_W_GATE_UP), 2 * I, H, &pp);
           if (rc == MINITP_OK) {
             rc = launch_silu_mul_partials(st, pp, w.act, I, I);
-          } else if (rc == MINITP_ERR_UNSUPPORTED) {
+          } else if (rc == MINITP_ERR_UNSUPPORTED && MINITP_GEMM_SWIGLU_EPI && !use_blaslt) {
+            // unsplit: SwiGLU in the GEMM's epilogue
+            rc = launch_gemm_swiglu(st, c.dtype, w.h, H, L(l, MINITP_W_GATE_UP), w.act, I, M, I, H);
+          }
+          if (rc == MINITP_ERR_UNSUPPORTED) {
             rc = lin(w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.gu, 2 * I, 2 * I, H);
             const char* up = (const char*)w.gu + I * es();
             if (!rc) rc = launch_silu_mul(st, c.dtype, w.gu, up, 2 * I, w.act, I, M, I);
