@@ -13,7 +13,7 @@
 // a branch, so the compiler can count them precisely instead of waiting for
 // all of them before the next ones issue. Rows are padded by 16 bytes in LDS
 // to spread the MFMA fragment reads over the banks.
-//   bf16: v_mfma_f32_32x32x8bf16_1k (A/B: 4 bf16 per lane, k = 4*(lane/32)+i)
+//   bf16: v_mfma_f32_32x32x16_bf16 (A/B: 8 bf16 per lane, k = 8*(lane/32)+i)
 //   fp32: v_mfma_f32_32x32x2f32     (A/B: 1 float per lane, k = lane/32)
 // Accumulator layout: lane l, register r -> row 8*(r/4) + 4*(l/32) + r%4,
 // column l%32.
