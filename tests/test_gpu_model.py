@@ -122,11 +122,24 @@ def test_synthetic_tiny_equals_state_dict_copy():
         assert ka == kb and torch.equal(va, vb), ka
 
 
-def test_q05b_fp32_256_greedy_ids_bitexact():
+def _set_path(model, path):
+    """Decode path of the model's program: "graph" (the default's per-op
+    kernels) or "persistent" (the opt-in one-launch decode)."""
+    from minitp import _native as N
+
+    prog = model.program()
+    prog.set_decode_path(N.DECODE_PERSISTENT if path == "persistent" else N.DECODE_GRAPH)
+    if path == "persistent":
+        assert prog.persistent_ok(), N.last_error()
+
+
+@pytest.mark.parametrize("path", ["graph", "persistent"])
+def test_q05b_fp32_256_greedy_ids_bitexact(path):
     from minitp.generation import generate_greedy
 
     fx = _fixture("q05b_fp32")
     model = _synthetic("QWEN05B", torch.float32)
+    _set_path(model, path)
     prompt = torch.from_numpy(fx["prompt"]).to(DEV)
     n = fx["ids"].shape[1] - prompt.shape[1]
     ids = generate_greedy(model, prompt, n, early_stop=False).cpu().numpy()
@@ -137,12 +150,15 @@ def test_q05b_fp32_256_greedy_ids_bitexact():
     err = _check_summaries(rows, fx, "step", FP32_LOGIT_ATOL)
     pre = prefill[:, torch.from_numpy(fx["prefill_positions"])].transpose(0, 1)
     err_p = _check_summaries(pre, fx, "prefill", FP32_LOGIT_ATOL)
-    print(f"q05b fp32: 256/256 ids exact; max logit err decode {err:.2e} prefill {err_p:.2e}")
+    model.program().check_decode()
+    print(f"q05b fp32 {path}: 256/256 ids exact; max logit err decode {err:.2e} prefill {err_p:.2e}")
 
 
-def test_q05b_bf16_logits_teacher_forced():
+@pytest.mark.parametrize("path", ["graph", "persistent"])
+def test_q05b_bf16_logits_teacher_forced(path):
     fx = _fixture("q05b_bf16")
     model = _synthetic("QWEN05B", torch.bfloat16)
+    _set_path(model, path)
     prompt = torch.from_numpy(fx["prompt"]).to(DEV)
     n = fx["ids"].shape[1] - prompt.shape[1]
     rows, prefill = _teacher_forced_rows(model, prompt, torch.from_numpy(fx["ids"]), n)
@@ -154,7 +170,8 @@ def test_q05b_bf16_logits_teacher_forced():
     ref = fx["ids"][0, prompt.shape[1]:]
     clear = fx["step_margin"][:, 0] > 0.1
     assert np.array_equal(picks[clear], ref[clear])
-    print(f"q05b bf16: max logit err decode {err:.3f} prefill {err_p:.3f}")
+    model.program().check_decode()
+    print(f"q05b bf16 {path}: max logit err decode {err:.3f} prefill {err_p:.3f}")
 
 
 # ---------------------------------------------------------------------------
