@@ -640,6 +640,23 @@ __global__ __launch_bounds__(NWM * 64) void decode_attn_mfma_kernel(DecodeArgs a
   }
 }
 
+// Inside a forward (st != null) a prompt's attention takes the layer's
+// caches and cache_len from the step state, as the decode kernels do, so a
+// captured prompt graph replays for other caches and positions; direct calls
+// pass them by value.
+struct PrefillKV {
+  const StepState* st;
+  int64_t layer_off;  // elements from a cache base to this layer's [B, Hkv, S, D]
+  template <typename T>
+  __device__ __forceinline__ void resolve(const T*& kc, const T*& vc, int64_t& cache_len) const {
+    if (st != nullptr) {
+      kc = (const T*)st->args.k_cache + layer_off;
+      vc = (const T*)st->args.v_cache + layer_off;
+      cache_len = st->args.cache_len;
+    }
+  }
+};
+
 // ---------------------------------------------------------------------------
 // Prefill: flash-style causal attention, fp32 FMA. Block = (b * Hq + h,
 // 64-query tile); 4 lanes per query, each owning D/4 dims; key tiles of K
@@ -648,7 +665,8 @@ constexpr int QT = 64;
 
 template <typename T, int D>
 __global__ __launch_bounds__(256) void prefill_attn_kernel(const T* q, const T* kc, const T* vc, T* out, AttnShape s,
-                                                           int64_t cache_len, float scale) {
+                                                           int64_t cache_len, float scale, PrefillKV kv) {
+  kv.resolve(kc, vc, cache_len);
   constexpr int DQ = D / 4;
   constexpr int KT = D >= 128 ? 32 : 64;
   __shared__ float Ks[KT][D + 1];
@@ -731,7 +749,8 @@ __global__ __launch_bounds__(256) void prefill_attn_kernel(const T* q, const T* 
 template <int D, int PW>
 __global__ __launch_bounds__(PW * 64) void prefill_attn_mfma_kernel(const bf16* q, const bf16* kc, const bf16* vc,
                                                                     bf16* out, AttnShape s, int64_t cache_len,
-                                                                    float scale) {
+                                                                    float scale, PrefillKV kv) {
+  kv.resolve(kc, vc, cache_len);
   constexpr int PQ = 16 * PW;
   typedef short short4_t __attribute__((ext_vector_type(4)));
   typedef float float4_t __attribute__((ext_vector_type(4)));
@@ -962,7 +981,9 @@ __device__ __forceinline__ float quad_rows_sum(float v) {
 //    eight XCDs round-robin by linear id, and each XCD has its own L2).
 template <int D>
 __global__ __launch_bounds__(256, 2) void prefill_attn_fa_kernel(const bf16* q, const bf16* kc, const bf16* vc, bf16* out,
-                                                              AttnShape s, int64_t cache_len, float scale) {
+                                                              AttnShape s, int64_t cache_len, float scale,
+                                                              PrefillKV kv) {
+  kv.resolve(kc, vc, cache_len);
   typedef float float4_t __attribute__((ext_vector_type(4)));
   typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
   constexpr int NS = 2;              // 16-query strips per wave
@@ -1207,7 +1228,7 @@ int decode_by_d(hipStream_t st, DecodeArgs& a, int nsplit) {
 
 template <typename T, int D>
 int prefill_dispatch(hipStream_t st, const void* q, const void* k, const void* v, void* out, const AttnShape& s,
-                     int64_t cache_len) {
+                     int64_t cache_len, const PrefillKV& kv) {
   const float scale = 1.0f / sqrtf((float)D);
   if constexpr (sizeof(T) == 2) {
     // 128-query blocks (eight strips share each staged K / V tile) once they
@@ -1215,32 +1236,32 @@ int prefill_dispatch(hipStream_t st, const void* q, const void* k, const void* v
     if (D % 32 == 0 && (int64_t)s.B * s.Hq * cdiv(s.T, 128) >= 512)
       hipLaunchKernelGGL((prefill_attn_fa_kernel<D % 32 == 0 ? D : 32>), dim3(s.B * s.Hq, (unsigned)cdiv(s.T, 128)),
                          dim3(256), 0, st, (const bf16*)q, (const bf16*)k, (const bf16*)v, (bf16*)out, s, cache_len,
-                         scale);
+                         scale, kv);
     else if ((int64_t)s.B * s.Hq * cdiv(s.T, 128) >= 512)
       hipLaunchKernelGGL((prefill_attn_mfma_kernel<D, 8>), dim3(s.B * s.Hq, (unsigned)cdiv(s.T, 128)), dim3(512), 0,
-                         st, (const bf16*)q, (const bf16*)k, (const bf16*)v, (bf16*)out, s, cache_len, scale);
+                         st, (const bf16*)q, (const bf16*)k, (const bf16*)v, (bf16*)out, s, cache_len, scale, kv);
     else
       hipLaunchKernelGGL((prefill_attn_mfma_kernel<D, 4>), dim3(s.B * s.Hq, (unsigned)cdiv(s.T, 64)), dim3(256), 0,
-                         st, (const bf16*)q, (const bf16*)k, (const bf16*)v, (bf16*)out, s, cache_len, scale);
+                         st, (const bf16*)q, (const bf16*)k, (const bf16*)v, (bf16*)out, s, cache_len, scale, kv);
   } else
     hipLaunchKernelGGL((prefill_attn_kernel<T, D>), dim3(s.B * s.Hq, (unsigned)cdiv(s.T, QT)), dim3(256), 0, st,
-                       (const T*)q, (const T*)k, (const T*)v, (T*)out, s, cache_len, scale);
+                       (const T*)q, (const T*)k, (const T*)v, (T*)out, s, cache_len, scale, kv);
   MINITP_LAUNCH_CHECK();
   return MINITP_OK;
 }
 
 template <typename T>
 int prefill_by_d(hipStream_t st, const void* q, const void* k, const void* v, void* out, const AttnShape& s,
-                 int64_t cache_len) {
+                 int64_t cache_len, const PrefillKV& kv) {
   switch (s.D) {
     case 16:
-      return prefill_dispatch<T, 16>(st, q, k, v, out, s, cache_len);
+      return prefill_dispatch<T, 16>(st, q, k, v, out, s, cache_len, kv);
     case 32:
-      return prefill_dispatch<T, 32>(st, q, k, v, out, s, cache_len);
+      return prefill_dispatch<T, 32>(st, q, k, v, out, s, cache_len, kv);
     case 64:
-      return prefill_dispatch<T, 64>(st, q, k, v, out, s, cache_len);
+      return prefill_dispatch<T, 64>(st, q, k, v, out, s, cache_len, kv);
     case 128:
-      return prefill_dispatch<T, 128>(st, q, k, v, out, s, cache_len);
+      return prefill_dispatch<T, 128>(st, q, k, v, out, s, cache_len, kv);
   }
   set_error("attention: head_dim %d not supported (16, 32, 64, 128)", s.D);
   return MINITP_ERR_UNSUPPORTED;
@@ -1350,14 +1371,15 @@ int launch_decode_attention(hipStream_t st, int dtype, const void* q, const void
 }
 
 int launch_prefill_attention(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,
-                             void* out, const AttnShape& s, int64_t cache_len) {
+                             void* out, const AttnShape& s, int64_t cache_len, const StepState* state, int layer) {
+  const PrefillKV kv{state, (int64_t)layer * s.B * s.Hkv * s.S * s.D};
   if (s.Hq % s.Hkv != 0) {
     set_error("attention: Hq=%d not divisible by Hkv=%d", s.Hq, s.Hkv);
     return MINITP_ERR_ARG;
   }
   if (s.B * s.T == 0) return MINITP_OK;
-  return dtype == MINITP_F32 ? prefill_by_d<float>(st, q, k_cache, v_cache, out, s, cache_len)
-                             : prefill_by_d<bf16>(st, q, k_cache, v_cache, out, s, cache_len);
+  return dtype == MINITP_F32 ? prefill_by_d<float>(st, q, k_cache, v_cache, out, s, cache_len, kv)
+                             : prefill_by_d<bf16>(st, q, k_cache, v_cache, out, s, cache_len, kv);
 }
 
 }  // namespace minitp

@@ -201,8 +201,11 @@ int64_t attention_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv,
 int launch_decode_attention(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,
                             void* out, const AttnShape& a, int64_t cache_len, const StepState* state, int layer,
                             void* workspace, int64_t workspace_bytes);
+// Inside a forward (state != null) the caches of layer `layer` and cache_len
+// come from the step state (k_cache, v_cache and cache_len unused).
 int launch_prefill_attention(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,
-                             void* out, const AttnShape& a, int64_t cache_len);
+                             void* out, const AttnShape& a, int64_t cache_len, const StepState* state = nullptr,
+                             int layer = 0);
 
 // argmax.hip
 int64_t argmax_workspace_bytes(int64_t B, int64_t V);

@@ -109,7 +109,7 @@ struct Ws {
 };
 
 struct GraphEntry {
-  int64_t batch, max_seq;
+  int64_t batch, tokens, max_seq;
   void* workspace;
   bool eos;  // records the end-of-sequence update after the token selection
   bool pick; // records the token selection (next_tok set; batch > 4 has no pick node otherwise)
@@ -142,6 +142,10 @@ struct Qwen2Program {
   int64_t spin_ticks = 0;
   std::string loop_why = "not initialised";
   int decode_path = MINITP_DECODE_AUTO;
+  // bf16 prompt forwards (last-position logits) through a graph per shape;
+  // direct launches when MINITP_PREFILL_GRAPH=0 is in the environment at
+  // creation
+  bool prefill_graphs = true;
   uint64_t* trace = nullptr;  // persistent-decode phase trace (profiling)
 
   // Bytes at the start of every workspace kept for the persistent decode
@@ -273,7 +277,7 @@ struct Qwen2Program {
         if (rc) return rc;
         const char* kc = (const char*)s.k_cache + l * layer_elems * es();
         const char* vc = (const char*)s.v_cache + l * layer_elems * es();
-        if ((rc = launch_prefill_attention(st, c.dtype, w.q, kc, vc, w.attn, as, s.cache_len))) return rc;
+        if ((rc = launch_prefill_attention(st, c.dtype, w.q, kc, vc, w.attn, as, s.cache_len, w.st, l))) return rc;
         // x += o_proj(attn), h = post_attention_layernorm(x)
         rc = partials(w.attn, q_rows(), L(l, MINITP_W_O), H, q_rows(), &pp);
         if (rc == MINITP_OK) {
@@ -358,7 +362,7 @@ struct Qwen2Program {
       } else {
         const char* kc = (const char*)s.k_cache + l * layer_elems * es();
         const char* vc = (const char*)s.v_cache + l * layer_elems * es();
-        if ((rc = launch_prefill_attention(st, c.dtype, w.q, kc, vc, w.attn, as, s.cache_len))) return rc;
+        if ((rc = launch_prefill_attention(st, c.dtype, w.q, kc, vc, w.attn, as, s.cache_len, w.st, l))) return rc;
       }
       if (fz) {
         GemvArgs g{};
@@ -640,7 +644,7 @@ static int patch_and_launch(Qwen2Program* p, GraphEntry& g, hipStream_t st, cons
   StepState* dst = w.st;
   const void* table = p->embed;
   void* out = w.x;
-  int64_t hidden = p->c.hidden, vocab = p->c.vocab, tt = 1, max_pos = p->c.max_pos;
+  int64_t hidden = p->c.hidden, vocab = p->c.vocab, tt = s.tokens, max_pos = p->c.max_pos;
   const float* cos_tab = p->cos_tab;
   const float* sin_tab = p->sin_tab;
   int head_dim = p->c.head_dim;
@@ -648,13 +652,62 @@ static int patch_and_launch(Qwen2Program* p, GraphEntry& g, hipStream_t st, cons
                   &max_pos, &head_dim};
   hipKernelNodeParams kp{};
   kp.func = p->c.dtype == MINITP_F32 ? (void*)step_embed_kernel<float> : (void*)step_embed_kernel<bf16>;
-  kp.gridDim = dim3((unsigned)s.batch);
+  kp.gridDim = dim3((unsigned)(s.batch * s.tokens));
   kp.blockDim = dim3(EMBED_THREADS);
   kp.sharedMemBytes = 0;
   kp.kernelParams = args;
   kp.extra = nullptr;
   MINITP_RETURN_HIP(hipGraphExecKernelNodeSetParams(g.exec, g.first, &kp));
   MINITP_RETURN_HIP(hipGraphLaunch(g.exec, st));
+  return MINITP_OK;
+}
+
+// One forward through a captured graph of its launch sequence: replayed when
+// a graph of this shape (batch, tokens, max_seq, workspace, early stop, token
+// pick) exists, else run eagerly once and recorded. Every kernel after the
+// first reads the per-call values (ids, positions, cache_len, caches, logits,
+// token outputs) from the step state the first kernel writes, so only that
+// kernel's parameters are patched per call.
+static int run_graphed(Qwen2Program* p, hipStream_t st, const minitp_qwen2_step& s, const Ws& w) {
+  std::lock_guard<std::mutex> lock(p->mu);
+  for (auto& g : p->graphs)
+    if (g.batch == s.batch && g.tokens == s.tokens && g.max_seq == s.max_seq && g.workspace == s.workspace &&
+        g.eos == (s.eos_state != nullptr) && g.pick == (s.next_tok != nullptr))
+      return patch_and_launch(p, g, st, s, w);
+  // First call with this shape: run eagerly, then record the same sequence.
+  int rc = p->run(st, s, w);
+  if (rc) return rc;
+  if (!p->capture_stream) MINITP_RETURN_HIP(hipStreamCreateWithFlags(&p->capture_stream, hipStreamNonBlocking));
+  GraphEntry g{};
+  g.batch = s.batch;
+  g.tokens = s.tokens;
+  g.max_seq = s.max_seq;
+  g.workspace = s.workspace;
+  g.eos = s.eos_state != nullptr;
+  g.pick = s.next_tok != nullptr;
+  MINITP_RETURN_HIP(hipStreamBeginCapture(p->capture_stream, hipStreamCaptureModeRelaxed));
+  rc = p->run(p->capture_stream, s, w);
+  hipError_t e = hipStreamEndCapture(p->capture_stream, &g.graph);
+  if (rc) {
+    if (e == hipSuccess) (void)hipGraphDestroy(g.graph);
+    return rc;
+  }
+  MINITP_RETURN_HIP(e);
+  size_t n_roots = 0;
+  MINITP_RETURN_HIP(hipGraphGetRootNodes(g.graph, nullptr, &n_roots));
+  if (n_roots != 1) {
+    (void)hipGraphDestroy(g.graph);
+    set_error("forward graph has %zu root nodes, expected 1", n_roots);
+    return MINITP_ERR_HIP;
+  }
+  MINITP_RETURN_HIP(hipGraphGetRootNodes(g.graph, &g.first, &n_roots));
+  MINITP_RETURN_HIP(hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0));
+  if (p->graphs.size() >= 8) {  // bounded cache: drop the oldest shape
+    (void)hipGraphExecDestroy(p->graphs.front().exec);
+    (void)hipGraphDestroy(p->graphs.front().graph);
+    p->graphs.erase(p->graphs.begin());
+  }
+  p->graphs.push_back(g);
   return MINITP_OK;
 }
 
@@ -681,6 +734,10 @@ int minitp_qwen2_create(const minitp_qwen2_config* cfg, const minitp_qwen2_weigh
     MINITP_CHECK_ARG(w->layers[i] != nullptr && minitp::aligned16(w->layers[i]), "layer weight %d NULL or unaligned",
                      i);
   auto* p = new (std::nothrow) Qwen2Program();
+  if (p != nullptr) {
+    const char* pg = getenv("MINITP_PREFILL_GRAPH");
+    p->prefill_graphs = !(pg != nullptr && pg[0] == '0');
+  }
   if (!p) {
     minitp::set_error("out of host memory");
     return MINITP_ERR_HIP;
@@ -772,6 +829,11 @@ int minitp_qwen2_forward(void* handle, void* stream, const minitp_qwen2_step* st
   minitp::Ws w;
   int rc = p->check_step(step, w);
   if (rc) return rc;
+  // bf16 prompts with last-position logits replay a graph per shape (those
+  // with every position's logits store to a per-call buffer: run directly)
+  if (p->prefill_graphs && step->tokens > 1 && !step->logits_all && p->c.dtype == MINITP_BF16 &&
+      !minitp::blaslt_requested())
+    return minitp::run_graphed(p, (hipStream_t)stream, *step, w);
   return p->run((hipStream_t)stream, *step, w);
 }
 
@@ -798,44 +860,7 @@ int minitp_qwen2_decode(void* handle, void* stream, const minitp_qwen2_step* ste
     }
     return p->run_loop(st, *step);
   }
-  std::lock_guard<std::mutex> lock(p->mu);
-  for (auto& g : p->graphs)
-    if (g.batch == step->batch && g.max_seq == step->max_seq && g.workspace == step->workspace &&
-        g.eos == (step->eos_state != nullptr) && g.pick == (step->next_tok != nullptr))
-      return minitp::patch_and_launch(p, g, st, *step, w);
-  // First step with this shape: run eagerly, then record the same sequence.
-  if ((rc = p->run(st, *step, w))) return rc;
-  if (!p->capture_stream) MINITP_RETURN_HIP(hipStreamCreateWithFlags(&p->capture_stream, hipStreamNonBlocking));
-  minitp::GraphEntry g{};
-  g.batch = step->batch;
-  g.max_seq = step->max_seq;
-  g.workspace = step->workspace;
-  g.eos = step->eos_state != nullptr;
-  g.pick = step->next_tok != nullptr;
-  MINITP_RETURN_HIP(hipStreamBeginCapture(p->capture_stream, hipStreamCaptureModeRelaxed));
-  rc = p->run(p->capture_stream, *step, w);
-  hipError_t e = hipStreamEndCapture(p->capture_stream, &g.graph);
-  if (rc) {
-    if (e == hipSuccess) (void)hipGraphDestroy(g.graph);
-    return rc;
-  }
-  MINITP_RETURN_HIP(e);
-  size_t n_roots = 0;
-  MINITP_RETURN_HIP(hipGraphGetRootNodes(g.graph, nullptr, &n_roots));
-  if (n_roots != 1) {
-    (void)hipGraphDestroy(g.graph);
-    minitp::set_error("decode graph has %zu root nodes, expected 1", n_roots);
-    return MINITP_ERR_HIP;
-  }
-  MINITP_RETURN_HIP(hipGraphGetRootNodes(g.graph, &g.first, &n_roots));
-  MINITP_RETURN_HIP(hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0));
-  if (p->graphs.size() >= 8) {  // bounded cache: drop the oldest shape
-    (void)hipGraphExecDestroy(p->graphs.front().exec);
-    (void)hipGraphDestroy(p->graphs.front().graph);
-    p->graphs.erase(p->graphs.begin());
-  }
-  p->graphs.push_back(g);
-  return MINITP_OK;
+  return minitp::run_graphed(p, st, *step, w);
 }
 
 }  // extern "C"

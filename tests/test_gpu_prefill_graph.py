@@ -1,0 +1,81 @@
+"""bf16 prompt forwards with last-position logits run through a graph per
+shape (batch, tokens, max_seq, workspace, early stop, token pick): the first
+call of a shape runs directly and is recorded, later calls patch the first
+kernel's per-call values and replay. Every later kernel reads the prompt ids,
+positions, cache_len, the caches and the logits buffer from the step state, so
+a replay with other prompts, other caches or a non-empty cache must give the
+bits of a direct run (MINITP_PREFILL_GRAPH=0 when the program is created).
+Shapes: the 0.5B layer shape with 2 layers, batch 1, 3 (LM-head GEMV + argmax)
+and 8 (LM-head GEMM, then argmax)."""
+
+import dataclasses
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _models(monkeypatch):
+    from minitp import synthetic
+
+    cfg = dataclasses.replace(synthetic.SHAPES["qwen2.5-0.5b"], num_hidden_layers=2)
+    graphed = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device=DEV, seed=0)
+    direct = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device=DEV, seed=0)
+    monkeypatch.setenv("MINITP_PREFILL_GRAPH", "0")
+    direct_prog = direct.program()
+    monkeypatch.delenv("MINITP_PREFILL_GRAPH")
+    graphed_prog = graphed.program()
+    return cfg, (graphed, graphed_prog), (direct, direct_prog)
+
+
+def _run(model, prompts):
+    """Last-position prefill logits and three greedy picks for each prompt in
+    turn (the first of a shape records the graph, the rest replay it)."""
+    from minitp.generation import GenerationState
+
+    out = []
+    for p in prompts:
+        st = GenerationState(model, p, 4, prefill_logits="last")
+        logits = st.prefill()
+        out.append(logits.float().clone())
+        tok = st.select_next(logits)
+        for _ in range(3):
+            out.append(tok.clone())
+            pos = st.append(tok)
+            tok = st.select_next(st.decode_step(tok, pos))
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("batch", [1, 3, 8])
+def test_prefill_graph_replays_match_direct_runs_bitwise(batch, monkeypatch):
+    cfg, (graphed, gprog), (direct, dprog) = _models(monkeypatch)
+    g = torch.Generator().manual_seed(11 + batch)
+    prompts = [torch.randint(0, cfg.vocab_size, (batch, 40), generator=g).to(DEV) for _ in range(3)]
+    resume = [torch.randint(0, cfg.vocab_size, (batch, 40), generator=g).to(DEV)]
+    got = _run(graphed, prompts)
+    ref = _run(direct, prompts)
+    assert graphed.program() is gprog and direct.program() is dprog  # created once, as set above
+    assert len(got) == len(ref)
+    for i, (a, b) in enumerate(zip(got, ref)):
+        assert torch.isfinite(a.float()).all(), i
+        assert torch.equal(a, b), (i, (a.float() - b.float()).abs().max().item())
+    # the prompts differ, so the replays were not returning the recorded call's values
+    assert not torch.equal(got[0], got[4])
+    # prefills of the same length on a filled cache (cache_len 40, then 80)
+    # replay the graph recorded for the empty one
+    from minitp.generation import GenerationState
+
+    outs = []
+    for model in (graphed, direct):
+        first = GenerationState(model, prompts[0], 100, prefill_logits="last")
+        first.prefill()
+        second = GenerationState(model, prompts[1], 1, prefill_logits="last", kv=first.kv)
+        a = second.prefill().float().clone()
+        third = GenerationState(model, resume[0], 1, prefill_logits="last", kv=second.kv)
+        outs.append((a, third.prefill().float().clone()))
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
+    assert torch.isfinite(outs[0][1]).all()
