@@ -669,6 +669,9 @@ static int patch_and_launch(Qwen2Program* p, GraphEntry& g, hipStream_t st, cons
 // token outputs) from the step state the first kernel writes, so only that
 // kernel's parameters are patched per call.
 static int run_graphed(Qwen2Program* p, hipStream_t st, const minitp_qwen2_step& s, const Ws& w) {
+  // a caller capturing its own stream records the direct launch sequence
+  hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) return p->run(st, s, w);
   std::lock_guard<std::mutex> lock(p->mu);
   for (auto& g : p->graphs)
     if (g.batch == s.batch && g.tokens == s.tokens && g.max_seq == s.max_seq && g.workspace == s.workspace &&
