@@ -113,6 +113,7 @@ struct GraphEntry {
   void* workspace;
   bool eos;  // records the end-of-sequence update after the token selection
   bool pick; // records the token selection (next_tok set; batch > 4 has no pick node otherwise)
+  bool all;  // every position's logits (an LM head over B x T rows) rather than the last's
   hipGraph_t graph;
   hipGraphExec_t exec;
   hipGraphNode_t first;
@@ -187,6 +188,18 @@ struct Qwen2Program {
     w.split_count = w.st ? (uint32_t*)((char*)w.st + offsetof(StepState, split_count)) : nullptr;
     w.bytes = off;
     return w;
+  }
+
+  // bf16 prompts replay a graph per shape when every kernel of their forward
+  // reads the per-call values from the step state: all of them with the last
+  // position's logits; with every position's logits, those whose LM head runs
+  // launch_gemm (logits pointer from the state), not the GEMV form (few rows)
+  // or the tile kernel (M >= 256), which store to the pointer they are given.
+  bool prompt_graphable(const minitp_qwen2_step& s) const {
+    if (!prefill_graphs || s.tokens <= 1 || c.dtype != MINITP_BF16 || blaslt_requested()) return false;
+    if (!s.logits_all) return true;
+    const int64_t M = s.batch * s.tokens;
+    return !fused(M) && !gemm_tile_supported(M, c.vocab, c.hidden, c.hidden, c.vocab, false);
   }
 
   bool fused(int64_t M) const {
@@ -466,7 +479,7 @@ struct Qwen2Program {
       g.norm_w = final_norm;
       g.eps = c.eps;
       g.w = lm_head;
-      g.y = s.logits;  // forwards with every position's logits are never captured
+      g.y = s.logits;  // (not captured: prompt_graphable)
       g.ldy = V;
       g.M = M;
       g.N = V;
@@ -664,7 +677,8 @@ static int patch_and_launch(Qwen2Program* p, GraphEntry& g, hipStream_t st, cons
 
 // One forward through a captured graph of its launch sequence: replayed when
 // a graph of this shape (batch, tokens, max_seq, workspace, early stop, token
-// pick) exists, else run eagerly once and recorded. Every kernel after the
+// pick, all-position logits: everything the launch sequence depends on)
+// exists, else run eagerly once and recorded. Every kernel after the
 // first reads the per-call values (ids, positions, cache_len, caches, logits,
 // token outputs) from the step state the first kernel writes, so only that
 // kernel's parameters are patched per call.
@@ -675,7 +689,7 @@ static int run_graphed(Qwen2Program* p, hipStream_t st, const minitp_qwen2_step&
   std::lock_guard<std::mutex> lock(p->mu);
   for (auto& g : p->graphs)
     if (g.batch == s.batch && g.tokens == s.tokens && g.max_seq == s.max_seq && g.workspace == s.workspace &&
-        g.eos == (s.eos_state != nullptr) && g.pick == (s.next_tok != nullptr))
+        g.eos == (s.eos_state != nullptr) && g.pick == (s.next_tok != nullptr) && g.all == (s.logits_all != 0))
       return patch_and_launch(p, g, st, s, w);
   // First call with this shape: run eagerly, then record the same sequence.
   int rc = p->run(st, s, w);
@@ -688,6 +702,7 @@ static int run_graphed(Qwen2Program* p, hipStream_t st, const minitp_qwen2_step&
   g.workspace = s.workspace;
   g.eos = s.eos_state != nullptr;
   g.pick = s.next_tok != nullptr;
+  g.all = s.logits_all != 0;
   MINITP_RETURN_HIP(hipStreamBeginCapture(p->capture_stream, hipStreamCaptureModeRelaxed));
   rc = p->run(p->capture_stream, s, w);
   hipError_t e = hipStreamEndCapture(p->capture_stream, &g.graph);
@@ -832,11 +847,7 @@ int minitp_qwen2_forward(void* handle, void* stream, const minitp_qwen2_step* st
   minitp::Ws w;
   int rc = p->check_step(step, w);
   if (rc) return rc;
-  // bf16 prompts with last-position logits replay a graph per shape (those
-  // with every position's logits store to a per-call buffer: run directly)
-  if (p->prefill_graphs && step->tokens > 1 && !step->logits_all && p->c.dtype == MINITP_BF16 &&
-      !minitp::blaslt_requested())
-    return minitp::run_graphed(p, (hipStream_t)stream, *step, w);
+  if (p->prompt_graphable(*step)) return minitp::run_graphed(p, (hipStream_t)stream, *step, w);
   return p->run((hipStream_t)stream, *step, w);
 }
 

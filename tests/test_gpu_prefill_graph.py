@@ -1,4 +1,5 @@
-"""bf16 prompt forwards with last-position logits run through a graph per
+"""bf16 prompt forwards (last-position logits; every position's logits where
+the LM head is the small-M GEMM) run through a graph per
 shape (batch, tokens, max_seq, workspace, early stop, token pick): the first
 call of a shape runs directly and is recorded, later calls patch the first
 kernel's per-call values and replay. Every later kernel reads the prompt ids,
@@ -79,3 +80,46 @@ def test_prefill_graph_replays_match_direct_runs_bitwise(batch, monkeypatch):
     torch.cuda.synchronize()
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
     assert torch.isfinite(outs[0][1]).all()
+
+
+def test_prefill_graph_all_position_logits_bitwise(monkeypatch):
+    """The reference's default prefill (every position's logits) replays a
+    graph too when its LM head is the small-M GEMM, which stores through the
+    step state's logits pointer: two prompts of 40 tokens, bitwise against a
+    direct run, each into its own logits buffer."""
+    from minitp.generation import GenerationState
+
+    cfg, (graphed, _), (direct, _) = _models(monkeypatch)
+    g = torch.Generator().manual_seed(3)
+    prompts = [torch.randint(0, cfg.vocab_size, (1, 40), generator=g).to(DEV) for _ in range(3)]
+    outs = []
+    for model in (graphed, direct):
+        outs.append([GenerationState(model, p, 2).prefill().float().clone() for p in prompts])
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert a.shape == (1, 40, cfg.vocab_size) and torch.isfinite(a).all()
+        assert torch.equal(a, b), (a - b).abs().max().item()
+    assert not torch.equal(outs[0][0], outs[0][1])
+
+
+def test_prefill_graphs_of_one_shape_keep_the_logits_form_apart(monkeypatch):
+    """Every-position and last-position prefills of one shape run different
+    LM heads into buffers of different sizes: each replays its own graph
+    (alternating forms, bitwise against direct runs)."""
+    from minitp.generation import GenerationState
+
+    cfg, (graphed, _), (direct, _) = _models(monkeypatch)
+    g = torch.Generator().manual_seed(9)
+    prompts = [torch.randint(0, cfg.vocab_size, (2, 64), generator=g).to(DEV) for _ in range(2)]
+    outs = []
+    for model in (graphed, direct):
+        got = []
+        for p in prompts:
+            for form in ("all", "last", "all"):
+                got.append(GenerationState(model, p, 4, prefill_logits=form).prefill().float().clone())
+        outs.append(got)
+    torch.cuda.synchronize()
+    for a, b in zip(*outs):
+        assert torch.isfinite(a).all()
+        assert torch.equal(a, b), (a - b).abs().max().item()
+    assert outs[0][0].shape == (2, 64, cfg.vocab_size) and outs[0][1].shape == (2, 1, cfg.vocab_size)
