@@ -108,6 +108,17 @@ struct Ws {
   int64_t bytes;
 };
 
+// What a prompt forward's launch sequence depends on (its graph key).
+struct GraphKey {
+  int64_t batch, tokens, max_seq;
+  void* workspace;
+  bool eos, pick, all;
+  bool operator==(const GraphKey& o) const {
+    return batch == o.batch && tokens == o.tokens && max_seq == o.max_seq && workspace == o.workspace &&
+           eos == o.eos && pick == o.pick && all == o.all;
+  }
+};
+
 struct GraphEntry {
   int64_t batch, tokens, max_seq;
   void* workspace;
@@ -133,6 +144,7 @@ struct Qwen2Program {
   std::vector<const void*> lw;
   std::mutex mu;
   std::vector<GraphEntry> graphs;
+  std::vector<GraphKey> prompt_seen;  // prompt shapes run once (recorded on the next call)
   hipStream_t capture_stream = nullptr;
   // persistent batch-1 decode (decode_loop.hip)
   LoopLayout loop_ll{};
@@ -692,8 +704,21 @@ static int run_graphed(Qwen2Program* p, hipStream_t st, const minitp_qwen2_step&
         g.eos == (s.eos_state != nullptr) && g.pick == (s.next_tok != nullptr) && g.all == (s.logits_all != 0))
       return patch_and_launch(p, g, st, s, w);
   // First call with this shape: run eagerly, then record the same sequence.
+  // A prompt shape records on its second call only, so one-off prompt
+  // lengths never pay a capture or push a graph out of the cache.
   int rc = p->run(st, s, w);
   if (rc) return rc;
+  if (s.tokens > 1) {
+    const GraphKey key{s.batch, s.tokens, s.max_seq, s.workspace, s.eos_state != nullptr, s.next_tok != nullptr,
+                       s.logits_all != 0};
+    bool seen = false;
+    for (const auto& k : p->prompt_seen) seen = seen || k == key;
+    if (!seen) {
+      if (p->prompt_seen.size() >= 32) p->prompt_seen.erase(p->prompt_seen.begin());
+      p->prompt_seen.push_back(key);
+      return MINITP_OK;
+    }
+  }
   if (!p->capture_stream) MINITP_RETURN_HIP(hipStreamCreateWithFlags(&p->capture_stream, hipStreamNonBlocking));
   GraphEntry g{};
   g.batch = s.batch;
@@ -720,10 +745,18 @@ static int run_graphed(Qwen2Program* p, hipStream_t st, const minitp_qwen2_step&
   }
   MINITP_RETURN_HIP(hipGraphGetRootNodes(g.graph, &g.first, &n_roots));
   MINITP_RETURN_HIP(hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0));
-  if (p->graphs.size() >= 8) {  // bounded cache: drop the oldest shape
-    (void)hipGraphExecDestroy(p->graphs.front().exec);
-    (void)hipGraphDestroy(p->graphs.front().graph);
-    p->graphs.erase(p->graphs.begin());
+  // bounded cache, at most 8 decode and 8 prompt graphs: drop the oldest of
+  // the new graph's kind
+  int same_kind = 0;
+  for (const auto& e : p->graphs) same_kind += (e.tokens > 1) == (g.tokens > 1);
+  if (same_kind >= 8) {
+    for (auto it = p->graphs.begin(); it != p->graphs.end(); ++it)
+      if ((it->tokens > 1) == (g.tokens > 1)) {
+        (void)hipGraphExecDestroy(it->exec);
+        (void)hipGraphDestroy(it->graph);
+        p->graphs.erase(it);
+        break;
+      }
   }
   p->graphs.push_back(g);
   return MINITP_OK;

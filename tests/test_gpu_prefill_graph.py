@@ -1,8 +1,8 @@
 """bf16 prompt forwards (last-position logits; every position's logits where
 the LM head is the small-M GEMM) run through a graph per
-shape (batch, tokens, max_seq, workspace, early stop, token pick): the first
-call of a shape runs directly and is recorded, later calls patch the first
-kernel's per-call values and replay. Every later kernel reads the prompt ids,
+shape (batch, tokens, max_seq, workspace, early stop, token pick, logits
+form): the first call of a shape runs directly, the second runs directly and
+is recorded, later calls patch the first kernel's per-call values and replay. Every later kernel reads the prompt ids,
 positions, cache_len, the caches and the logits buffer from the step state, so
 a replay with other prompts, other caches or a non-empty cache must give the
 bits of a direct run (MINITP_PREFILL_GRAPH=0 when the program is created).
@@ -33,7 +33,7 @@ def _models(monkeypatch):
 
 def _run(model, prompts):
     """Last-position prefill logits and three greedy picks for each prompt in
-    turn (the first of a shape records the graph, the rest replay it)."""
+    turn (the second of a shape records the graph, the third replays it)."""
     from minitp.generation import GenerationState
 
     out = []
@@ -65,8 +65,8 @@ def test_prefill_graph_replays_match_direct_runs_bitwise(batch, monkeypatch):
         assert torch.equal(a, b), (i, (a.float() - b.float()).abs().max().item())
     # the prompts differ, so the replays were not returning the recorded call's values
     assert not torch.equal(got[0], got[4])
-    # prefills of the same length on a filled cache (cache_len 40, then 80)
-    # replay the graph recorded for the empty one
+    # prefills of the same length on an empty cache, then on a filled one
+    # (cache_len 40: recorded), then at cache_len 80 (a replay)
     from minitp.generation import GenerationState
 
     outs = []
