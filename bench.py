@@ -89,7 +89,6 @@ def parse(argv=None):
                     help="host seconds of decode steps per CPU-baseline sample (the prefill comes on top)")
     ap.add_argument("--cpu-configs", default="tiny-fp32,q05b-bf16,q05b-fp32,q7b-bf16,q7b-fp32",
                     help="comma-separated CPU-baseline samples")
-    ap.add_argument("--decode-path", default="auto", choices=["auto", "graph", "persistent"])
     ap.add_argument("--workload", default="q05b", choices=["q05b", *sorted(WORKLOADS)],
                     help="q05b (default): the headline line; another name prints only that workload's line")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -107,8 +106,8 @@ def parse(argv=None):
                     help="only run one generation of the headline workload with TOKENS new tokens after a warm-up "
                          "one and exit: the workload of the decode kernel profiles")
     ap.add_argument("--eager-decode", type=int, default=0, metavar="STEPS",
-                    help="prefill the --workload's prompt, then run STEPS decode steps as eager launches (no graph, "
-                         "no persistent kernel) and exit: the workload of the per-kernel counter passes")
+                    help="prefill the --workload's prompt, then run STEPS decode steps as eager launches (no graph) "
+                         "and exit: the workload of the per-kernel counter passes")
     return ap.parse_args(argv)
 
 
@@ -169,13 +168,6 @@ class StepSource:
             self.left -= m
             k -= m
         return seconds
-
-
-def set_decode_path(model, path: str) -> None:
-    from minitp import _native as N
-
-    code = {"auto": N.DECODE_AUTO, "graph": N.DECODE_GRAPH, "persistent": N.DECODE_PERSISTENT}[path]
-    model.program().set_decode_path(code)
 
 
 def one_generation(model, prompt, new_tokens: int, prefill_logits: str = "last") -> dict:
@@ -552,7 +544,6 @@ def headline(args) -> dict:
     warm = max(1, args.warmup)
     with torch.inference_mode():
         model = build_synthetic_model(cfg, dtype=torch.bfloat16, device="cuda", seed=0)
-        set_decode_path(model, args.decode_path)
         prompt = synthetic_prompt(cfg.vocab_size, 1, PROMPT_LEN, seed=0, device="cuda")
         src = StepSource(model, prompt, NEW_TOKENS)
         src.run(warm)
@@ -656,7 +647,6 @@ def main(argv=None):
                 torch.cuda.synchronize()
                 print(json.dumps({"kernel": DOMINANT, "launches": 4 * QWEN05B.num_hidden_layers}), flush=True)
                 return
-            set_decode_path(model, args.decode_path)
             prompt = synthetic_prompt(QWEN05B.vocab_size, 1, PROMPT_LEN, seed=0, device="cuda")
             src = StepSource(model, prompt, args.decode_only)
             src.run(args.decode_only - 1)

@@ -22,7 +22,7 @@
 extern "C" {
 #endif
 
-#define MINITP_ABI_VERSION 4
+#define MINITP_ABI_VERSION 5
 
 enum {
   MINITP_OK = 0,
@@ -199,17 +199,7 @@ typedef struct minitp_qwen2_weights {
   const float* rope_cos;  /* [max_pos, D] fp32 */
   const float* rope_sin;
   const void* const* layers; /* [num_layers * MINITP_W_PER_LAYER] */
-  /* Device memory of at least minitp_qwen2_table_bytes(cfg) bytes, owned by
-   * the caller for the life of the handle: create() writes the per-layer
-   * weight table of the persistent decode into it (one synchronous copy).
-   * NULL disables the persistent decode (decode then always replays the
-   * graph). */
-  void* device_table;
-  int64_t device_table_bytes;
 } minitp_qwen2_weights;
-
-/* Bytes of device memory minitp_qwen2_weights.device_table must provide. */
-int64_t minitp_qwen2_table_bytes(const minitp_qwen2_config* cfg);
 
 /* One forward over ids [B, T]. logits: [B, T, V] when logits_all, else the
  * last position only [B, V]. next_tok (optional): argmax of the last
@@ -260,9 +250,10 @@ int minitp_qwen2_create(const minitp_qwen2_config* cfg, const minitp_qwen2_weigh
                         void** handle);
 int minitp_qwen2_destroy(void* handle);
 /* Workspace for forwards of up to max_tokens = B*T rows, batch B, cache S.
- * A workspace used by minitp_qwen2_decode must be zero-filled once before
- * its first use (its first bytes hold the persistent decode's step counter
- * and hand-off words) and then only be used with this handle. */
+ * A workspace must be zero-filled once before its first use (its first
+ * bytes hold the step state: the error word and the arrival words of the
+ * split products, which every launch leaves at zero) and then only be used
+ * with this handle. */
 int64_t minitp_qwen2_workspace_bytes(void* handle, int64_t max_tokens, int64_t batch,
                                      int64_t max_seq);
 /* GenerationState.prefill / TPQwen2ForCausalLM.forward (generation.py:112-117,
@@ -271,35 +262,14 @@ int minitp_qwen2_forward(void* handle, void* stream, const minitp_qwen2_step* st
 /* GenerationState.decode_step (generation.py:129-130): one T == 1 forward,
  * replayed from a hipGraph captured on first use for (batch, max_seq,
  * workspace), with per-step scalars and pointers patched into the graph's
- * first node. With MINITP_DECODE_PERSISTENT selected, batch 1 runs the
- * persistent decode instead (one launch per token, one block per CU, blocks
- * exchanging results through the workspace). */
+ * first node. */
 int minitp_qwen2_decode(void* handle, void* stream, const minitp_qwen2_step* step);
-
-/* Decode path selection (tests, benchmarks): MINITP_DECODE_AUTO (default:
- * the graph, the faster path at every measured shape), MINITP_DECODE_GRAPH (always the
- * graph) or MINITP_DECODE_PERSISTENT (batch 1 only; decode returns
- * MINITP_ERR_UNSUPPORTED where the persistent kernel cannot run). */
-enum { MINITP_DECODE_AUTO = 0, MINITP_DECODE_GRAPH = 1, MINITP_DECODE_PERSISTENT = 2 };
-int minitp_qwen2_set_decode_path(void* handle, int path);
-/* Phase trace of the persistent decode (profiling): with a device buffer of
- * at least minitp_qwen2_trace_bytes(handle) bytes set, every persistent
- * step writes, per block, the wall clock (64-bit ticks of the device's
- * constant-rate clock, hipDeviceAttributeWallClockRate kHz) at its start, at
- * the input-ready and output-written points of every layer's phases (A_in,
- * A_out, B_in, B_attn, B_out, C_in, C_out, D_in, D_out) and at the LM head
- * (input ready, partial written, token written), row b = block b. NULL
- * turns tracing off. */
-int64_t minitp_qwen2_trace_bytes(void* handle);
-int minitp_qwen2_set_trace(void* handle, void* trace, int64_t bytes);
-/* 1 when batch-1 decode of this handle runs the persistent kernel, else 0
- * (reason in minitp_last_error). */
-int minitp_qwen2_persistent_ok(void* handle);
-/* Waits for `stream`, then reports a persistent-decode failure recorded in
- * `workspace` since the last check: MINITP_ERR_HIP when a hand-off wait ran
- * out of time (every later step on that workspace aborts until this call
- * clears the record), MINITP_ERR_RANGE for a position outside the RoPE
- * table. Clears the record. */
+/* Out-of-range RoPE positions (rope.py:37-45, where the reference's gather
+ * raises): a forward whose position lies outside the table computes with NaN
+ * rotary rows and sets a sticky error word in its workspace, because a
+ * graph-replayed step cannot return a status for a value that lives on the
+ * device. This waits for `stream`, returns MINITP_ERR_RANGE if any forward
+ * on `workspace` since the last check set the word, and clears it. */
 int minitp_qwen2_decode_check(void* handle, void* stream, void* workspace);
 
 #ifdef __cplusplus

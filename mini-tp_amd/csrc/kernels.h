@@ -104,11 +104,10 @@ bool gemv_norm_supported(int dtype, int64_t M, int64_t K);
 // When `state` is non-null the output base is state->logits (graph replays).
 // With a workspace (ws, ws_bytes), small-M products split K over more
 // blocks and reduce the fp32 partials in a second kernel.
-// GEMM workspace of a forward: hipBLASLt's (its heuristics find solutions
-// for the 7B prefill shapes only with tens of MiB), of which the split-K
-// partials of launch_gemm use the first GEMM_SPLIT_BYTES.
-// The tile GEMM's split of its last, partial round over K (TileTail) takes
-// the next TILE_TAIL_BYTES.
+// GEMM workspace of a forward: the split-K partials of launch_gemm use the
+// first GEMM_SPLIT_BYTES (launch_gemm_partials may take all of it); the
+// tile GEMM's split of its last, partial round over K (TileTail) takes the
+// next TILE_TAIL_BYTES.
 constexpr int64_t GEMM_SPLIT_BYTES = 8LL << 20;
 constexpr int64_t TILE_TAIL_BYTES = 64LL << 20;
 constexpr int64_t GEMM_WS_BYTES = GEMM_SPLIT_BYTES + TILE_TAIL_BYTES;
@@ -170,13 +169,6 @@ int launch_add_rmsnorm(hipStream_t st, int dtype, void* x, const void* delta, co
 int launch_add_rmsnorm_partials(hipStream_t st, void* x, const Partials& delta, const void* w, void* out,
                                 int64_t hidden, float eps);
 int launch_silu_mul_partials(hipStream_t st, const Partials& gu, void* out, int64_t ld_out, int64_t n);
-// MINITP_GEMM=blaslt in the environment: prompt GEMMs on hipBLASLt (a
-// benchmark comparison; the product path runs the library's own kernels)
-bool blaslt_requested();
-// hipBLASLt bf16 y = x W^T (+ bias) for prompt-sized M outside stream capture;
-// MINITP_ERR_UNSUPPORTED when it does not apply (the caller then runs launch_gemm)
-int blaslt_linear_bf16(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
-                       int64_t ldy, int64_t M, int64_t N, int64_t K, void* ws, int64_t ws_bytes);
 
 // rope.hip
 int launch_rope(hipStream_t st, int dtype, const void* q, const void* k, void* q_out, void* k_out, const float* cos_tab,

@@ -20,7 +20,6 @@
 #include <vector>
 
 #include "common.h"
-#include "decode_loop.h"
 #include "kernels.h"
 
 #ifndef MINITP_DOWN_TILE_SPLIT
@@ -37,7 +36,8 @@ namespace {
 // First kernel of every forward: publishes the per-forward values (StepState)
 // for the rest of the sequence, copies the RoPE rows of a single-token
 // forward's position next to them, and gathers the embedding rows
-// (embedding.py:44-46).
+// (embedding.py:44-46). The error word is sticky: a position outside the
+// RoPE table sets it, and only minitp_qwen2_decode_check clears it.
 template <typename T>
 __global__ void step_embed_kernel(StepState* dst, StepArgs val, const T* __restrict__ table, T* __restrict__ out,
                                   int64_t hidden, int64_t vocab, int64_t T_, const float* cos_tab,
@@ -46,7 +46,6 @@ __global__ void step_embed_kernel(StepState* dst, StepArgs val, const T* __restr
     for (int i = threadIdx.x; i < SPLIT_MAX_TUPLES; i += blockDim.x) dst->split_count[i] = 0u;
     if (threadIdx.x == 0) {
       dst->args = val;
-      dst->error = 0;
       dst->halted = val.eos_state != nullptr && val.eos_state[gridDim.x / T_] != 0;
     }
     if (T_ == 1) {
@@ -146,24 +145,10 @@ struct Qwen2Program {
   std::vector<GraphEntry> graphs;
   std::vector<GraphKey> prompt_seen;  // prompt shapes run once (recorded on the next call)
   hipStream_t capture_stream = nullptr;
-  // persistent batch-1 decode (decode_loop.hip)
-  LoopLayout loop_ll{};
-  LoopLds loop_lds{};
-  const LoopLayerW* table = nullptr;
-  const void* loop_kern = nullptr;
-  int loop_nb = 0;
-  int64_t spin_ticks = 0;
-  std::string loop_why = "not initialised";
-  int decode_path = MINITP_DECODE_AUTO;
   // bf16 prompt forwards (last-position logits) through a graph per shape;
   // direct launches when MINITP_PREFILL_GRAPH=0 is in the environment at
   // creation
   bool prefill_graphs = true;
-  uint64_t* trace = nullptr;  // persistent-decode phase trace (profiling)
-
-  // Bytes at the start of every workspace kept for the persistent decode
-  // (step counter, error words, hand-off words).
-  int64_t loop_region() const { return align256(loop_ll.bytes); }
 
   int es() const { return c.dtype == MINITP_F32 ? 4 : 2; }
   int qkv_rows() const { return (c.heads + 2 * c.kv_heads) * c.head_dim; }
@@ -173,7 +158,7 @@ struct Qwen2Program {
   Ws layout(void* base, int64_t M, int64_t B, int64_t S) const {
     Ws w{};
     char* p = (char*)base;
-    int64_t off = loop_region();
+    int64_t off = 0;
     auto take = [&](int64_t bytes) {
       char* r = p ? p + off : nullptr;
       off += align256(bytes);
@@ -208,7 +193,7 @@ struct Qwen2Program {
   // launch_gemm (logits pointer from the state), not the GEMV form (few rows)
   // or the tile kernel (M >= 256), which store to the pointer they are given.
   bool prompt_graphable(const minitp_qwen2_step& s) const {
-    if (!prefill_graphs || s.tokens <= 1 || c.dtype != MINITP_BF16 || blaslt_requested()) return false;
+    if (!prefill_graphs || s.tokens <= 1 || c.dtype != MINITP_BF16) return false;
     if (!s.logits_all) return true;
     const int64_t M = s.batch * s.tokens;
     return !fused(M) && !gemm_tile_supported(M, c.vocab, c.hidden, c.hidden, c.vocab, false);
@@ -249,24 +234,15 @@ struct Qwen2Program {
     // the tile kernel's epilogue. The residual adds go with the next RMSNorm
     // (one fused kernel, the reference's rounding order), the projections
     // that feed them writing into the normed-input buffer h, free at that
-    // point. MINITP_GEMM=blaslt runs the plain GEMMs on hipBLASLt instead
-    // (outside stream capture only): a comparison for the benchmark, not
-    // the product path.
+    // point.
     const bool blas = c.dtype == MINITP_BF16 && !fz && T > 1;
-    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
-    const bool use_blaslt = blas && blaslt_requested() && hipStreamIsCapturing(st, &cap) == hipSuccess &&
-                            cap == hipStreamCaptureStatusNone;
     // the tile GEMM's split last round: partials after the split-K region,
     // arrival words in the step state (zeroed by the embedding kernel)
     const TileTail tail{(float*)((char*)w.gemm_ws + GEMM_SPLIT_BYTES), w.split_count};
     auto lin = [&](const void* xin, int64_t ldx, const void* wt, const void* b, void* y, int64_t ldy, int64_t n,
                    int64_t k) -> int {
-      int r = use_blaslt ? blaslt_linear_bf16(st, xin, ldx, wt, b, y, ldy, M, n, k, w.gemm_ws, GEMM_WS_BYTES)
-                         : MINITP_ERR_UNSUPPORTED;
-      if (r == MINITP_ERR_UNSUPPORTED)
-        r = launch_gemm(st, c.dtype, xin, ldx, wt, b, y, ldy, M, n, k, MINITP_EPI_NONE, nullptr, nullptr, w.gemm_ws,
-                        GEMM_SPLIT_BYTES, tail);
-      return r;
+      return launch_gemm(st, c.dtype, xin, ldx, wt, b, y, ldy, M, n, k, MINITP_EPI_NONE, nullptr, nullptr, w.gemm_ws,
+                         GEMM_SPLIT_BYTES, tail);
     };
     if (blas && (rc = launch_rmsnorm(st, c.dtype, w.x, L(0, MINITP_W_LN1), w.h, M, H, c.eps))) return rc;
     // Prompt products that the split-K GEMM serves hand their partials to
@@ -274,7 +250,7 @@ struct Qwen2Program {
     // SwiGLU), which adds them up in split order: no reduction launch, and
     // the same bits as reduce-then-consume. The partials may take the whole
     // GEMM workspace (nothing else in it is live between the two launches).
-    const bool fuse_split = blas && !use_blaslt && D % 16 == 0 && H % 8 == 0 && I % 8 == 0 &&
+    const bool fuse_split = blas && D % 16 == 0 && H % 8 == 0 && I % 8 == 0 &&
                             aligned16(cos_tab) && aligned16(sin_tab);
     auto partials = [&](const void* xin, int64_t ldx, const void* wt, int64_t n, int64_t k, Partials* p) -> int {
       if (!fuse_split) return MINITP_ERR_UNSUPPORTED;
@@ -312,14 +288,14 @@ struct Qwen2Program {
           if (!rc) rc = launch_add_rmsnorm(st, c.dtype, w.x, w.h, L(l, MINITP_W_LN2), w.h, M, H, c.eps);
         }
         if (rc) return rc;
-        if (!use_blaslt && gemm_tile_supported(M, I, H, H, I, true)) {
+        if (gemm_tile_supported(M, I, H, H, I, true)) {
           if ((rc = launch_gemm_tile(st, w.h, H, L(l, MINITP_W_GATE_UP), nullptr, w.act, I, M, I, H, true, tail)))
             return rc;
         } else {
           rc = partials(w.h, H, L(l, MINITP_W_GATE_UP), 2 * I, H, &pp);
           if (rc == MINITP_OK) {
             rc = launch_silu_mul_partials(st, pp, w.act, I, I);
-          } else if (rc == MINITP_ERR_UNSUPPORTED && MINITP_GEMM_SWIGLU_EPI && !use_blaslt) {
+          } else if (rc == MINITP_ERR_UNSUPPORTED && MINITP_GEMM_SWIGLU_EPI) {
             // unsplit: SwiGLU in the GEMM's epilogue
             rc = launch_gemm_swiglu(st, c.dtype, w.h, H, L(l, MINITP_W_GATE_UP), w.act, I, M, I, H);
           }
@@ -334,7 +310,7 @@ struct Qwen2Program {
         const void* next_norm = l + 1 < c.num_layers ? L(l + 1, MINITP_W_LN1) : final_norm;
         // (a long K over too few tiles, e.g. 7B at 512 tokens: the tile kernel
         // with every tile split over K, then the residual add + norm)
-        if (MINITP_DOWN_TILE_SPLIT && !use_blaslt && gemm_tile_split_supported(M, H, I, I, H, false)) {
+        if (MINITP_DOWN_TILE_SPLIT && gemm_tile_split_supported(M, H, I, I, H, false)) {
           rc = launch_gemm_tile_split(st, w.act, I, L(l, MINITP_W_DOWN), nullptr, w.h, H, M, H, I, false, tail);
           if (!rc) rc = launch_add_rmsnorm(st, c.dtype, w.x, w.h, next_norm, w.h, M, H, c.eps);
           if (rc) return rc;
@@ -504,9 +480,8 @@ struct Qwen2Program {
     }
     if (!blas && (rc = launch_rmsnorm(st, c.dtype, w.x, final_norm, w.h, M, H, c.eps))) return rc;
     if (s.logits_all) {  // (with blas, h already holds norm(x))
-      rc = use_blaslt ? blaslt_linear_bf16(st, w.h, H, lm_head, nullptr, s.logits, V, M, V, H, w.gemm_ws, GEMM_WS_BYTES)
-                      : MINITP_ERR_UNSUPPORTED;
-      if (rc == MINITP_ERR_UNSUPPORTED && blas && gemm_tile_supported(M, V, H, H, V, false))
+      rc = MINITP_ERR_UNSUPPORTED;
+      if (blas && gemm_tile_supported(M, V, H, H, V, false))
         rc = launch_gemm_tile(st, w.h, H, lm_head, nullptr, s.logits, V, M, V, H, false, tail);
       if (rc == MINITP_ERR_UNSUPPORTED)
         rc = launch_gemm(st, c.dtype, w.h, H, lm_head, nullptr, nullptr, V, M, V, H, MINITP_EPI_NONE, nullptr, w.st);
@@ -521,105 +496,6 @@ struct Qwen2Program {
                           w.st)))
       return rc;
     if (s.next_tok) return launch_argmax(st, c.dtype, nullptr, V, B, V, nullptr, 0, w.amax_ws, w.amax_ws_bytes, w.st, 0);
-    return MINITP_OK;
-  }
-
-  // Writes the device weight table and decides whether (and with which grid
-  // and LDS layout) the persistent decode serves this model on the current
-  // device.
-  int init_loop(const minitp_qwen2_weights* w) {
-    loop_ll = loop_layout(c);
-    if (!w->device_table) {
-      loop_why = "no device table given at create";
-      return MINITP_OK;
-    }
-    const int64_t need = (int64_t)c.num_layers * (int64_t)sizeof(LoopLayerW);
-    MINITP_CHECK_ARG(w->device_table_bytes >= need && aligned16(w->device_table),
-                     "device_table: %lld B (need %lld, 16-byte aligned)", (long long)w->device_table_bytes,
-                     (long long)need);
-    std::vector<LoopLayerW> t((size_t)c.num_layers);
-    for (int l = 0; l < c.num_layers; ++l) {
-      t[l] = LoopLayerW{L(l, MINITP_W_LN1),     L(l, MINITP_W_LN2), L(l, MINITP_W_QKV), L(l, MINITP_W_QKV_BIAS),
-                        L(l, MINITP_W_O),       L(l, MINITP_W_GATE_UP), L(l, MINITP_W_DOWN), nullptr};
-    }
-    MINITP_RETURN_HIP(hipMemcpy(w->device_table, t.data(), (size_t)need, hipMemcpyHostToDevice));
-    table = (const LoopLayerW*)w->device_table;
-    int dev = 0, cus = 0, khz = 0;
-    MINITP_RETURN_HIP(hipGetDevice(&dev));
-    MINITP_RETURN_HIP(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
-    MINITP_RETURN_HIP(hipDeviceGetAttribute(&khz, hipDeviceAttributeWallClockRate, dev));
-    loop_nb = std::min(cus, LOOP_MAX_BLOCKS);
-    if (const char* why = loop_unsupported(c, loop_nb, &loop_lds)) {
-      loop_why = why;
-      return MINITP_OK;
-    }
-    loop_kern = loop_kernel(c.dtype, c.head_dim);
-    if (!loop_kern) {
-      loop_why = "no kernel instantiated for this dtype / head_dim";
-      return MINITP_OK;
-    }
-    int rc = ensure_lds_limit(loop_kern, loop_lds.bytes);
-    if (rc) return rc;
-    int occ = 0;
-    MINITP_RETURN_HIP(hipOccupancyMaxActiveBlocksPerMultiprocessor(&occ, loop_kern, LOOP_THREADS, loop_lds.bytes));
-    if (occ < 1) {
-      loop_why = "persistent kernel does not fit one block per CU";
-      return MINITP_OK;
-    }
-    spin_ticks = (int64_t)khz * 1000 * 2;  // a wait may last 2 s
-    loop_why.clear();
-    return MINITP_OK;
-  }
-
-  // One batch-1 decode step as one persistent launch (decode_loop.hip).
-  int run_loop(hipStream_t st, const minitp_qwen2_step& s) {
-    LoopParams a{};
-    a.L = c.num_layers;
-    a.H = c.hidden;
-    a.Hq = c.heads;
-    a.Hkv = c.kv_heads;
-    a.G = c.heads / c.kv_heads;
-    a.I = c.intermediate;
-    a.V = c.vocab;
-    a.eps = c.eps;
-    a.scale = 1.0f / sqrtf((float)c.head_dim);  // SDPA default (attention.py:92)
-    a.S = s.max_seq;
-    a.max_pos = c.max_pos;
-    a.embed = embed;
-    a.lm_head = lm_head;
-    a.final_norm = final_norm;
-    a.cos_tab = cos_tab;
-    a.sin_tab = sin_tab;
-    a.layers = table;
-    a.ids = s.ids;
-    a.positions = s.positions;
-    a.cache_len = s.cache_len;
-    a.k_cache = s.k_cache;
-    a.v_cache = s.v_cache;
-    a.logits = s.logits;
-    a.next_tok = s.next_tok;
-    a.ctrl = (uint32_t*)s.workspace;
-    a.ll = (uint64_t*)((char*)s.workspace + LOOP_CTRL_BYTES);
-    a.ll_layer_words = loop_ll.layer_words;
-    a.off_qkv = loop_ll.off_qkv;
-    a.off_p = loop_ll.off_p;
-    a.off_act = loop_ll.off_act;
-    a.off_down = loop_ll.off_down;
-    a.off_lm = loop_ll.off_lm;
-    a.lds_xs = loop_lds.xs;
-    a.lds_xin = loop_lds.xin;
-    a.lds_stage = loop_lds.stage;
-    a.lds_qstage = loop_lds.qstage;
-    a.lds_rowres = loop_lds.rowres;
-    a.lds_norm = loop_lds.norm;
-    a.lds_tile = loop_lds.tile;
-    a.lds_misc = loop_lds.misc;
-    a.spin_limit = spin_ticks;
-    loop_roles(c, loop_nb, a.role);
-    a.trace = trace;
-    a.trace_slots = loop_trace_slots(c.num_layers);
-    void* args[] = {&a};
-    MINITP_RETURN_HIP(hipLaunchKernel(loop_kern, dim3(loop_nb), dim3(LOOP_THREADS), args, loop_lds.bytes, st));
     return MINITP_OK;
   }
 
@@ -800,67 +676,23 @@ int minitp_qwen2_create(const minitp_qwen2_config* cfg, const minitp_qwen2_weigh
   p->cos_tab = w->rope_cos;
   p->sin_tab = w->rope_sin;
   p->lw.assign(w->layers, w->layers + (size_t)c.num_layers * MINITP_W_PER_LAYER);
-  const int rc = p->init_loop(w);
-  if (rc) {
-    delete p;
-    return rc;
-  }
   *handle = p;
   return MINITP_OK;
-}
-
-int64_t minitp_qwen2_table_bytes(const minitp_qwen2_config* cfg) {
-  if (!cfg || cfg->num_layers < 1) return -1;
-  return (int64_t)cfg->num_layers * (int64_t)sizeof(minitp::LoopLayerW);
-}
-
-int minitp_qwen2_set_decode_path(void* handle, int path) {
-  MINITP_CHECK_ARG(handle != nullptr, "NULL handle");
-  MINITP_CHECK_ARG(path == MINITP_DECODE_AUTO || path == MINITP_DECODE_GRAPH || path == MINITP_DECODE_PERSISTENT,
-                   "decode path %d", path);
-  ((Qwen2Program*)handle)->decode_path = path;
-  return MINITP_OK;
-}
-
-int64_t minitp_qwen2_trace_bytes(void* handle) {
-  if (!handle) return -1;
-  auto* p = (Qwen2Program*)handle;
-  return (int64_t)minitp::LOOP_MAX_BLOCKS * minitp::loop_trace_slots(p->c.num_layers) * (minitp::LOOP_THREADS / 64) * 8;
-}
-
-int minitp_qwen2_set_trace(void* handle, void* trace, int64_t bytes) {
-  MINITP_CHECK_ARG(handle != nullptr, "NULL handle");
-  auto* p = (Qwen2Program*)handle;
-  MINITP_CHECK_ARG(trace == nullptr || bytes >= minitp_qwen2_trace_bytes(handle), "trace buffer too small");
-  p->trace = (uint64_t*)trace;
-  return MINITP_OK;
-}
-
-int minitp_qwen2_persistent_ok(void* handle) {
-  if (!handle) return 0;
-  auto* p = (Qwen2Program*)handle;
-  if (!p->loop_why.empty()) {
-    minitp::set_error("persistent decode unavailable: %s", p->loop_why.c_str());
-    return 0;
-  }
-  return 1;
 }
 
 int minitp_qwen2_decode_check(void* handle, void* stream, void* workspace) {
   MINITP_CHECK_ARG(handle != nullptr && workspace != nullptr, "NULL argument");
   MINITP_RETURN_HIP(hipStreamSynchronize((hipStream_t)stream));
-  uint32_t ctrl[4] = {0, 0, 0, 0};
-  MINITP_RETURN_HIP(hipMemcpy(ctrl, workspace, sizeof(ctrl), hipMemcpyDeviceToHost));
-  if (ctrl[minitp::LOOP_CTRL_ERROR] == 0 && ctrl[minitp::LOOP_CTRL_ABORT] == 0) return MINITP_OK;
-  const uint32_t err = ctrl[minitp::LOOP_CTRL_ERROR];
-  // clear the record (error and abort words; the step counter stays)
-  MINITP_RETURN_HIP(hipMemset((char*)workspace + 4 * minitp::LOOP_CTRL_ERROR, 0, 8));
-  if (err & minitp::LOOP_ERR_TIMEOUT || !(err & minitp::LOOP_ERR_POSITION)) {
-    minitp::set_error("persistent decode: a hand-off wait timed out (error bits 0x%x); the step's outputs are invalid",
-                      err);
-    return MINITP_ERR_HIP;
-  }
-  minitp::set_error("persistent decode: position outside the RoPE table");
+  // the step state sits at the start of every workspace (layout())
+  auto* state = (minitp::StepState*)workspace;
+  int32_t err = 0;
+  MINITP_RETURN_HIP(hipMemcpy(&err, &state->error, sizeof(err), hipMemcpyDeviceToHost));
+  if (err == 0) return MINITP_OK;
+  const int32_t zero = 0;
+  MINITP_RETURN_HIP(hipMemcpy(&state->error, &zero, sizeof(zero), hipMemcpyHostToDevice));
+  minitp::set_error("position out of range for the RoPE table of %d rows (a forward on this workspace ran with NaN "
+                    "rotary rows)",
+                    ((Qwen2Program*)handle)->c.max_pos);
   return MINITP_ERR_RANGE;
 }
 
@@ -896,18 +728,7 @@ int minitp_qwen2_decode(void* handle, void* stream, const minitp_qwen2_step* ste
   minitp::Ws w;
   int rc = p->check_step(step, w);
   if (rc) return rc;
-  hipStream_t st = (hipStream_t)stream;
-  // AUTO takes the graph: it is the faster path at every measured shape. The
-  // persistent kernel has no end-of-sequence update, so early stop replays
-  // the graph whatever path is selected.
-  if (p->decode_path == MINITP_DECODE_PERSISTENT && step->eos_state == nullptr) {
-    if (!p->loop_why.empty() || step->batch != 1) {
-      minitp::set_error("persistent decode unavailable: %s", step->batch != 1 ? "batch != 1" : p->loop_why.c_str());
-      return MINITP_ERR_UNSUPPORTED;
-    }
-    return p->run_loop(st, *step);
-  }
-  return minitp::run_graphed(p, st, *step, w);
+  return minitp::run_graphed(p, (hipStream_t)stream, *step, w);
 }
 
 }  // extern "C"

@@ -61,15 +61,8 @@ SIGNATURES = {
     "minitp_qwen2_workspace_bytes": (_i64, [_vp, _i64, _i64, _i64]),
     "minitp_qwen2_forward": (_int, [_vp, _vp, _vp]),
     "minitp_qwen2_decode": (_int, [_vp, _vp, _vp]),
-    "minitp_qwen2_table_bytes": (_i64, [_vp]),
-    "minitp_qwen2_set_decode_path": (_int, [_vp, _int]),
-    "minitp_qwen2_persistent_ok": (_int, [_vp]),
     "minitp_qwen2_decode_check": (_int, [_vp, _vp, _vp]),
-    "minitp_qwen2_trace_bytes": (_i64, [_vp]),
-    "minitp_qwen2_set_trace": (_int, [_vp, _vp, _i64]),
 }
-
-DECODE_AUTO, DECODE_GRAPH, DECODE_PERSISTENT = 0, 1, 2
 
 
 class Qwen2Config(ctypes.Structure):
@@ -79,7 +72,7 @@ class Qwen2Config(ctypes.Structure):
 
 class Qwen2Weights(ctypes.Structure):
     _fields_ = [("embed", _vp), ("lm_head", _vp), ("final_norm", _vp), ("rope_cos", _vp), ("rope_sin", _vp),
-                ("layers", ctypes.POINTER(_vp)), ("device_table", _vp), ("device_table_bytes", _i64)]
+                ("layers", ctypes.POINTER(_vp))]
 
 
 class Qwen2Step(ctypes.Structure):

@@ -84,13 +84,9 @@ class _Program:
                           cfg.head_dim, model.model.layers[0].mlp.intermediate_local, cfg.vocab_size,
                           model.rotary.max_seq_len, cfg.rms_norm_eps)
         arr = (ctypes.c_void_p * len(params))(*[p.data_ptr() for p in params])
-        # device memory for the persistent decode's per-layer weight table
-        nbytes = lib.minitp_qwen2_table_bytes(ctypes.byref(c))
-        self.table = torch.zeros(max(int(nbytes), 16), dtype=torch.uint8, device=head[0].device)
         w = N.Qwen2Weights(head[0].data_ptr(), head[1].data_ptr(), head[2].data_ptr(),
                            model.rotary.cos_cache.data_ptr(), model.rotary.sin_cache.data_ptr(),
-                           ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p)), self.table.data_ptr(),
-                           self.table.numel())
+                           ctypes.cast(arr, ctypes.POINTER(ctypes.c_void_p)))
         h = ctypes.c_void_p()
         N.check(lib.minitp_qwen2_create(ctypes.byref(c), ctypes.byref(w), ctypes.byref(h)), "qwen2_create")
         self.handle = h
@@ -100,21 +96,8 @@ class _Program:
         self.fwd_ws: torch.Tensor | None = None
         self.decode_ws: dict[tuple[int, int], torch.Tensor] = {}
 
-    def set_decode_path(self, path: int) -> None:
-        """N.DECODE_AUTO (the graph of per-op kernels),
-        N.DECODE_GRAPH or N.DECODE_PERSISTENT."""
-        N.check(N.lib().minitp_qwen2_set_decode_path(self.handle, path), "qwen2_set_decode_path")
-        self.decode_path = path
-
-    def persistent_ok(self) -> bool:
-        return bool(N.lib().minitp_qwen2_persistent_ok(self.handle))
-
     def decode_path_name(self, batch: int = 1) -> str:
-        """Which decode form serves a step of `batch` rows."""
-        persistent = getattr(self, "decode_path", N.DECODE_AUTO) == N.DECODE_PERSISTENT
-        if persistent and batch == 1 and self.persistent_ok():
-            return ("persistent: one launch per token, one block per CU, blocks exchange each layer's results "
-                    "through epoch-tagged words in HBM")
+        """The decode form that serves a step of `batch` rows."""
         return ("one hipGraph replay per token: embedding; per layer norm+QKV+RoPE+KV write, attention, "
                 "o_proj+residual, norm+gate/up+SwiGLU, down+residual; norm+LM head+argmax partials, merge")
 
@@ -130,9 +113,10 @@ class _Program:
                                  f"need a contiguous {want} {self.dtype} cache on {self.device}")
 
     def check_decode(self) -> None:
-        """Synchronise and raise if a persistent decode step on any of this
-        program's decode workspaces recorded a failure."""
-        for ws in self.decode_ws.values():
+        """Synchronise and raise IndexError if a forward on any of this
+        program's workspaces ran at a position outside the RoPE table (the
+        sticky error word of the step state; cleared by the check)."""
+        for ws in list(self.decode_ws.values()) + ([self.fwd_ws] if self.fwd_ws is not None else []):
             N.check(N.lib().minitp_qwen2_decode_check(self.handle, N.stream(), ws.data_ptr()), "qwen2_decode")
 
     def valid_for(self, model: "TPQwen2ForCausalLM") -> bool:

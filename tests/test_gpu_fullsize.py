@@ -178,21 +178,16 @@ def _teacher_forced(model, prompt, start, check):
     assert st.kv.seq_len == t
 
 
-@pytest.mark.parametrize("path", ["graph", "persistent"])
-def test_7b_every_decode_context_equals_whole_prompt(path):
+def test_7b_every_decode_context_equals_whole_prompt():
     """7B shapes (2 layers, batch 1): the whole 768-token prompt's logits at
     each position 511 .. 767 against prefill(512) plus 256 teacher-forced
     decode steps (contexts 513 .. 768: the generation's 255 steps plus one)."""
-    from minitp import _native as N
     from minitp import synthetic
     from minitp.generation import GenerationState
 
     cfg = dataclasses.replace(synthetic.QWEN7B, num_hidden_layers=2)
     model = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device=DEV, seed=2)
     prog = model.program()
-    prog.set_decode_path(N.DECODE_PERSISTENT if path == "persistent" else N.DECODE_GRAPH)
-    if path == "persistent" and not prog.persistent_ok():
-        pytest.skip(f"persistent decode not available for this shape: {N.last_error()}")
     prompt = synthetic.synthetic_prompt(cfg.vocab_size, 1, 768, seed=7, device=DEV)
     whole = GenerationState(model, prompt, 1, prefill_logits="all").prefill()[0].float()
     assert whole.shape == (768, cfg.vocab_size) and torch.isfinite(whole).all()
@@ -206,7 +201,7 @@ def test_7b_every_decode_context_equals_whole_prompt(path):
         _teacher_forced(model, prompt, 512, check)
     prog.check_decode()
     worst = max(errs, key=errs.get)
-    print(f"7B {path}: {len(errs)} positions, max |logit diff| {errs[worst]:.4f} at position {worst}")
+    print(f"7B: {len(errs)} positions, max |logit diff| {errs[worst]:.4f} at position {worst}")
     assert len(errs) == 257 and errs[worst] <= BF16_LOGIT_ATOL
 
 

@@ -122,24 +122,11 @@ def test_synthetic_tiny_equals_state_dict_copy():
         assert ka == kb and torch.equal(va, vb), ka
 
 
-def _set_path(model, path):
-    """Decode path of the model's program: "graph" (the default's per-op
-    kernels) or "persistent" (the opt-in one-launch decode)."""
-    from minitp import _native as N
-
-    prog = model.program()
-    prog.set_decode_path(N.DECODE_PERSISTENT if path == "persistent" else N.DECODE_GRAPH)
-    if path == "persistent":
-        assert prog.persistent_ok(), N.last_error()
-
-
-@pytest.mark.parametrize("path", ["graph", "persistent"])
-def test_q05b_fp32_256_greedy_ids_bitexact(path):
+def test_q05b_fp32_256_greedy_ids_bitexact():
     from minitp.generation import generate_greedy
 
     fx = _fixture("q05b_fp32")
     model = _synthetic("QWEN05B", torch.float32)
-    _set_path(model, path)
     prompt = torch.from_numpy(fx["prompt"]).to(DEV)
     n = fx["ids"].shape[1] - prompt.shape[1]
     ids = generate_greedy(model, prompt, n, early_stop=False).cpu().numpy()
@@ -151,14 +138,12 @@ def test_q05b_fp32_256_greedy_ids_bitexact(path):
     pre = prefill[:, torch.from_numpy(fx["prefill_positions"])].transpose(0, 1)
     err_p = _check_summaries(pre, fx, "prefill", FP32_LOGIT_ATOL)
     model.program().check_decode()
-    print(f"q05b fp32 {path}: 256/256 ids exact; max logit err decode {err:.2e} prefill {err_p:.2e}")
+    print(f"q05b fp32: 256/256 ids exact; max logit err decode {err:.2e} prefill {err_p:.2e}")
 
 
-@pytest.mark.parametrize("path", ["graph", "persistent"])
-def test_q05b_bf16_logits_teacher_forced(path):
+def test_q05b_bf16_logits_teacher_forced():
     fx = _fixture("q05b_bf16")
     model = _synthetic("QWEN05B", torch.bfloat16)
-    _set_path(model, path)
     prompt = torch.from_numpy(fx["prompt"]).to(DEV)
     n = fx["ids"].shape[1] - prompt.shape[1]
     rows, prefill = _teacher_forced_rows(model, prompt, torch.from_numpy(fx["ids"]), n)
@@ -171,7 +156,7 @@ def test_q05b_bf16_logits_teacher_forced(path):
     clear = fx["step_margin"][:, 0] > 0.1
     assert np.array_equal(picks[clear], ref[clear])
     model.program().check_decode()
-    print(f"q05b bf16 {path}: max logit err decode {err:.3f} prefill {err_p:.3f}")
+    print(f"q05b bf16: max logit err decode {err:.3f} prefill {err_p:.3f}")
 
 
 # ---------------------------------------------------------------------------
@@ -185,11 +170,9 @@ def _tiny(dtype=torch.float32):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_graph_decode_equals_direct_forward(dtype):
-    from minitp import _native as N
     from minitp.generation import GenerationState, make_kv_cache
 
-    model = _tiny(dtype)
-    model.program().set_decode_path(N.DECODE_GRAPH)  # the graph replays the direct launch sequence
+    model = _tiny(dtype)  # the decode graph replays the direct launch sequence
     prompt = torch.tensor([[3, 17, 256, 999, 41]], device=DEV)
     st = GenerationState(model, prompt, 6)
     kv = make_kv_cache(model, 1, 11)
@@ -202,70 +185,6 @@ def test_graph_decode_equals_direct_forward(dtype):
         logits = st.decode_step(tok, pos)
         d = model(tok.unsqueeze(-1), positions=pos.reshape(1), kv_cache=kv)
         assert torch.equal(logits, d)
-
-
-def _decode_rows(model, prompt, ref_ids, n_steps, path):
-    from minitp import _native as N
-
-    model.program().set_decode_path(path)
-    try:
-        rows, _ = _teacher_forced_rows(model, prompt, ref_ids, n_steps)
-        model.program().check_decode()
-    finally:
-        model.program().set_decode_path(N.DECODE_AUTO)
-    return rows
-
-
-@pytest.mark.parametrize("shape_name", ["TINY", "QWEN05B"])
-@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-def test_persistent_decode_matches_graph_decode(shape_name, dtype):
-    """The one-launch persistent decode and the graph of per-op kernels run
-    the same math with different summation orders: teacher-forced logits
-    agree to fp32 rounding (fp32) or within a few bf16 steps (bf16), and the
-    greedy picks agree wherever the top-2 margin is clear."""
-    from minitp import _native as N
-    from minitp.generation import generate_greedy
-
-    model = _synthetic(shape_name, dtype)
-    assert model.program().persistent_ok(), N.last_error()
-    v = model.cfg.vocab_size
-    prompt = torch.randint(0, v, (1, 16), generator=torch.Generator().manual_seed(5)).to(DEV)
-    model.program().set_decode_path(N.DECODE_PERSISTENT)
-    try:
-        ids = generate_greedy(model, prompt, 40, early_stop=False)
-        model.program().check_decode()
-    finally:
-        model.program().set_decode_path(N.DECODE_AUTO)
-    rp = _decode_rows(model, prompt, ids.cpu(), 40, N.DECODE_PERSISTENT)
-    rg = _decode_rows(model, prompt, ids.cpu(), 40, N.DECODE_GRAPH)
-    atol = 2e-4 if dtype == torch.float32 else 0.25
-    err = (rp - rg).abs().max().item()
-    assert err <= atol, err
-    top2 = rg.topk(2, dim=-1).values
-    clear = (top2[..., 0] - top2[..., 1]) > 2 * atol
-    assert torch.equal(rp.argmax(-1)[clear], rg.argmax(-1)[clear])
-    # the persistent path is what generate_greedy ran: its ids follow its own logits
-    assert torch.equal(rp.argmax(-1)[1:, 0].cpu(), ids[0, 17:].cpu())
-    print(f"{shape_name} {dtype}: persistent vs graph max logit diff {err:.3e}")
-
-
-def test_persistent_decode_steps_with_cursor_and_epochs():
-    """Many steps on one workspace (the step counter advances every launch)
-    and a fresh GenerationState reusing the program's workspace: the ids of
-    two identical generations match and no wait timed out."""
-    from minitp import _native as N
-    from minitp.generation import generate_greedy
-
-    model = _synthetic("TINY", torch.bfloat16)
-    prompt = torch.tensor([[5, 6, 7]], device=DEV)
-    model.program().set_decode_path(N.DECODE_PERSISTENT)
-    try:
-        a = generate_greedy(model, prompt, 60, early_stop=False)
-        b = generate_greedy(model, prompt, 60, early_stop=False)
-        model.program().check_decode()
-    finally:
-        model.program().set_decode_path(N.DECODE_AUTO)
-    assert torch.equal(a, b)
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])

@@ -168,7 +168,7 @@ def test_abi_validation_paths_return_status_without_gpu_work():
     from minitp import _native as N
 
     lib = N.lib()
-    assert lib.minitp_abi_version() == 4
+    assert lib.minitp_abi_version() == 5
     assert lib.minitp_status_string(N.ERR_OVERFLOW) == b"KV cache overflow"
     # K not a multiple of 8 bf16 elements: rejected before any launch
     st = lib.minitp_linear(None, N.BF16, 16, 12, 16, None, 16, 4, 1, 4, 12, N.EPI_NONE, None)
