@@ -108,6 +108,19 @@ int minitp_rmsnorm_linear(void* stream, int dtype, const void* x, int64_t ldx, c
                           float eps, const void* w, const void* bias, void* y, int64_t ldy, int64_t M,
                           int64_t N, int64_t K, int epilogue, const void* aux);
 
+/* The decoder layer's residual add, post_attention_layernorm and gate_up_proj
+ * with SwiGLU for one row (layer.py:63-67, mlp.py:34-38), where the o_proj
+ * product arrives as nparts fp32 partial rows over disjoint parts of its K
+ * (the per-head partials of the batch-1 decode attention, which folds o_proj
+ * in): x_out = dtype(x + dtype(parts[0] + parts[1] + ... in row order)), then
+ * y = silu(gate) * up of RMSNorm(x_out) W^T as minitp_rmsnorm_linear.
+ * x, x_out: [K]; parts: [nparts, K] fp32; W: [2N, K]; y: [N]. epilogue must be
+ * MINITP_EPI_SWIGLU; K <= 1024, 1 <= nparts <= 16, else
+ * MINITP_ERR_UNSUPPORTED. */
+int minitp_add_rmsnorm_linear_parts(void* stream, int dtype, const void* x, const float* parts, int32_t nparts,
+                                    void* x_out, const void* norm_w, float eps, const void* w, void* y,
+                                    int64_t N, int64_t K, int epilogue);
+
 /* ---- rotary embedding and KV cache -------------------------------------- */
 /* RotaryEmbedding.apply (rope.py:47-64): q [B, Hq, T, D] and k [B, Hkv, T, D]
  * (contiguous) rotated by rows positions[t] of the fp32 tables [max_pos, D];

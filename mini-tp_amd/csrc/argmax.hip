@@ -35,7 +35,9 @@ __global__ __launch_bounds__(256) void argmax_slice_kernel(const T* logits, int6
   const int64_t start = (int64_t)blockIdx.x * SLICE, end = std::min<int64_t>(V, start + SLICE);
   if ((((uint64_t)lr) & 15) == 0 && V * (int64_t)sizeof(T) < (1LL << 31)) {
     // 16 consecutive elements per thread, every 16-byte load issued before
-    // the first comparison (past the row's end: zeros, dropped by index)
+    // the first comparison. Only whole vectors inside the row are loaded
+    // that way (the others read zeros and are dropped by index); a vector
+    // that straddles the row's end is read element by element below.
     constexpr int VE = 16 / (int)sizeof(T), NV = 16 / VE;
     const __amdgpu_buffer_rsrc_t r = span_rsrc(lr, (uint32_t)(V * (int64_t)sizeof(T)));
     const int64_t j0 = start + 16 * tid;
@@ -44,8 +46,22 @@ __global__ __launch_bounds__(256) void argmax_slice_kernel(const T* logits, int6
     for (int u = 0; u < NV; ++u) {
       const int64_t j = j0 + u * VE;
       const u32x4 w = __builtin_bit_cast(
-          u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, j < end ? (uint32_t)(j * (int64_t)sizeof(T)) : 0xffffffffu, 0, 0));
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                     r, j + VE <= end ? (uint32_t)(j * (int64_t)sizeof(T)) : 0xffffffffu, 0, 0));
       raw[u] = make_uint4(w.x, w.y, w.z, w.w);
+    }
+#pragma unroll
+    for (int u = 0; u < NV; ++u) {
+      const int64_t j = j0 + u * VE;
+      if (j < end && j + VE > end) {  // the straddling vector: its elements one by one
+        for (int64_t e = j; e < end; ++e) {
+          const float x = load_f32<T>(lr, e);
+          if (argmax_better(x, e, v, i)) {
+            v = x;
+            i = e;
+          }
+        }
+      }
     }
 #pragma unroll
     for (int u = 0; u < NV; ++u) {
@@ -58,7 +74,7 @@ __global__ __launch_bounds__(256) void argmax_slice_kernel(const T* logits, int6
           x = bf16_to_f32((uint16_t)(wd[e / 2] >> (16 * (e % 2))));
         else
           x = __builtin_bit_cast(float, wd[e]);
-        if (j < end && argmax_better(x, j, v, i)) {
+        if (j0 + u * VE + VE <= end && argmax_better(x, j, v, i)) {
           v = x;
           i = j;
         }

@@ -49,7 +49,14 @@ struct DecodeArgs {
   // (the forward's step state holds them): when set, the MFMA kernel's last
   // split block of a unit merges the splits itself (no merge launch).
   uint32_t* count;
+  OprojArgs op;  // decode_attn_kernel<..., NLW > 0>: the folded o_proj
 };
+
+// 16-byte load of streamed weights (read once per step: non-temporal).
+__device__ __forceinline__ uint4 weight_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
+  return make_uint4(v.x, v.y, v.z, v.w);
+}
 
 // Value held by lane j ^ (2 * MK - 1) (rows of 16 lanes, DPP). Used for a
 // reduce-scatter whose masks fall from high to low: the bits above MK are
@@ -164,7 +171,15 @@ __device__ __forceinline__ void wave_lds_sync() {
 // holds back from wave-private LDS for P V. A wave's VALU work per chunk
 // grows with HP: small batches run HP = 1 (more blocks, K/V re-read from
 // L2 per head), large ones the whole group (K/V read once).
-template <typename T, int D, int HP>
+//
+// NLW > 0 folds o_proj in (one batch row, HP = 1, one split; gridDim.y is
+// the number of W_o row slices): every block loads its slice of W_o (rows
+// blockIdx.y * rows .., the D columns of its head; NLW 16-byte loads per
+// thread) before the attention, rounds the head's output to the dtype (the
+// SDPA output, attention.py:92-105) and writes o . W_o[row, head columns] as
+// fp32 partial rows part[head][row]. Each row's D-element dot is one chunk
+// per lane (a fixed fmaf chain) plus a butterfly over the row's lanes.
+template <typename T, int D, int HP, int NLW = 0>
 __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(DecodeArgs a) {
   using Geo = DecodeGeom<D>;
   constexpr int LPR = Geo::LPR, PPI = Geo::PPI, NI = Geo::NI, CP = Geo::CP, DUP = Geo::DUP;
@@ -178,7 +193,7 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(DecodeArgs a) {
   const AttnShape& s = a.s;
   const int G = s.Hq / s.Hkv;
   const int bh = blockIdx.x, b = bh / s.Hkv, g = bh % s.Hkv;
-  const int split = blockIdx.y, nsplit = gridDim.y;
+  const int split = NLW > 0 ? 0 : (int)blockIdx.y, nsplit = NLW > 0 ? 1 : (int)gridDim.y;
   const int h0 = blockIdx.z * HP;  // first query head (within the group) of this block
   const int nh = std::min(HP, G - h0);
   const int64_t ctx = (a.st ? a.st->args.cache_len : a.cache_len) + 1;
@@ -192,11 +207,51 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(DecodeArgs a) {
   const T* kc = (const T*)(a.st ? a.st->args.k_cache : a.k) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
   const T* vc = (const T*)(a.st ? a.st->args.v_cache : a.v) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
 
+  // The context's K / V rows through resources that end at row ctx (rows past
+  // it read zeros, so the loads are unconditional), and this wave's first
+  // chunk requested before the query: its addresses do not depend on the
+  // query, so the two memory round trips overlap.
+  const uint32_t kv_bytes = (uint32_t)(ctx * D * (int64_t)sizeof(T));
+  const __amdgpu_buffer_rsrc_t krs = span_rsrc(kc, kv_bytes), vrs = span_rsrc(vc, kv_bytes);
+  uint4 kr[NI][U], vr[NI][U];
+  auto load_chunk = [&](int64_t c) {
+#pragma unroll
+    for (int r = 0; r < NI; ++r) {
+      const uint32_t off = (uint32_t)(((c * CP + r * PPI + grow) * D + col * 8) * (int64_t)sizeof(T));
+#pragma unroll
+      for (int u = 0; u < U; ++u) {
+        kr[r][u] = attn_load16(krs, off + 16 * u);
+        vr[r][u] = attn_load16(vrs, off + 16 * u);
+      }
+    }
+  };
+  const int64_t c_first = (int64_t)w * nsplit + split;
+  load_chunk(c_first);
+
   {
     const T* q = (const T*)a.q + ((int64_t)b * s.Hq + (int64_t)g * G + h0) * D;
     for (int i = tid; i < HP * D; i += NW * 64) (&qs[0][0])[i] = i < nh * D ? q[i] : T{};
   }
   __syncthreads();
+
+  // (NLW > 0) this block's W_o slice, in flight during the attention
+  constexpr int OV = Vec<T>::N, CPR = D / OV;  // elements per load; loads per row segment
+  static_assert(NLW == 0 || (HP == 1 && CPR >= 1 && CPR <= 64 && (64 % CPR) == 0), "o_proj slice layout");
+  uint4 wo[NLW > 0 ? NLW : 1];
+  int64_t orow0 = 0, onrows = 0;
+  if constexpr (NLW > 0) {
+    const int hq = g * G + h0;
+    orow0 = (int64_t)blockIdx.y * a.op.rows;
+    onrows = std::min<int64_t>(a.op.rows, a.op.H - orow0);
+    const int64_t ldw = (int64_t)s.Hq * D;
+    const __amdgpu_buffer_rsrc_t wr =
+        span_rsrc((const T*)a.op.w + orow0 * ldw + (int64_t)hq * D, (uint32_t)(onrows * ldw * sizeof(T)));
+#pragma unroll
+    for (int i = 0; i < NLW; ++i) {
+      const int f = tid + i * NW * 64;
+      wo[i] = weight_load16(wr, (uint32_t)(((int64_t)(f / CPR) * ldw + (f % CPR) * OV) * sizeof(T)));
+    }
+  }
 
   float m[HP], lsum[HP], acc[NA];
 #pragma unroll
@@ -207,21 +262,9 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(DecodeArgs a) {
 #pragma unroll
   for (int i = 0; i < NA; ++i) acc[i] = 0.f;
 
-  for (int64_t c = (int64_t)w * nsplit + split; c < nchunk; c += (int64_t)NW * nsplit) {
+  for (int64_t c = c_first; c < nchunk; c += (int64_t)NW * nsplit) {
     const int64_t p0 = c * CP;
-    uint4 kr[NI][U], vr[NI][U];
-#pragma unroll
-    for (int r = 0; r < NI; ++r) {
-      const int64_t pos = p0 + r * PPI + grow;
-      const bool ok = pos < ctx;
-      const uint4* kp = reinterpret_cast<const uint4*>(kc + pos * D + col * 8);
-      const uint4* vp = reinterpret_cast<const uint4*>(vc + pos * D + col * 8);
-#pragma unroll
-      for (int u = 0; u < U; ++u) {
-        kr[r][u] = ok ? kp[u] : make_uint4(0, 0, 0, 0);
-        vr[r][u] = ok ? vp[u] : make_uint4(0, 0, 0, 0);
-      }
-    }
+    if (c != c_first) load_chunk(c);
     // scores of this lane's 8-element slices, summed across each row
     float sc[8][HP];
 #pragma unroll
@@ -311,7 +354,9 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(DecodeArgs a) {
         o = fmaf(sc, po[j][h][d], o);
       }
     }
-    if (nsplit == 1) {
+    if constexpr (NLW > 0) {
+      po[0][0][d] = round_to<T>(o / l);  // (element d is read and written by this thread only)
+    } else if (nsplit == 1) {
       store_f32<T>(out, ((int64_t)b * s.Hq + g * G + h0 + h) * D + d, o / l);
     } else {
       const int64_t slot = ((int64_t)bh * nsplit + split) * GMAX + h0 + h;
@@ -320,6 +365,24 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(DecodeArgs a) {
         a.ws_ml[slot * 2] = mx;
         a.ws_ml[slot * 2 + 1] = l;
       }
+    }
+  }
+
+  // ---- (NLW > 0) o_proj partial of this head over the block's rows -------------
+  if constexpr (NLW > 0) {
+    __syncthreads();
+    float* part = a.op.part + (int64_t)(g * G + h0) * a.op.H + orow0;
+#pragma unroll
+    for (int i = 0; i < NLW; ++i) {
+      const int f = tid + i * NW * 64, row = f / CPR, c = f % CPR;
+      float wf[OV];
+      unpack16(wo[i], wf, (T*)nullptr);
+      float acc = 0.f;
+#pragma unroll
+      for (int e = 0; e < OV; ++e) acc = fmaf(wf[e], po[0][0][c * OV + e], acc);
+#pragma unroll
+      for (int o = CPR / 2; o >= 1; o >>= 1) acc += __shfl_xor(acc, o, 64);
+      if (c == 0 && row < onrows) part[row] = acc;
     }
   }
 }
@@ -1319,6 +1382,10 @@ int launch_decode_attention(hipStream_t st, int dtype, const void* q, const void
     set_error("attention: Hq=%d Hkv=%d (group must divide and be <= %d)", s.Hq, s.Hkv, GMAX);
     return MINITP_ERR_UNSUPPORTED;
   }
+  if (s.S * s.D * (dtype == MINITP_F32 ? 4 : 2) >= (1LL << 32)) {
+    set_error("attention: a (row, KV head) cache of %lld x %d exceeds 4 GiB", (long long)s.S, s.D);
+    return MINITP_ERR_UNSUPPORTED;
+  }
   const int64_t need = attention_workspace_bytes(s.B, 1, s.Hq, s.Hkv, s.D, s.S);
   if (workspace_bytes < need || workspace == nullptr) {
     set_error("attention: workspace %lld B < %lld B", (long long)workspace_bytes, (long long)need);
@@ -1368,6 +1435,90 @@ int launch_decode_attention(hipStream_t st, int dtype, const void* q, const void
     return MINITP_OK;
   }
   return dtype == MINITP_F32 ? decode_by_d<float>(st, a, nsplit) : decode_by_d<bf16>(st, a, nsplit);
+}
+
+// The folded o_proj: one batch row, one KV group per block row of heads,
+// head dims with whole 16-byte chunks, and a W_o slice of at most 16 loads
+// per thread in at most OPROJ_MAX_SLICES slices (more would re-run each
+// head's attention too often).
+constexpr int OPROJ_MAX_SLICES = 16;
+constexpr int OPROJ_MAX_NLW = 16;
+
+int attn_oproj_rows(int dtype, const AttnShape& s, int64_t H, int slices) {
+  const int es = dtype == MINITP_F32 ? 4 : 2;
+  const int64_t cpr = (int64_t)s.D * es / 16;  // loads per row segment
+  const int64_t per_block = (int64_t)OPROJ_MAX_NLW * NW * 64 / std::max<int64_t>(cpr, 1);
+  const int64_t rows = std::max<int64_t>(cdiv(H, std::max(slices, 1)), 1);
+  return (int)std::min<int64_t>(per_block, rows);
+}
+
+bool attn_oproj_supported(int dtype, const AttnShape& s, int64_t H, int slices) {
+  if (s.B != 1 || s.T != 1 || s.Hkv < 1 || s.Hq % s.Hkv != 0 || s.Hq / s.Hkv > GMAX || H < 1) return false;
+  if (!(s.D == 16 || s.D == 32 || s.D == 64 || s.D == 128) || s.Hq > PART_MAX_PARTS) return false;
+  const int es = dtype == MINITP_F32 ? 4 : 2;
+  if (s.S * s.D * es >= (1LL << 32)) return false;
+  if ((int64_t)s.D * es % 16 != 0 || (int64_t)s.D * es / 16 > 64) return false;
+  const int rows = attn_oproj_rows(dtype, s, H, slices);
+  return cdiv(H, rows) <= OPROJ_MAX_SLICES && (int64_t)rows * s.Hq * s.D * es < (1LL << 31);
+}
+
+namespace {
+template <typename T, int D, int NLW>
+void oproj_launch(hipStream_t st, DecodeArgs& a, dim3 grid) {
+  hipLaunchKernelGGL((decode_attn_kernel<T, D, 1, NLW>), grid, dim3(NW * 64), 0, st, a);
+}
+
+template <typename T, int D>
+int oproj_by_nlw(hipStream_t st, DecodeArgs& a) {
+  const int cpr = D * (int)sizeof(T) / 16;
+  const int64_t chunks = (int64_t)a.op.rows * cpr;
+  const dim3 grid((unsigned)a.s.Hkv, (unsigned)cdiv(a.op.H, a.op.rows), (unsigned)(a.s.Hq / a.s.Hkv));
+  if (chunks <= NW * 64)
+    oproj_launch<T, D, 1>(st, a, grid);
+  else if (chunks <= 2 * NW * 64)
+    oproj_launch<T, D, 2>(st, a, grid);
+  else if (chunks <= 4 * NW * 64)
+    oproj_launch<T, D, 4>(st, a, grid);
+  else if (chunks <= 8 * NW * 64)
+    oproj_launch<T, D, 8>(st, a, grid);
+  else
+    oproj_launch<T, D, 16>(st, a, grid);
+  MINITP_LAUNCH_CHECK();
+  return MINITP_OK;
+}
+
+template <typename T>
+int oproj_by_d(hipStream_t st, DecodeArgs& a) {
+  switch (a.s.D) {
+    case 16:
+      return oproj_by_nlw<T, 16>(st, a);
+    case 32:
+      return oproj_by_nlw<T, 32>(st, a);
+    case 64:
+      return oproj_by_nlw<T, 64>(st, a);
+    default:
+      return oproj_by_nlw<T, 128>(st, a);
+  }
+}
+}  // namespace
+
+int launch_decode_attention_oproj(hipStream_t st, int dtype, const void* q, const AttnShape& s,
+                                  const StepState* state, int layer, const OprojArgs& o) {
+  const int slices = (int)cdiv(o.H, std::max(o.rows, 1));
+  if (!attn_oproj_supported(dtype, s, o.H, slices) || state == nullptr ||
+      o.rows != attn_oproj_rows(dtype, s, o.H, slices) || !aligned16(o.w) || o.part == nullptr) {
+    set_error("attention + o_proj: unsupported shape (B=%d T=%d Hq=%d Hkv=%d D=%d H=%lld)", s.B, s.T, s.Hq, s.Hkv,
+              s.D, (long long)o.H);
+    return MINITP_ERR_UNSUPPORTED;
+  }
+  DecodeArgs a{};
+  a.q = q;
+  a.s = s;
+  a.st = state;
+  a.layer = layer;
+  a.scale = 1.0f / sqrtf((float)s.D);
+  a.op = o;
+  return dtype == MINITP_F32 ? oproj_by_d<float>(st, a) : oproj_by_d<bf16>(st, a);
 }
 
 int launch_prefill_attention(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,

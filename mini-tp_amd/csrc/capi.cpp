@@ -216,6 +216,30 @@ int minitp_rmsnorm_linear(void* stream, int dtype, const void* x, int64_t ldx, c
   return launch_gemv(S(stream), dtype, PRO_NORM, gemv_epilogue(epilogue), g);
 }
 
+int minitp_add_rmsnorm_linear_parts(void* stream, int dtype, const void* x, const float* parts, int32_t nparts,
+                                    void* x_out, const void* norm_w, float eps, const void* w, void* y, int64_t N,
+                                    int64_t K, int epilogue) {
+  CHECK_DTYPE(dtype);
+  MINITP_CHECK_ARG(x && parts && x_out && norm_w && w && y, "add_rmsnorm_linear_parts: NULL pointer");
+  MINITP_CHECK_ARG(N >= 1 && K >= 1, "add_rmsnorm_linear_parts: N=%lld K=%lld", (long long)N, (long long)K);
+  MINITP_CHECK_ARG(aligned16(x) && aligned16(parts) && aligned16(w) && aligned16(norm_w),
+                   "add_rmsnorm_linear_parts: pointers must be 16-byte aligned");
+  MINITP_CHECK_ARG(x_out != x, "add_rmsnorm_linear_parts: x_out must not alias x");
+  if (epilogue != MINITP_EPI_SWIGLU || !gemv_part_supported(dtype, K, nparts)) {
+    set_error("add_rmsnorm_linear_parts: serves the SwiGLU epilogue with K <= %lld (a multiple of 8 bf16 / 4 fp32) "
+              "and 1..%d partial rows (epilogue %d, K %lld, %d rows)",
+              (long long)PART_MAX_K, PART_MAX_PARTS, epilogue, (long long)K, (int)nparts);
+    return MINITP_ERR_UNSUPPORTED;
+  }
+  GemvArgs g = gemv_args(x, K, w, nullptr, y, N, 1, N, K, nullptr);
+  g.norm_w = norm_w;
+  g.eps = eps;
+  g.part = parts;
+  g.nparts = nparts;
+  g.x_out = x_out;
+  return launch_gemv_part_swiglu(S(stream), dtype, g);
+}
+
 int minitp_rope(void* stream, int dtype, const void* q, const void* k, void* q_out, void* k_out, const float* cos_tab,
                 const float* sin_tab, const int64_t* positions, int64_t B, int64_t Hq, int64_t Hkv, int64_t T,
                 int64_t D) {

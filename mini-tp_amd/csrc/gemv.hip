@@ -228,6 +228,9 @@ __device__ __forceinline__ void finish_pair(const GemvArgs& a, int m, int64_t ro
 // part_val / part_idx [m][block]; argmax_merge_kernel (a separate launch)
 // picks the winner. The order of a (value, index) comparison under
 // argmax_better is total, so the merge order cannot change the winner.
+// (A merge by the grid's last block, after device-coherent partial stores
+// and an arrival count, measured no faster: 0.5218 against 0.5198 ms a
+// token at 0.5B; the count and the partial loads cost what the launch did.)
 template <int MM, int SLOTS>
 __device__ __forceinline__ void argmax_finish(const GemvArgs& a, int M, int slot, int kw, const float* bv,
                                               const int64_t* bi, float (*best_v)[MM], int64_t (*best_i)[MM]) {
@@ -254,10 +257,25 @@ __device__ __forceinline__ void argmax_finish(const GemvArgs& a, int M, int slot
   }
 }
 
+// Chunk (V elements) of a row staged in LDS as floats, packed as the dtype's
+// 16 bytes (exact: the values are already rounded to the dtype).
+template <typename T>
+__device__ __forceinline__ uint4 lds_chunk16(const float* xs, int64_t c) {
+  if constexpr (sizeof(T) == 2) {
+    return pack_bf16x8(xs + c * 8);
+  } else {
+    return make_uint4(__float_as_uint(xs[c * 4]), __float_as_uint(xs[c * 4 + 1]), __float_as_uint(xs[c * 4 + 2]),
+                      __float_as_uint(xs[c * 4 + 3]));
+  }
+}
+
 template <typename T, int MM, int KSPLIT, int JMAX, int PRO, int EPI>
 __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
   constexpr int V = Vec<T>::N;
   constexpr int SLOTS = 4 / KSPLIT;
+  constexpr bool NORM = PRO != PRO_NONE;
+  constexpr bool PART = PRO == PRO_PART_NORM;
+  static_assert(!PART || MM == 1, "the partial-sum prologue serves one row");
   __shared__ float red[4][MM * R];
   __shared__ float nrm[4][MM];
   __shared__ float best_v[4][MM];
@@ -313,15 +331,46 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
   float xf[MM][JMAX][V];
   uint4 xb[MM][JMAX];
   uint4 nw[JMAX];
+  // PRO_PART_NORM: thread tid sums elements 4 tid .. 4 tid + 3 of the partial
+  // rows (all of them in flight at once; rows past nparts read zeros). They
+  // are requested before the weights: the prologue's sum, LDS exchange and
+  // norm then overlap the weight stream (weights first measured 0.540
+  // against 0.517 ms a token at 0.5B).
+  u32x4 pv[PART ? PART_MAX_PARTS : 1];
+  float xres[4];
+  auto load_parts = [&]() {
+    const __amdgpu_buffer_rsrc_t pr = span_rsrc(a.part, (uint32_t)(a.nparts * a.K * 4));
+#pragma unroll
+    for (int h = 0; h < PART_MAX_PARTS; ++h)
+      pv[h] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                            pr, (uint32_t)((h * a.K + 4 * threadIdx.x) * 4), 0, 0));
+    const __amdgpu_buffer_rsrc_t xr = span_rsrc(x, row_bytes);
+    if constexpr (sizeof(T) == 2) {
+      const uint2 v = __builtin_bit_cast(uint2, __builtin_amdgcn_raw_buffer_load_b64(xr, 8 * threadIdx.x, 0, 0));
+      xres[0] = __uint_as_float(v.x << 16);
+      xres[1] = __uint_as_float(v.x & 0xffff0000u);
+      xres[2] = __uint_as_float(v.y << 16);
+      xres[3] = __uint_as_float(v.y & 0xffff0000u);
+    } else {
+      const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(xr, 16 * threadIdx.x, 0, 0));
+      xres[0] = __uint_as_float(v.x);
+      xres[1] = __uint_as_float(v.y);
+      xres[2] = __uint_as_float(v.z);
+      xres[3] = __uint_as_float(v.w);
+    }
+  };
+  if constexpr (PART) load_parts();
   {
-    __amdgpu_buffer_rsrc_t nr = span_rsrc(a.norm_w, PRO == PRO_NORM ? row_bytes : 0u);
+    __amdgpu_buffer_rsrc_t nr = span_rsrc(a.norm_w, NORM ? row_bytes : 0u);
 #pragma unroll
-    for (int j = 0; j < JMAX; ++j) nw[j] = PRO == PRO_NORM ? span_load16<0>(nr, coff[j]) : make_uint4(0, 0, 0, 0);
+    for (int j = 0; j < JMAX; ++j) nw[j] = NORM ? span_load16<0>(nr, coff[j]) : make_uint4(0, 0, 0, 0);
+    if constexpr (!PART) {
 #pragma unroll
-    for (int m = 0; m < MM; ++m) {
-      __amdgpu_buffer_rsrc_t xr = span_rsrc(x + (m < M ? m : 0) * a.ldx, m < M ? row_bytes : 0u);
+      for (int m = 0; m < MM; ++m) {
+        __amdgpu_buffer_rsrc_t xr = span_rsrc(x + (m < M ? m : 0) * a.ldx, m < M ? row_bytes : 0u);
 #pragma unroll
-      for (int j = 0; j < JMAX; ++j) xb[m][j] = span_load16<0>(xr, coff[j]);
+        for (int j = 0; j < JMAX; ++j) xb[m][j] = span_load16<0>(xr, coff[j]);
+      }
     }
   }
 
@@ -342,12 +391,47 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
     load_side<T, EPI>(a, em, ep, rows, rok, pos, side);
   }
 
+  // ---- 3b. PRO_PART_NORM: x + sum of the partials (in row order) ------------
+  // rounded like o_proj's output and the residual add (layer.py:63), through
+  // LDS to the waves' chunks; block 0 also stores the row for the residual
+  // add that follows the next product
+  if constexpr (PART) {
+    __shared__ __attribute__((aligned(16))) float xs[PART_MAX_K];
+    const int64_t e0 = 4 * (int64_t)threadIdx.x;
+    if (e0 < a.K) {
+      float sum[4] = {__uint_as_float(pv[0].x), __uint_as_float(pv[0].y), __uint_as_float(pv[0].z),
+                      __uint_as_float(pv[0].w)};
+#pragma unroll
+      for (int h = 1; h < PART_MAX_PARTS; ++h) {
+        if (h < a.nparts) {
+          sum[0] = add_rn(sum[0], __uint_as_float(pv[h].x));
+          sum[1] = add_rn(sum[1], __uint_as_float(pv[h].y));
+          sum[2] = add_rn(sum[2], __uint_as_float(pv[h].z));
+          sum[3] = add_rn(sum[3], __uint_as_float(pv[h].w));
+        }
+      }
+      T* xo = (T*)a.x_out;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float v = round_to<T>(add_rn(xres[e], round_to<T>(sum[e])));
+        xs[e0 + e] = v;
+        if (blockIdx.x == 0) store_f32<T>(xo, e0 + e, v);
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int j = 0; j < JMAX; ++j) {
+      const int64_t c = coff[j] / 16;
+      xb[0][j] = c * V < a.K ? lds_chunk16<T>(xs, c) : make_uint4(0, 0, 0, 0);
+    }
+  }
+
   // ---- 4. input rows in registers (normed and rounded like layer.py:39-42) --
 #pragma unroll
   for (int m = 0; m < MM; ++m)
 #pragma unroll
     for (int j = 0; j < JMAX; ++j) unpack16(xb[m][j], xf[m][j], (T*)nullptr);
-  if constexpr (PRO == PRO_NORM) {
+  if constexpr (NORM) {
     // Every wave recomputes the row's norm, so this stays short: for bf16 the
     // sum of squares runs on packed dot instructions (exact products, fp32
     // accumulation) and the normed row is rounded two elements per
@@ -1870,11 +1954,13 @@ int launch_mfma(hipStream_t st, const GemvArgs& a) {
 template <typename T, int MM, int KSPLIT, int JMAX, int PRO, int EPI>
 int launch_reg(hipStream_t st, const GemvArgs& a) {
   const int64_t slots = 4 / KSPLIT;
-  const int64_t cap = EPI == EPI_ARGMAX ? gemv_argmax_partials(a.N) : MAX_GRID;
+  const int64_t cap = EPI == EPI_ARGMAX ? gemv_argmax_partials(a.N) : a.max_grid > 0 ? a.max_grid : MAX_GRID;
   const int grid = (int)std::min<int64_t>(cdiv(num_tuples<EPI>(a), slots), cap);
   hipLaunchKernelGGL((gemv_reg_kernel<T, MM, KSPLIT, JMAX, PRO, EPI>), dim3(grid), dim3(256), 0, st, a);
   MINITP_LAUNCH_CHECK();
-  if constexpr (EPI == EPI_ARGMAX) return launch_argmax_merge(st, a.part_val, a.part_idx, grid, a.M, nullptr, 0, a.st);
+  if constexpr (EPI == EPI_ARGMAX) {
+    return launch_argmax_merge(st, a.part_val, a.part_idx, grid, a.M, nullptr, 0, a.st);
+  }
   return MINITP_OK;
 }
 
@@ -1888,7 +1974,9 @@ int launch_lds(hipStream_t st, const GemvArgs& a) {
   const int grid = (int)std::min<int64_t>(num_tuples<EPI>(a), cap);
   hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, a);
   MINITP_LAUNCH_CHECK();
-  if constexpr (EPI == EPI_ARGMAX) return launch_argmax_merge(st, a.part_val, a.part_idx, grid, a.M, nullptr, 0, a.st);
+  if constexpr (EPI == EPI_ARGMAX) {
+    return launch_argmax_merge(st, a.part_val, a.part_idx, grid, a.M, nullptr, 0, a.st);
+  }
   return MINITP_OK;
 }
 
@@ -1989,7 +2077,31 @@ int pick_epi(hipStream_t st, int epi, const GemvArgs& a) {
   return MINITP_ERR_ARG;
 }
 
+template <typename T>
+int launch_part_swiglu_t(hipStream_t st, const GemvArgs& a) {
+  const int64_t nchunk = a.K / Vec<T>::N;
+  // (K <= PART_MAX_K: bf16 rows are at most 128 chunks, fp32 rows 256)
+  if (nchunk <= 128) return launch_reg<T, 1, 1, 2, PRO_PART_NORM, EPI_SWIGLU>(st, a);
+  if constexpr (sizeof(T) == 4) return launch_reg<T, 1, 2, 4, PRO_PART_NORM, EPI_SWIGLU>(st, a);
+  set_error("gemv: partial-sum prologue row of %lld chunks", (long long)nchunk);
+  return MINITP_ERR_UNSUPPORTED;
+}
+
 }  // namespace
+
+bool gemv_part_supported(int dtype, int64_t K, int nparts) {
+  const int v = dtype == MINITP_F32 ? 4 : 8;
+  return nparts >= 1 && nparts <= PART_MAX_PARTS && K >= v && K % v == 0 && K <= PART_MAX_K;
+}
+
+int launch_gemv_part_swiglu(hipStream_t st, int dtype, const GemvArgs& a) {
+  if (a.M != 1 || !gemv_part_supported(dtype, a.K, a.nparts) || a.part == nullptr || a.x_out == nullptr) {
+    set_error("gemv: partial-sum prologue needs one row, K <= %lld, 1..%d partial rows (M=%lld K=%lld parts=%d)",
+              (long long)PART_MAX_K, PART_MAX_PARTS, (long long)a.M, (long long)a.K, a.nparts);
+    return MINITP_ERR_UNSUPPORTED;
+  }
+  return dtype == MINITP_F32 ? launch_part_swiglu_t<float>(st, a) : launch_part_swiglu_t<bf16>(st, a);
+}
 
 int64_t gemv_split_part_bytes(int64_t M) {
   const int64_t reg = (int64_t)SPLIT_MAX_TUPLES * SPLIT_MAX_SEG * 4 * R * sizeof(float);

@@ -56,7 +56,11 @@ struct AttnShape {
   int64_t S;  // cache capacity per (b, kv head)
 };
 
-enum GemvPro { PRO_NONE = 0, PRO_NORM = 1 };
+// PRO_PART_NORM (one input row): the input is x + the sum of `nparts` fp32
+// partial rows of a product split over K (the per-head o_proj partials of the
+// fused attention), rounded like the residual add of layer.py:63 before the
+// RMSNorm; block 0 also stores that row to x_out.
+enum GemvPro { PRO_NONE = 0, PRO_NORM = 1, PRO_PART_NORM = 2 };
 enum GemvEpi { EPI_STORE = 0, EPI_RESID = 1, EPI_SWIGLU = 2, EPI_QKV_ROPE = 3, EPI_ARGMAX = 4 };
 
 struct GemvArgs {
@@ -87,9 +91,21 @@ struct GemvArgs {
   float* split_part;
   uint32_t* split_count;
   int64_t split_part_bytes;
+  // PRO_PART_NORM: partial rows [nparts][K] fp32 and where block 0 writes x + their sum
+  const float* part;
+  int nparts;
+  void* x_out;
+  int max_grid;  // register form: cap on the grid (0: the default)
 };
 
 // gemv.hip
+// The partial-sum prologue's limits: at most PART_MAX_PARTS partial rows of
+// K <= PART_MAX_K elements (one row).
+constexpr int PART_MAX_PARTS = 16;
+constexpr int64_t PART_MAX_K = 1024;
+bool gemv_part_supported(int dtype, int64_t K, int nparts);
+// RMSNorm(x + sum of partials) -> gate/up -> SwiGLU for one row (PRO_PART_NORM, EPI_SWIGLU)
+int launch_gemv_part_swiglu(hipStream_t st, int dtype, const GemvArgs& a);
 int64_t gemv_argmax_partials(int64_t N);
 int launch_gemv(hipStream_t st, int dtype, int pro, int epi, const GemvArgs& a);
 bool gemv_supported(int dtype, int64_t M, int64_t K);
@@ -193,6 +209,27 @@ int64_t attention_workspace_bytes(int64_t B, int64_t T, int64_t Hq, int64_t Hkv,
 int launch_decode_attention(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,
                             void* out, const AttnShape& a, int64_t cache_len, const StepState* state, int layer,
                             void* workspace, int64_t workspace_bytes);
+// Decode attention of one batch row with the o_proj product folded in
+// (attention.py:77-105 then o_proj, attention.py:42-44 / linear.py:117):
+// block (query head h, row slice r) runs head h's attention, rounds its
+// output to the dtype and multiplies it by W_o[rows of slice r, h * D ..
+// h * D + D), storing the fp32 partial part[h][rows]. Summed over h (in
+// head order) by the next kernel's prologue. Cache and cache_len from the
+// step state. One batch row; served when attn_oproj_supported says so.
+struct OprojArgs {
+  const void* w;   // W_o [H, Hq * D]
+  int64_t H;       // output rows
+  int rows;        // rows per slice (gridDim.y = ceil(H / rows))
+  float* part;     // [Hq][H]
+};
+// W_o row slices a model asks for: more slices re-run each head's attention
+// more often but give each block fewer rows (0.5B: 4 slices 0.524 ms a
+// token, 8 0.518, 16 0.517).
+constexpr int OPROJ_SLICES = 16;
+bool attn_oproj_supported(int dtype, const AttnShape& a, int64_t H, int slices);
+int attn_oproj_rows(int dtype, const AttnShape& a, int64_t H, int slices);
+int launch_decode_attention_oproj(hipStream_t st, int dtype, const void* q, const AttnShape& a,
+                                  const StepState* state, int layer, const OprojArgs& o);
 // Inside a forward (state != null) the caches of layer `layer` and cache_len
 // come from the step state (k_cache, v_cache and cache_len unused).
 int launch_prefill_attention(hipStream_t st, int dtype, const void* q, const void* k_cache, const void* v_cache,

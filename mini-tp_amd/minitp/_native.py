@@ -45,6 +45,8 @@ SIGNATURES = {
     "minitp_linear": (_int, [_vp, _int, _vp, _i64, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int, _vp]),
     "minitp_rmsnorm_linear": (_int, [_vp, _int, _vp, _i64, _vp, _f32, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _int,
                                      _vp]),
+    "minitp_add_rmsnorm_linear_parts": (_int, [_vp, _int, _vp, _vp, _i32, _vp, _vp, _f32, _vp, _vp, _i64, _i64,
+                                               _int]),
     "minitp_rope": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64]),
     "minitp_kv_write": (_int, [_vp, _int, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _i64, _i64]),
     "minitp_rope_kv_write": (_int, [_vp, _int, _vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,

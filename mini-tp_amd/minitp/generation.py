@@ -161,9 +161,14 @@ class GenerationState:
             self._check_position(self.cursor - 1)  # pos is positions_buf[cursor - 1]: value known
         else:
             # any other position tensor: read its value (one host sync, off the
-            # generate_greedy path), so a position past the RoPE table raises
-            # IndexError here as the reference's table gather does (rope.py:37-45)
-            self._check_position(int(pos.reshape(-1).max()))
+            # generate_greedy path) so that it indexes the RoPE table as the
+            # reference's gather does: past the table raises IndexError, a
+            # negative position wraps (rope.py:37-45)
+            from minitp.rope import _check_positions
+
+            limit = self.model.cfg.max_position_embeddings
+            _check_positions(pos, limit)
+            pos = torch.where(pos < 0, pos + limit, pos)
         if not self.reuse_decode_logits or self._decode_logits is None or self._decode_logits.shape[0] != b:
             self._decode_logits = torch.empty(b, 1, self.model.cfg.vocab_size, dtype=self.kv.k_buf.dtype,
                                               device=self.out_ids.device)

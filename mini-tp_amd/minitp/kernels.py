@@ -174,6 +174,26 @@ def rmsnorm_linear(x: torch.Tensor, norm_w: torch.Tensor, eps: float, w: torch.T
     return out
 
 
+def add_rmsnorm_linear_parts(x: torch.Tensor, parts: torch.Tensor, norm_w: torch.Tensor, eps: float,
+                             w: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """One row: x_out = x + (sum of the fp32 partial rows ``parts`` [P, K],
+    in row order), each rounded to the dtype (layer.py:63), then
+    silu(gate) * up of rmsnorm(x_out) W^T (layer.py:64-67, mlp.py:34-38).
+    Returns (x_out [K], y [N])."""
+    N.require_gpu(x, parts, norm_w, w, what="add_rmsnorm_linear_parts")
+    if parts.dtype != torch.float32 or x.dtype != w.dtype or norm_w.dtype != w.dtype:
+        raise TypeError(f"add_rmsnorm_linear_parts: dtypes x={x.dtype} parts={parts.dtype} w={w.dtype}")
+    k = x.numel()
+    x, parts, w, norm_w = x.contiguous(), parts.contiguous(), w.contiguous(), norm_w.contiguous()
+    x_out = torch.empty_like(x)
+    y = torch.empty(w.shape[0] // 2, dtype=x.dtype, device=x.device)
+    N.check(_lib().minitp_add_rmsnorm_linear_parts(N.stream(), N.dtype_code(x.dtype), x.data_ptr(), parts.data_ptr(),
+                                                   parts.shape[0], x_out.data_ptr(), norm_w.data_ptr(), float(eps),
+                                                   w.data_ptr(), y.data_ptr(), y.numel(), k, N.EPI_SWIGLU),
+            "add_rmsnorm_linear_parts")
+    return x_out, y
+
+
 def rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, positions: torch.Tensor):
     """RotaryEmbedding.apply on contiguous [B, H, T, D] q and k."""
     N.require_gpu(q, k, cos, sin, positions, what="rope")

@@ -245,6 +245,33 @@ def test_mfma_gemv_many_tuples_equals_column_blocks(m, n, k, epilogue, norm):
     assert ((got - ref).abs() <= tol).all(), (got - ref).abs().max().item()
 
 
+@pytest.mark.parametrize("k,nparts", [(896, 14), (64, 4), (1024, 16), (896, 1), (512, 7)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_add_rmsnorm_linear_parts(k, nparts, dtype):
+    """The gate/up prologue that takes o_proj as fp32 partial rows: x_out is
+    exactly dtype(x + dtype(p0 + p1 + ...)) with the rows added in order in
+    fp32 (layer.py:63), and y is bitwise the fused norm + gate/up GEMV run on
+    x_out (the same kernel code past the prologue; that GEMV has its float64
+    check in test_rmsnorm_linear_matches_two_step_reference)."""
+    from minitp import _native as N
+
+    g = torch.Generator().manual_seed(k + nparts)
+    n, eps = 768, 1e-6
+    x = torch.randn(k, generator=g).to(dtype)
+    parts = torch.randn(nparts, k, generator=g) * 0.5
+    nw = (1 + 0.1 * torch.randn(k, generator=g)).to(dtype)
+    w = (torch.randn(2 * n, k, generator=g) * 0.02).to(dtype)
+    s = parts[0].clone()
+    for p in range(1, nparts):
+        s = s + parts[p]  # fp32, row order
+    want_x = (x.float() + s.to(dtype).float()).to(dtype)
+    x_out, y = _k().add_rmsnorm_linear_parts(x.to(DEV), parts.to(DEV), nw.to(DEV), eps, w.to(DEV))
+    assert torch.equal(x_out.cpu(), want_x)
+    y_ref = _k().rmsnorm_linear(want_x.to(DEV).reshape(1, k), nw.to(DEV), eps, w.to(DEV), None,
+                                epilogue=N.EPI_SWIGLU)
+    assert torch.equal(y.cpu(), y_ref.reshape(-1).cpu())
+
+
 def test_rmsnorm_linear_refuses_prefill_shapes():
     x = torch.randn(8, 896, device=DEV)
     nw = torch.ones(896, device=DEV)
@@ -451,6 +478,7 @@ def test_prefill_attention_causal_bf16_long(b, t, cache_len, hq, hkv, d):
 def test_argmax_matches_torch(dtype, v):
     g = torch.Generator().manual_seed(v)
     x = torch.randn(5, v, generator=g).to(dtype)
+    x[0, v - 1] = x[0].max() + 1  # unique max in the last element of a 16-byte-aligned row (the tail vector)
     x[1, v // 3] = x[1].max() + 1  # unique max
     x[2, 3] = x[2, v - 1] = x[2].max() + 1  # tie -> smaller id
     x[3] = -x[3].abs() - 1  # all negative

@@ -163,6 +163,55 @@ def test_q05b_bf16_logits_teacher_forced():
 # execution paths agree
 
 
+def _program_with_env(model, name, value):
+    """(Re)create the model's native program with an environment switch set
+    (the library reads it when the program is created)."""
+    import os
+
+    old = os.environ.get(name)
+    os.environ[name] = value
+    try:
+        model._prog = None
+        model.program()
+    finally:
+        if old is None:
+            del os.environ[name]
+        else:
+            os.environ[name] = old
+
+
+@pytest.mark.parametrize("shape_name", ["TINY", "QWEN05B"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_fused_attention_oproj_matches_separate_oproj(shape_name, dtype):
+    """Batch-1 decode folds o_proj into the attention kernel (per-head fp32
+    partials, summed with the residual by the gate/up prologue). Against the
+    separate o_proj GEMV (MINITP_FUSE_OPROJ=0) only o_proj's summation order
+    differs: teacher-forced logits agree to fp32 rounding (fp32) or within
+    the bf16 logit bar, the greedy picks wherever the top-2 margin is clear,
+    and the fused run's ids are the greedy ids of its own logits."""
+    from minitp.generation import generate_greedy
+
+    fused = _synthetic(shape_name, dtype)
+    split = _synthetic(shape_name, dtype)
+    _program_with_env(split, "MINITP_FUSE_OPROJ", "0")
+    v = fused.cfg.vocab_size
+    prompt = torch.randint(0, v, (1, 12), generator=torch.Generator().manual_seed(11)).to(DEV)
+    ids = generate_greedy(fused, prompt, 48, early_stop=False)
+    rf, _ = _teacher_forced_rows(fused, prompt, ids.cpu(), 48)
+    rs, _ = _teacher_forced_rows(split, prompt, ids.cpu(), 48)
+    fused.program().check_decode()
+    split.program().check_decode()
+    atol = 2e-4 if dtype == torch.float32 else BF16_LOGIT_ATOL
+    err = (rf - rs).abs().max().item()
+    assert torch.isfinite(rf).all() and err <= atol, err
+    top2 = rs.topk(2, dim=-1).values
+    clear = (top2[..., 0] - top2[..., 1]) > 2 * atol
+    assert torch.equal(rf.argmax(-1)[clear], rs.argmax(-1)[clear])
+    # decode rows (the prefill row comes from the every-position prompt form)
+    assert torch.equal(rf.argmax(-1)[1:, 0], ids[0, 13:].cpu())
+    print(f"{shape_name} {dtype}: fused vs separate o_proj max logit diff {err:.3e}")
+
+
 def _tiny(dtype=torch.float32):
     shape, state = _oracle_state("TINY", torch.float32)
     return _model_from_state(shape, state, dtype)

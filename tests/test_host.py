@@ -183,6 +183,22 @@ def test_abi_validation_paths_return_status_without_gpu_work():
     assert lib.minitp_argmax_workspace_bytes(1, 151936) > 0
 
 
+def test_add_rmsnorm_linear_parts_refuses_unserved_shapes():
+    from minitp import _native as N
+
+    lib = N.lib()
+    # 17 partial rows, K past 1024, an epilogue other than SwiGLU: refused before any launch
+    st = lib.minitp_add_rmsnorm_linear_parts(None, N.BF16, 16, 16, 17, 32, 16, 1e-6, 16, 16, 64, 896, N.EPI_SWIGLU)
+    assert st == N.ERR_UNSUPPORTED and b"partial rows" in lib.minitp_last_error()
+    st = lib.minitp_add_rmsnorm_linear_parts(None, N.BF16, 16, 16, 4, 32, 16, 1e-6, 16, 16, 64, 2048, N.EPI_SWIGLU)
+    assert st == N.ERR_UNSUPPORTED
+    st = lib.minitp_add_rmsnorm_linear_parts(None, N.BF16, 16, 16, 4, 32, 16, 1e-6, 16, 16, 64, 896, N.EPI_NONE)
+    assert st == N.ERR_UNSUPPORTED
+    with pytest.raises(ValueError, match="alias"):
+        N.check(lib.minitp_add_rmsnorm_linear_parts(None, N.BF16, 16, 16, 4, 16, 16, 1e-6, 16, 16, 64, 896,
+                                                    N.EPI_SWIGLU), "parts")
+
+
 def test_program_create_validates_and_sizes_workspace():
     from minitp import _native as N
 
