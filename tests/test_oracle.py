@@ -103,23 +103,99 @@ def test_rope_invariants():
     torch.testing.assert_close(rq, uq, atol=1e-6, rtol=1e-5)
 
 
-def test_attention_single_key_zero_query_and_gqa_mapping():
-    shape = R.Qwen2Shape(32, 64, 1, 4, 2, 8, 50, 1e-6, 1e4, 64, True)
+def _attention_probe(q_bias=None, w_v_identity=False, seed=3):
+    """Oracle attention of layer 0 with o_proj = I (hq * hd == hidden), so its
+    output is the raw SDPA output [B, T, Hq * D]. The QKV projection is chosen
+    per check: q from q_bias only (weight rows 0), k from random weights, v
+    either the identity on the input's first Hkv * D dims or random."""
+    hq, hkv, hd, hid = 4, 2, 8, 32
+    shape = R.Qwen2Shape(hid, 64, 1, hq, hkv, hd, 50, 1e-6, 1e4, 64, True)
     sd = R.synthetic_state(shape, seed=1)
+    g = torch.Generator().manual_seed(seed)
+    w = torch.zeros((hq + 2 * hkv) * hd, hid)
+    b = torch.zeros((hq + 2 * hkv) * hd)
+    if q_bias is not None:
+        b[: hq * hd] = q_bias
+    w[hq * hd:(hq + hkv) * hd] = torch.randn(hkv * hd, hid, generator=g)  # k
+    if w_v_identity:
+        w[(hq + hkv) * hd:, : hkv * hd] = torch.eye(hkv * hd)  # v = x[:, :Hkv * D]
+    else:
+        w[(hq + hkv) * hd:] = torch.randn(hkv * hd, hid, generator=g)
+    sd["model.layers.0.self_attn.qkv_proj.weight"] = w
+    sd["model.layers.0.self_attn.qkv_proj.bias"] = b
+    sd["model.layers.0.self_attn.o_proj.weight"] = torch.eye(hid)
     m = R.OracleQwen2(shape, sd)
-    m.cos_cache, m.sin_cache = R.rope_tables(8, 1e4, 64)
-    kv = m.make_kv_cache(1, 4)
-    x = torch.randn(1, 1, 32)
-    m.attention(0, x, torch.tensor([0]), kv, True)
-    # ctx == 1: every q head's output equals V[0] of its KV group; check via o_proj inverse
-    y = F.linear(x, sd["model.layers.0.self_attn.qkv_proj.weight"], sd["model.layers.0.self_attn.qkv_proj.bias"])
-    v = y[..., 32 + 16:].view(2, 8)
-    out = m.attention  # noqa: F841  (exercise done above)
-    k = kv.v[0][0, :, 0]
-    torch.testing.assert_close(k, v)
-    # GQA order: repeat_interleave maps q head h to kv head h // (Hq / Hkv)
-    kk = torch.arange(2.0).view(1, 2, 1, 1).expand(1, 2, 3, 1)
-    assert kk.repeat_interleave(2, dim=1)[0, :, 0, 0].tolist() == [0.0, 0.0, 1.0, 1.0]
+    m.cos_cache, m.sin_cache = R.rope_tables(hd, 1e4, 64)
+    return m, (hq, hkv, hd, hid)
+
+
+def _check_attention_closed_forms(m, dims):
+    """Closed forms of SDPA over a GQA cache (attention.py:77-103), checked
+    on the oracle's attention output (o_proj = I):
+    * one key: query head h returns V[0] of KV head h // (Hq / Hkv);
+    * q = 0: uniform weights, so causal position t returns the mean of
+      V[0..t] of its KV head."""
+    hq, hkv, hd, hid = dims
+    grp = hq // hkv
+    g = torch.Generator().manual_seed(7)
+    # (1) a single key: a one-token prompt on an empty cache
+    x = torch.randn(1, 1, hid, generator=g)
+    kv = m.make_kv_cache(1, 8)
+    out = m.attention(0, x, torch.tensor([0]), kv, True)[0, 0].view(hq, hd)
+    v0 = kv.v[0][0, :, 0]  # [Hkv, D], as the cache holds it
+    for h in range(hq):
+        torch.testing.assert_close(out[h], v0[h // grp], atol=1e-6, rtol=0)
+    # (2) q = 0 over a 5-token causal prompt: prefix means of V
+    x = torch.randn(1, 5, hid, generator=g)
+    kv = m.make_kv_cache(1, 8)
+    out = m.attention(0, x, torch.arange(5), kv, True)[0].view(5, hq, hd)
+    vals = kv.v[0][0, :, :5]  # [Hkv, 5, D]
+    for t in range(5):
+        mean = vals[:, : t + 1].mean(dim=1)
+        for h in range(hq):
+            torch.testing.assert_close(out[t, h], mean[h // grp], atol=1e-5, rtol=0)
+
+
+def test_attention_closed_forms_single_key_zero_query_and_gqa_mapping():
+    m, dims = _attention_probe(q_bias=None, w_v_identity=True)
+    hq, hkv, hd, hid = dims
+    # the KV heads' values differ, so the head -> KV head map is observable
+    _check_attention_closed_forms(m, dims)
+    # a non-zero query with a single key still returns V[0] (softmax of one score)
+    m2, _ = _attention_probe(q_bias=torch.randn(hq * hd, generator=torch.Generator().manual_seed(2)))
+    x = torch.randn(1, 1, hid)
+    kv = m2.make_kv_cache(1, 4)
+    out = m2.attention(0, x, torch.tensor([0]), kv, True)[0, 0].view(hq, hd)
+    for h in range(hq):
+        torch.testing.assert_close(out[h], kv.v[0][0, h // (hq // hkv), 0], atol=1e-6, rtol=0)
+
+
+def test_attention_closed_forms_catch_a_planted_gqa_mistake(monkeypatch):
+    """Planted mistake: KV heads tiled (h % Hkv) instead of interleaved
+    (h // G). The closed-form check must reject that oracle."""
+    m, dims = _attention_probe(q_bias=None, w_v_identity=True)
+    monkeypatch.setattr(torch.Tensor, "repeat_interleave", lambda self, n, dim: self.repeat(1, n, 1, 1))
+    with pytest.raises(AssertionError):
+        _check_attention_closed_forms(m, dims)
+
+
+def test_attention_closed_forms_catch_a_planted_mask_mistake(monkeypatch):
+    """Planted mistake: a causal mask shifted by one (the query sees one key
+    fewer). The prefix-mean check must reject it."""
+    m, dims = _attention_probe(q_bias=None, w_v_identity=True)
+    real = F.scaled_dot_product_attention
+
+    def shifted(q, k, v, attn_mask=None, is_causal=False, **kw):
+        if is_causal:
+            t, s = q.shape[-2], k.shape[-2]
+            mask = torch.ones(t, s, dtype=torch.bool).tril(diagonal=-1)
+            mask[0, 0] = True  # keep row 0 defined
+            return real(q, k, v, attn_mask=mask)
+        return real(q, k, v, attn_mask=attn_mask, is_causal=is_causal)
+
+    monkeypatch.setattr(R.F, "scaled_dot_product_attention", shifted)
+    with pytest.raises(AssertionError):
+        _check_attention_closed_forms(m, dims)
 
 
 def test_tril_offset_mask_is_causal_with_cache():
