@@ -20,6 +20,8 @@
 // prefetches the next tuple's weights before its own reduction and epilogue.
 // gemv_lds_kernel stages the input in LDS and serves longer rows.
 // gemv_mfma_kernel serves bf16 decode batches of 5 to 32 rows on MFMA.
+#include <mutex>
+
 #include "common.h"
 #include "kernels.h"
 
@@ -2094,12 +2096,32 @@ bool gemv_part_supported(int dtype, int64_t K, int nparts) {
   return nparts >= 1 && nparts <= PART_MAX_PARTS && K >= v && K % v == 0 && K <= PART_MAX_K;
 }
 
-int launch_gemv_part_swiglu(hipStream_t st, int dtype, const GemvArgs& a) {
-  if (a.M != 1 || !gemv_part_supported(dtype, a.K, a.nparts) || a.part == nullptr || a.x_out == nullptr) {
+// Compute units of the current device (cached per device).
+static int device_cus() {
+  static std::mutex mu;
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  std::lock_guard<std::mutex> lock(mu);
+  if (cus[dev] == 0) {
+    int n = 0;
+    cus[dev] = hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0 ? n : 256;
+  }
+  return cus[dev];
+}
+
+int launch_gemv_part_swiglu(hipStream_t st, int dtype, const GemvArgs& a_in) {
+  if (a_in.M != 1 || !gemv_part_supported(dtype, a_in.K, a_in.nparts) || a_in.part == nullptr ||
+      a_in.x_out == nullptr) {
     set_error("gemv: partial-sum prologue needs one row, K <= %lld, 1..%d partial rows (M=%lld K=%lld parts=%d)",
-              (long long)PART_MAX_K, PART_MAX_PARTS, (long long)a.M, (long long)a.K, a.nparts);
+              (long long)PART_MAX_K, PART_MAX_PARTS, (long long)a_in.M, (long long)a_in.K, a_in.nparts);
     return MINITP_ERR_UNSUPPORTED;
   }
+  // One block per CU: every block reads all the partial rows once, so fewer
+  // blocks read less (0.5B decode: 608 blocks 0.553 ms a token, 256 blocks
+  // 0.517, 320 0.543).
+  GemvArgs a = a_in;
+  if (a.max_grid <= 0) a.max_grid = device_cus();
   return dtype == MINITP_F32 ? launch_part_swiglu_t<float>(st, a) : launch_part_swiglu_t<bf16>(st, a);
 }
 

@@ -120,14 +120,20 @@ struct GraphKey {
 };
 
 struct GraphEntry {
-  int64_t batch, tokens, max_seq;
-  void* workspace;
-  bool eos;  // records the end-of-sequence update after the token selection
-  bool pick; // records the token selection (next_tok set; batch > 4 has no pick node otherwise)
-  bool all;  // every position's logits (an LM head over B x T rows) rather than the last's
+  GraphKey key;  // eos: the end-of-sequence update after the token selection;
+                 // pick: the token selection (next_tok set; batch > 4 has no pick
+                 // node otherwise); all: every position's logits, not the last's
   hipGraph_t graph;
   hipGraphExec_t exec;
   hipGraphNode_t first;
+  uint64_t last_use;         // call clock of the last replay (least recently used goes first)
+  hipStream_t last_stream;   // stream of the last launch (waited on before a destroy)
+};
+
+// Calls seen per shape, recorded or not (the graph cache's admission test).
+struct ShapeCalls {
+  GraphKey key;
+  uint64_t calls, last;
 };
 
 inline int64_t align256(int64_t v) { return (v + 255) & ~int64_t(255); }
@@ -144,7 +150,8 @@ struct Qwen2Program {
   std::vector<const void*> lw;
   std::mutex mu;
   std::vector<GraphEntry> graphs;
-  std::vector<GraphKey> prompt_seen;  // prompt shapes run once (recorded on the next call)
+  std::vector<ShapeCalls> shape_calls;  // calls per shape (at most 64 shapes tracked)
+  uint64_t clock = 0;                  // forward calls through run_graphed
   hipStream_t capture_stream = nullptr;
   // bf16 prompt forwards (last-position logits) through a graph per shape;
   // direct launches when MINITP_PREFILL_GRAPH=0 is in the environment at
@@ -154,10 +161,6 @@ struct Qwen2Program {
   // the gate/up prologue); MINITP_FUSE_OPROJ=0 at creation keeps the
   // separate o_proj GEMV
   bool fuse_oproj = true;
-  // The partial-sum gate/up runs one block per CU: each block reads all the
-  // partial rows once, so fewer blocks read less (measured at 0.5B: 608
-  // blocks 0.553 ms a token, 256 blocks 0.517, 320 0.543).
-  int part_grid = 256;
 
   int es() const { return c.dtype == MINITP_F32 ? 4 : 2; }
   int qkv_rows() const { return (c.heads + 2 * c.kv_heads) * c.head_dim; }
@@ -422,7 +425,6 @@ struct Qwen2Program {
           g.part = w.opart;
           g.nparts = c.heads;
           g.x_out = w.h;
-          g.max_grid = part_grid;
           if ((rc = launch_gemv_part_swiglu(st, c.dtype, g))) return rc;
         } else if ((rc = launch_gemv(st, c.dtype, PRO_NORM, EPI_SWIGLU, g))) {
           return rc;
@@ -603,35 +605,60 @@ static int run_graphed(Qwen2Program* p, hipStream_t st, const minitp_qwen2_step&
   hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
   if (hipStreamIsCapturing(st, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone) return p->run(st, s, w);
   std::lock_guard<std::mutex> lock(p->mu);
+  const GraphKey key{s.batch, s.tokens, s.max_seq, s.workspace, s.eos_state != nullptr, s.next_tok != nullptr,
+                     s.logits_all != 0};
+  const uint64_t now = ++p->clock;
+  // calls of this shape
+  ShapeCalls* sc = nullptr;
+  for (auto& c : p->shape_calls)
+    if (c.key == key) sc = &c;
+  if (sc == nullptr) {
+    if (p->shape_calls.size() >= 64) {  // forget the shape called least recently
+      auto old = p->shape_calls.begin();
+      for (auto it = p->shape_calls.begin(); it != p->shape_calls.end(); ++it)
+        if (it->last < old->last) old = it;
+      p->shape_calls.erase(old);
+    }
+    p->shape_calls.push_back(ShapeCalls{key, 0, 0});
+    sc = &p->shape_calls.back();
+  }
+  ++sc->calls;
+  sc->last = now;
+  const uint64_t calls = sc->calls;
   for (auto& g : p->graphs)
-    if (g.batch == s.batch && g.tokens == s.tokens && g.max_seq == s.max_seq && g.workspace == s.workspace &&
-        g.eos == (s.eos_state != nullptr) && g.pick == (s.next_tok != nullptr) && g.all == (s.logits_all != 0))
+    if (g.key == key) {
+      g.last_use = now;
+      g.last_stream = st;
       return patch_and_launch(p, g, st, s, w);
-  // First call with this shape: run eagerly, then record the same sequence.
-  // A prompt shape records on its second call only, so one-off prompt
-  // lengths never pay a capture or push a graph out of the cache.
+    }
+  // Not recorded: run directly. A prompt shape is recorded on its second
+  // call (a one-off prompt length pays no capture), a decode shape on its
+  // first. When the cache already holds 8 graphs of this kind, the shape
+  // takes the place of the least recently used one only if it has been
+  // called more often than that one, so a rotation of more shapes than the
+  // cache holds settles on replaying 8 of them instead of re-recording.
   int rc = p->run(st, s, w);
   if (rc) return rc;
-  if (s.tokens > 1) {
-    const GraphKey key{s.batch, s.tokens, s.max_seq, s.workspace, s.eos_state != nullptr, s.next_tok != nullptr,
-                       s.logits_all != 0};
-    bool seen = false;
-    for (const auto& k : p->prompt_seen) seen = seen || k == key;
-    if (!seen) {
-      if (p->prompt_seen.size() >= 32) p->prompt_seen.erase(p->prompt_seen.begin());
-      p->prompt_seen.push_back(key);
-      return MINITP_OK;
+  const bool prompt = s.tokens > 1;
+  if (prompt && calls < 2) return MINITP_OK;
+  GraphEntry* victim = nullptr;
+  int same_kind = 0;
+  for (auto& e : p->graphs)
+    if ((e.key.tokens > 1) == prompt) {
+      ++same_kind;
+      if (victim == nullptr || e.last_use < victim->last_use) victim = &e;
     }
+  if (same_kind >= 8) {
+    uint64_t victim_calls = 0;
+    for (const auto& c : p->shape_calls)
+      if (c.key == victim->key) victim_calls = c.calls;
+    if (calls <= victim_calls) return MINITP_OK;
   }
   if (!p->capture_stream) MINITP_RETURN_HIP(hipStreamCreateWithFlags(&p->capture_stream, hipStreamNonBlocking));
   GraphEntry g{};
-  g.batch = s.batch;
-  g.tokens = s.tokens;
-  g.max_seq = s.max_seq;
-  g.workspace = s.workspace;
-  g.eos = s.eos_state != nullptr;
-  g.pick = s.next_tok != nullptr;
-  g.all = s.logits_all != 0;
+  g.key = key;
+  g.last_use = now;
+  g.last_stream = st;
   MINITP_RETURN_HIP(hipStreamBeginCapture(p->capture_stream, hipStreamCaptureModeRelaxed));
   rc = p->run(p->capture_stream, s, w);
   hipError_t e = hipStreamEndCapture(p->capture_stream, &g.graph);
@@ -649,18 +676,13 @@ static int run_graphed(Qwen2Program* p, hipStream_t st, const minitp_qwen2_step&
   }
   MINITP_RETURN_HIP(hipGraphGetRootNodes(g.graph, &g.first, &n_roots));
   MINITP_RETURN_HIP(hipGraphInstantiate(&g.exec, g.graph, nullptr, nullptr, 0));
-  // bounded cache, at most 8 decode and 8 prompt graphs: drop the oldest of
-  // the new graph's kind
-  int same_kind = 0;
-  for (const auto& e : p->graphs) same_kind += (e.tokens > 1) == (g.tokens > 1);
   if (same_kind >= 8) {
-    for (auto it = p->graphs.begin(); it != p->graphs.end(); ++it)
-      if ((it->tokens > 1) == (g.tokens > 1)) {
-        (void)hipGraphExecDestroy(it->exec);
-        (void)hipGraphDestroy(it->graph);
-        p->graphs.erase(it);
-        break;
-      }
+    // a replay of the victim may still be running: wait for the stream it
+    // was last launched on before destroying it
+    (void)hipStreamSynchronize(victim->last_stream);
+    (void)hipGraphExecDestroy(victim->exec);
+    (void)hipGraphDestroy(victim->graph);
+    p->graphs.erase(p->graphs.begin() + (victim - p->graphs.data()));
   }
   p->graphs.push_back(g);
   return MINITP_OK;
@@ -705,10 +727,6 @@ int minitp_qwen2_create(const minitp_qwen2_config* cfg, const minitp_qwen2_weigh
   p->final_norm = w->final_norm;
   p->cos_tab = w->rope_cos;
   p->sin_tab = w->rope_sin;
-  int dev = 0, cus = 0;
-  if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) ==
-                                              hipSuccess && cus > 0)
-    p->part_grid = cus;
   p->lw.assign(w->layers, w->layers + (size_t)c.num_layers * MINITP_W_PER_LAYER);
   *handle = p;
   return MINITP_OK;

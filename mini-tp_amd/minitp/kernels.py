@@ -206,13 +206,29 @@ def rope(q: torch.Tensor, k: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor,
     return qo, ko
 
 
+def cache_rows(k_cache: torch.Tensor, v_cache: torch.Tensor) -> int:
+    """Row stride S of [B, Hkv, S, D] cache views whose rows are contiguous
+    (a KVCache layer view may show fewer rows than its buffer holds)."""
+    for c in (k_cache, v_cache):
+        b, h, s, d = c.shape
+        if c.stride(3) != 1 or c.stride(2) != d or c.stride(0) != h * c.stride(1) or c.stride(1) % d:
+            raise ValueError(f"KV cache view {tuple(c.shape)} with strides {c.stride()} is not a [B, Hkv, S, D] "
+                             "layout with contiguous rows")
+    if k_cache.stride() != v_cache.stride():
+        raise ValueError("K and V caches have different layouts")
+    return k_cache.stride(1) // k_cache.shape[3]
+
+
 def kv_write(k_new: torch.Tensor, v_new: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor,
              cache_len: int) -> None:
     N.require_gpu(k_new, v_new, k_cache, v_cache, what="KVCache.update")
     k_new, v_new = k_new.contiguous(), v_new.contiguous()
     b, h, t, d = k_new.shape
+    if cache_len + t > k_cache.shape[2]:
+        raise ValueError(f"KV cache overflow: seq {cache_len}+{t} > max_seq_len={k_cache.shape[2]}")
     N.check(_lib().minitp_kv_write(N.stream(), N.dtype_code(k_cache.dtype), k_new.data_ptr(), v_new.data_ptr(),
-                                   k_cache.data_ptr(), v_cache.data_ptr(), b, h, t, d, k_cache.shape[2], cache_len),
+                                   k_cache.data_ptr(), v_cache.data_ptr(), b, h, t, d, cache_rows(k_cache, v_cache),
+                                   cache_len),
             "kv_write")
 
 
@@ -225,7 +241,7 @@ def rope_kv_write(qkv: torch.Tensor, q_out: torch.Tensor, k_cache: torch.Tensor,
     N.check(_lib().minitp_rope_kv_write(N.stream(), N.dtype_code(qkv.dtype), qkv.data_ptr(), qkv.stride(1),
                                         q_out.data_ptr(), k_cache.data_ptr(), v_cache.data_ptr(), cos.data_ptr(),
                                         sin.data_ptr(), positions.contiguous().data_ptr(), cos.shape[0], b, t, hq,
-                                        hkv, d, k_cache.shape[2], cache_len), "rope_kv_write")
+                                        hkv, d, cache_rows(k_cache, v_cache), cache_len), "rope_kv_write")
 
 
 def attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cache_len: int) -> torch.Tensor:
@@ -233,7 +249,7 @@ def attention(q: torch.Tensor, k_cache: torch.Tensor, v_cache: torch.Tensor, cac
     N.require_gpu(q, k_cache, v_cache, what="attention")
     q = q.contiguous()
     b, t, hq, d = q.shape
-    hkv, s = k_cache.shape[1], k_cache.shape[2]
+    hkv, s = k_cache.shape[1], cache_rows(k_cache, v_cache)
     out = torch.empty(b, t, hq * d, dtype=q.dtype, device=q.device)
     nbytes = _lib().minitp_attention_workspace_bytes(b, t, hq, hkv, d, s)
     ws = N.scratch(q.device, "attention", nbytes)

@@ -102,10 +102,11 @@ class _Program:
                 "o_proj+residual, norm+gate/up+SwiGLU, down+residual; norm+LM head+argmax partials, merge")
 
     def check_cache(self, kv: KVCache, batch: int) -> None:
-        """The cache must be this model's: [L, batch, Hkv, S, D] in the model
-        dtype on the model's device (the kernels index it with those sizes)."""
+        """The cache must be this model's: [L, batch, Hkv, S, D] buffers (S =
+        its capacity) in the model dtype on the model's device (the kernels
+        index it with those sizes)."""
         c = self.cfg
-        want = (c.num_layers, batch, c.kv_heads, kv.max_seq_len, c.head_dim)
+        want = (c.num_layers, batch, c.kv_heads, kv.capacity, c.head_dim)
         for buf in (kv.k_buf, kv.v_buf):
             if tuple(buf.shape) != want or buf.dtype != self.dtype or buf.device != self.device or \
                     not buf.is_contiguous():
@@ -222,9 +223,9 @@ class TPQwen2ForCausalLM(nn.Module):
         kv.check_room(t)
         all_rows = t > 1 and not last_only
         logits = torch.empty(b, t if all_rows else 1, self.cfg.vocab_size, dtype=prog.dtype, device=dev)
-        ws = prog.forward_ws(b * t, b, kv.max_seq_len)
+        ws = prog.forward_ws(b * t, b, kv.capacity)
         step = N.Qwen2Step(ids.data_ptr(), ids.stride(0), pos.data_ptr(), b, t, kv.seq_len, kv.k_buf.data_ptr(),
-                           kv.v_buf.data_ptr(), kv.max_seq_len, logits.data_ptr(), 1 if all_rows else 0,
+                           kv.v_buf.data_ptr(), kv.capacity, logits.data_ptr(), 1 if all_rows else 0,
                            N.ptr(next_tok), next_tok.stride(0) if next_tok is not None else 0, ws.data_ptr(),
                            ws.numel(), *(eos or (None, 0, 0, None)))
         N.check(N.lib().minitp_qwen2_forward(prog.handle, N.stream(), ctypes.byref(step)), "qwen2_forward")
@@ -245,9 +246,9 @@ class TPQwen2ForCausalLM(nn.Module):
             raise ValueError(f"decode_step: pos must be one int64 position, got {pos.dtype} of {pos.numel()}")
         self._check_kv(prog, kv_cache, b)
         kv_cache.check_room(1)
-        ws = prog.decode_workspace(b, kv_cache.max_seq_len)
+        ws = prog.decode_workspace(b, kv_cache.capacity)
         step = N.Qwen2Step(tok.data_ptr(), tok.stride(0), pos.data_ptr(), b, 1, kv_cache.seq_len,
-                           kv_cache.k_buf.data_ptr(), kv_cache.v_buf.data_ptr(), kv_cache.max_seq_len,
+                           kv_cache.k_buf.data_ptr(), kv_cache.v_buf.data_ptr(), kv_cache.capacity,
                            logits.data_ptr(), 0, N.ptr(next_tok), next_tok.stride(0) if next_tok is not None else 0,
                            ws.data_ptr(), ws.numel(), *(eos or (None, 0, 0, None)))
         N.check(N.lib().minitp_qwen2_decode(prog.handle, N.stream(), ctypes.byref(step)), "qwen2_decode")

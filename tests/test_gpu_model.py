@@ -102,6 +102,27 @@ def test_tiny_fp32_greedy_ids_bitexact_and_logits(name):
     assert (prefill - torch.from_numpy(fx["prefill_logits"])).abs().max().item() <= FP32_LOGIT_ATOL
 
 
+def test_generation_lengths_sharing_a_cache_capacity_replay_one_graph():
+    """Caches of 28 and 32 positions both hold 32 rows (the capacity the
+    kernels index by), so the second generation replays the decode graph the
+    first recorded: its 16 + 8 ids are the fixture's, and the shorter run's ids
+    are the longer's prefix (fixed-length greedy)."""
+    from minitp.generation import generate_greedy
+
+    fx = _fixture("tiny_fp32")
+    shape, state = _oracle_state("TINY", torch.float32)
+    model = _model_from_state(shape, state, torch.float32)
+    prompt = torch.from_numpy(fx["prompt"]).to(DEV)
+    n = fx["ids"].shape[1] - prompt.shape[1]  # 16 new tokens: a 24-row cache of capacity 32
+    full = generate_greedy(model, prompt, n, early_stop=False)
+    short = generate_greedy(model, prompt, n - 4, early_stop=False)  # 20 rows, capacity 32
+    longer = generate_greedy(model, prompt, n + 8, early_stop=False)  # 32 rows, capacity 32
+    assert np.array_equal(full.cpu().numpy(), fx["ids"])
+    assert torch.equal(short, full[:, : prompt.shape[1] + n - 4])
+    assert torch.equal(longer[:, : full.shape[1]], full)
+    model.program().check_decode()
+
+
 def test_tiny_bf16_logits_teacher_forced():
     fx = _fixture("tiny_bf16")
     shape, state = _oracle_state("TINY", torch.float32)

@@ -6,8 +6,13 @@ is recorded, later calls patch the first kernel's per-call values and replay. Ev
 positions, cache_len, the caches and the logits buffer from the step state, so
 a replay with other prompts, other caches or a non-empty cache must give the
 bits of a direct run (MINITP_PREFILL_GRAPH=0 when the program is created).
-Shapes: the 0.5B layer shape with 2 layers, batch 1, 3 (LM-head GEMV + argmax)
-and 8 (LM-head GEMM, then argmax)."""
+Shapes: the 0.5B layer shape with 2 layers at batch 1 and 3 (LM-head GEMV +
+argmax) and 8 (the MFMA norm + LM-head GEMV of 5-32 rows, then argmax); the
+fused GEMV path of a short prompt (batch 1, 8 tokens); the LM-head GEMM of 40
+rows; and prompts whose products run on the 256 x 256 tile GEMM with its split
+last round (0.5B, 3 x 256 tokens) and its every-tile split (the 7B layer
+shape at 512 tokens), whose partials and arrival words live in the step
+state."""
 
 import dataclasses
 
@@ -18,10 +23,10 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-def _models(monkeypatch):
+def _models(monkeypatch, shape="qwen2.5-0.5b"):
     from minitp import synthetic
 
-    cfg = dataclasses.replace(synthetic.SHAPES["qwen2.5-0.5b"], num_hidden_layers=2)
+    cfg = dataclasses.replace(synthetic.SHAPES[shape], num_hidden_layers=2)
     graphed = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device=DEV, seed=0)
     direct = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device=DEV, seed=0)
     monkeypatch.setenv("MINITP_PREFILL_GRAPH", "0")
@@ -80,6 +85,25 @@ def test_prefill_graph_replays_match_direct_runs_bitwise(batch, monkeypatch):
     torch.cuda.synchronize()
     assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
     assert torch.isfinite(outs[0][1]).all()
+
+
+@pytest.mark.parametrize("shape,batch,tokens", [("qwen2.5-0.5b", 1, 8), ("qwen2.5-0.5b", 40, 8),
+                                                ("qwen2.5-0.5b", 3, 256), ("qwen2.5-7b", 1, 512)])
+def test_prefill_graph_replays_other_launch_paths_bitwise(shape, batch, tokens, monkeypatch):
+    """Three prompts of one shape (direct, recorded, replayed) against direct
+    runs, bitwise: the fused short-prompt GEMVs (1 x 8), the LM-head GEMM
+    that reads its logits pointer from the step state (40 rows), and the tile
+    GEMM's split last round and every-tile split (3 x 256 at 0.5B; 512 tokens
+    at 7B), which keep their arrival words and partials in the step state."""
+    cfg, (graphed, _), (direct, _) = _models(monkeypatch, shape)
+    g = torch.Generator().manual_seed(batch * 1000 + tokens)
+    prompts = [torch.randint(0, cfg.vocab_size, (batch, tokens), generator=g).to(DEV) for _ in range(3)]
+    got = _run(graphed, prompts)
+    ref = _run(direct, prompts)
+    for i, (a, b) in enumerate(zip(got, ref)):
+        assert torch.isfinite(a.float()).all(), i
+        assert torch.equal(a, b), (i, (a.float() - b.float()).abs().max().item())
+    assert not torch.equal(got[0], got[4])
 
 
 def test_prefill_graph_all_position_logits_bitwise(monkeypatch):

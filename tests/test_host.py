@@ -96,6 +96,19 @@ def test_kv_cache_host_validation():
         KVCache(2, 1, 2, 16, 8, torch.float32, torch.device("cpu"), init="bogus")
     kv = KVCache(2, 1, 2, 16, 8, torch.float32, torch.device("cpu"), init="zeros")
     assert kv.k[1].shape == (1, 2, 8, 16) and kv.k_buf.shape == (2, 1, 2, 8, 16)
+    # capacity: max_seq_len rounded up to a power of two (multiples of 8192 past it);
+    # the views keep the reference shape and every bound stays max_seq_len
+    from minitp.kv_cache import cache_capacity
+
+    assert [cache_capacity(n) for n in (1, 8, 9, 200, 384, 2560, 8192, 8193, 20000)] == \
+        [1, 8, 16, 256, 512, 4096, 8192, 16384, 24576]
+    kv2 = KVCache(3, 2, 2, 16, 200, torch.float32, torch.device("cpu"))
+    assert kv2.capacity == 256 and kv2.k_buf.shape == (3, 2, 2, 256, 16)
+    assert kv2.k[2].shape == (2, 2, 200, 16) and kv2.k[2].stride(1) == 256 * 16
+    kv2.seq_len = 199
+    kv2.check_room(1)
+    with pytest.raises(ValueError, match="overflow"):
+        kv2.check_room(2)
     assert kv.k[1].data_ptr() == kv.k_buf[1].data_ptr()  # views into one buffer
     with pytest.raises(ValueError, match="overflow"):
         kv.update(0, torch.zeros(1, 2, 9, 16), torch.zeros(1, 2, 9, 16))
