@@ -4,20 +4,30 @@
 // bf16-rounded products with rows j and I + j of W (mlp.py:34-38,
 // fused.py:102-104; F.linear semantics of fused.py:57-61 / linear.py:117).
 //
-// Block tile 256 x 256 x (K steps of 64), 512 threads = 8 waves in a 2 x 4
-// grid, each wave owning a 128 x 64 output tile as 4 x 2 fragments of
-// 32 x 32 (16 fp32 accumulators per lane each). Both operands are
-// K-contiguous (x rows, W rows), the layout the MFMA operands want:
+// Block tile 256 x 256 x (K steps of 64), 1,024 threads = 16 waves in a
+// 4 x 4 grid (four per SIMD), each wave owning a 64 x 64 output tile as 2 x 2
+// fragments of 32 x 32 (16 fp32 accumulators per lane each). Both operands
+// are K-contiguous (x rows, W rows), the layout the MFMA operands want:
 //   v_mfma_f32_32x32x16_bf16: lane l holds A[l % 32][8 (l / 32) + 0..7] and
 //   B[8 (l / 32) + 0..7][l % 32]; accumulator register r of lane l is
 //   D[8 (r / 4) + 4 (l / 32) + r % 4][l % 32].
 // K steps are staged in LDS (two buffers, 64 KiB each: 256 rows of x and of
 // W, 128 bytes per row), each 16-byte chunk c of row r stored at chunk
-// position c ^ (r & 7), so the 32 lanes reading one fragment column spread
-// over all banks. The global loads of the step after next are in flight in
-// registers while a step's MFMAs run (one LDS barrier per step). Loads are
-// buffer loads: rows past M or N and K past the matrix read zeros, so no load
-// is predicated.
+// position c ^ ((r / 2) & 7), so the lanes reading one fragment column spread
+// over all banks. The operands go from global memory straight into LDS
+// (gfx950's buffer_load_dwordx4 ... lds: no registers, no LDS write
+// instructions), the next step's while a step's MFMAs run, one barrier per
+// step. Loads are buffer loads: rows past M or N read zeros, so no load is
+// predicated.
+//
+// Measured at the 7B prefill shapes (16,384 rows): against 8 waves of
+// 128 x 64 with register staging, gate/up 3.86 -> 3.67 ms, QKV 0.48 -> 0.46,
+// down unchanged (1.91); the matrix pipes are then busy 71 % of the cycles at
+// the clock the part holds (1.63 GHz; 72 % with the operand loads left out,
+// at 1.81 GHz). Slower: the same 8-wave layout with DMA staging (no faster),
+// plus an L2 prefetch of the step after next split over the blocks sharing a
+// panel (5-8 % slower), 4 waves of 128 x 128 (20 % slower), 16 waves with
+// register staging (gate/up 6.8 ms).
 //
 // Tile order: blocks are dispatched to the 8 XCDs round-robin (block b runs on
 // XCD b % 8, each XCD with its own L2). Block b takes tile (b % 8) * per_xcd +
@@ -42,24 +52,40 @@ constexpr int ROWB = TK * 2;  // bytes per row per stage
 constexpr int A_BYTES = TM * ROWB, B_BYTES = TN * ROWB;
 constexpr int STAGE_BYTES = A_BYTES + B_BYTES;  // 64 KiB
 constexpr int LDS_TILE_BYTES = 2 * STAGE_BYTES;
-constexpr int CPR = ROWB / 16;  // 16-byte chunks per row per stage
-constexpr int GROUP_M = 8;  // row tiles per group (4 and 16 measured no better)
-// waves along N: 4 (8 waves of 128 x 64, two per SIMD; the default) or 2
-// (4 waves of 128 x 128, one per SIMD: a third less LDS traffic, but 15 %
-// slower at the 7B prefill shapes, one wave per SIMD hiding no latency)
+constexpr int GROUP_M = 8;  // row tiles per group (4 measured the same, 16 and 32 slower)
+// waves along N and M: 4 x 4 (64 x 64 wave tiles, four waves per SIMD; the
+// default), 4 x 2 (128 x 64, two per SIMD) or 2 x 2 (128 x 128, one per SIMD)
 #ifndef MINITP_TILE_WAVES_N
 #define MINITP_TILE_WAVES_N 4
 #endif
-// waves along M: 2 (128-row wave tiles; the default) or 4 (64 x 64 wave
-// tiles, 16 waves, four per SIMD)
 #ifndef MINITP_TILE_WAVES_M
-#define MINITP_TILE_WAVES_M 2
+#define MINITP_TILE_WAVES_M 4
 #endif
-constexpr uint32_t OOB_OFF = 0xffffffffu;
 
-__device__ __forceinline__ uint4 tile_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
-  const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
-  return make_uint4(v.x, v.y, v.z, v.w);
+// A row past the matrix: its voffset, plus any K offset in soffset, stays
+// past the resource's range (operands are below DMA_OOB bytes and K below
+// 2^27), so the load writes zeros.
+constexpr uint32_t DMA_OOB = 0xF0000000u;
+
+// Words of a raw buffer resource over [base, base + bytes) (SGPRs).
+__device__ __forceinline__ u32x4 rsrc_words(const void* base, uint32_t bytes) {
+  const uint64_t p = (uint64_t)base;
+  u32x4 r;
+  r.x = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)p);
+  r.y = (uint32_t)__builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));  // stride 0
+  r.z = (uint32_t)__builtin_amdgcn_readfirstlane(bytes);
+  r.w = 0x00020000u;
+  return r;
+}
+
+// 16 bytes per lane from the resource at voff + soff into LDS: lane l's
+// bytes land at LDS byte address lds_addr + 16 l (lds_addr wave-uniform, in
+// m0); an offset past the range writes zeros. Issued as asm so that the
+// compiler does not make every later LDS read wait for these loads: the
+// kernel waits for them itself (vmcnt(0) before the barrier that publishes
+// the stage).
+__device__ __forceinline__ void dma16(u32x4 r, uint32_t voff, uint32_t soff, uint32_t lds_addr) {
+  asm volatile("buffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voff), "s"(r), "s"(soff), "{m0}"(lds_addr) : "memory");
 }
 
 // byte offset of chunk c of row r inside an operand's stage buffer. The LDS
@@ -86,8 +112,6 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_tile_kernel(const
   constexpr int TTHREADS = 64 * WAVES_M * WAVES_N;
   constexpr int WTM = TM / WAVES_M, FM = WTM / 32;  // wave tile rows
   constexpr int WTN = TN / WAVES_N, FN = WTN / 32;
-  constexpr int LPT_A = TM * CPR / TTHREADS;  // chunks per thread per stage (x)
-  constexpr int LPT_B = TN * CPR / TTHREADS;  // (W)
   extern __shared__ __attribute__((aligned(16))) char lds[];
   const int b = blockIdx.x;
   // blocks [0, 8 per_xcd): tiles [0, full_tiles), one each, in
@@ -129,47 +153,7 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_tile_kernel(const
     return n < N ? n : -1;
   };
 
-  const __amdgpu_buffer_rsrc_t xr = span_rsrc(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
   const int64_t w_rows = EPI == TILE_SWIGLU ? 2LL * N : (int64_t)N;
-  const __amdgpu_buffer_rsrc_t wr = span_rsrc(w, (uint32_t)(w_rows * K * 2));
-
-  // per-thread load slots: chunk q = tid + i * 512 -> row q / CPR, chunk q % CPR
-  uint32_t a_base[LPT_A], b_base[LPT_B];
-  int a_lds[LPT_A], b_lds[LPT_B], a_c[LPT_A], b_c[LPT_B];
-#pragma unroll
-  for (int i = 0; i < LPT_A; ++i) {
-    const int q = tid + i * TTHREADS, r = q / CPR, c = q % CPR;
-    a_base[i] = m0 + r < M ? (uint32_t)(((int64_t)(m0 + r) * ldx + c * 8) * 2) : OOB_OFF;
-    a_lds[i] = lds_off(r, c);
-    a_c[i] = c * 8;
-  }
-#pragma unroll
-  for (int i = 0; i < LPT_B; ++i) {
-    const int q = tid + i * TTHREADS, r = q / CPR, c = q % CPR;
-    const int wrow = w_row(r);
-    b_base[i] = wrow >= 0 ? (uint32_t)(((int64_t)wrow * K + c * 8) * 2) : OOB_OFF;
-    b_lds[i] = A_BYTES + lds_off(r, c);
-    b_c[i] = c * 8;
-  }
-
-  // The NCH 16-byte chunks a thread moves per K step: 0 .. LPT_A - 1 of x,
-  // the rest of W; one register each.
-  constexpr int NCH = LPT_A + LPT_B;
-  uint4 rr[NCH];
-  auto load_chunk = [&](int i, int kstep) {
-    const int k0 = kstep * TK;
-    if (i < LPT_A) {
-      const bool ok = a_base[i] != OOB_OFF && k0 + a_c[i] < K;
-      rr[i] = tile_load16(xr, ok ? a_base[i] + (uint32_t)k0 * 2 : OOB_OFF);
-    } else {
-      const int j = i - LPT_A;
-      const bool ok = b_base[j] != OOB_OFF && k0 + b_c[j] < K;
-      rr[i] = tile_load16(wr, ok ? b_base[j] + (uint32_t)k0 * 2 : OOB_OFF);
-    }
-  };
-  auto stash_chunk = [&](int i, char* stage) {
-    *(uint4*)(stage + (i < LPT_A ? a_lds[i] : b_lds[i - LPT_A])) = rr[i];
-  };
 
   f32x16_g acc[FM][FN];
 #pragma unroll
@@ -183,31 +167,70 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_tile_kernel(const
   const int ar0 = wm * WTM + (lane & 31), br0 = wn * WTN + (lane & 31);
   const int half = lane >> 5;
 
-  // K step kt: the MFMAs read stage kt % 2; the registers hold step kt + 1,
-  // written to the other stage two chunks per 16-wide substep, and each
-  // freed register takes the same chunk of step kt + 2. Fragment reads run
-  // one substep ahead of the MFMAs that use them (two register sets). The
-  // stage writes and global loads sit between the two halves of a substep's
-  // MFMAs, so the matrix pipe has work queued while they issue; one barrier
-  // per step.
+  // A stage is 64 pieces of 1 KiB, each 8 rows x 128 bytes of one operand
+  // (x rows 0..255, then W rows), in lds_off's layout: lane l of the wave
+  // moving a piece takes the row's chunk whose swizzled position is l % 8, so
+  // the piece lands as one contiguous KiB. Wave w moves pieces w PPW ..
+  // w PPW + PPW - 1 of every stage.
+  constexpr int NWAVES = WAVES_M * WAVES_N, PIECES = (TM + TN) / 8, PPW = PIECES / NWAVES;
+  static_assert(PIECES % NWAVES == 0 && TM % 8 == 0, "pieces must split evenly over the waves");
+  const int wv = __builtin_amdgcn_readfirstlane(wave);  // uniform: the pieces' operand and LDS address
+  const u32x4 xq = rsrc_words(x, (uint32_t)(((int64_t)(M - 1) * ldx + K) * 2));
+  const u32x4 wq = rsrc_words(w, (uint32_t)(w_rows * K * 2));
+  const uint32_t lds0 = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) char*)lds;
+  uint32_t voff[PPW];  // byte offset of the lane's chunk at k = 0 (DMA_OOB: a row past the matrix)
+  int kc[PPW];         // its first k
+#pragma unroll
+  for (int j = 0; j < PPW; ++j) {
+    const int p = wv * PPW + j, is_w = p >= TM / 8;
+    const int r = 8 * (is_w ? p - TM / 8 : p) + (lane >> 3);
+    const int c = (lane & 7) ^ ((r >> MINITP_TILE_SWZ_SHIFT) & 7);
+    kc[j] = c * 8;
+    if (!is_w) {
+      voff[j] = m0 + r < M ? (uint32_t)(((int64_t)(m0 + r) * ldx + c * 8) * 2) : DMA_OOB;
+    } else {
+      const int wrow = w_row(r);
+      voff[j] = wrow >= 0 ? (uint32_t)(((int64_t)wrow * K + c * 8) * 2) : DMA_OOB;
+    }
+  }
+  auto issue = [&](int kstep, int stage) {
+    const int k0 = kstep * TK;
+    const uint32_t base = lds0 + stage * STAGE_BYTES;
+    if (k0 + TK <= K) {
+      const uint32_t so = (uint32_t)__builtin_amdgcn_readfirstlane(k0 * 2);
+#pragma unroll
+      for (int j = 0; j < PPW; ++j) {
+        const int p = wv * PPW + j;
+        dma16(p >= TM / 8 ? wq : xq, voff[j], so, (uint32_t)__builtin_amdgcn_readfirstlane(base + p * 1024));
+      }
+    } else {
+      // the K tail: chunks at or past K read zeros
+#pragma unroll
+      for (int j = 0; j < PPW; ++j) {
+        const int p = wv * PPW + j;
+        const uint32_t v = voff[j] != DMA_OOB && k0 + kc[j] < K ? voff[j] + (uint32_t)k0 * 2 : DMA_OOB;
+        dma16(p >= TM / 8 ? wq : xq, v, 0u, (uint32_t)__builtin_amdgcn_readfirstlane(base + p * 1024));
+      }
+    }
+  };
+
+  // K step kt: the MFMAs read stage kt % 2 while the pieces of step kt + 1
+  // load into the other stage; fragment reads run one 16-wide substep ahead
+  // of the MFMAs that use them (two register sets); one barrier per step.
   const int nk_all = (K + TK - 1) / TK;
   const int kper = (nk_all + tail_split - 1) / tail_split;
   const int kb = split_blk ? part * kper : 0;
   const int nk = split_blk ? min(nk_all, kb + kper) - kb : nk_all;  // steps of this block
-#pragma unroll
-  for (int i = 0; i < NCH; ++i) load_chunk(i, kb);
-#pragma unroll
-  for (int i = 0; i < NCH; ++i) stash_chunk(i, lds);
-#pragma unroll
-  for (int i = 0; i < NCH; ++i) load_chunk(i, kb + 1);
+  constexpr int KS = TK / 16;                                       // MFMA k substeps per step
+  issue(kb, 0);
+  __builtin_amdgcn_s_waitcnt(0x0F70);  // vmcnt(0)
   __syncthreads();
-  constexpr int KS = TK / 16;              // MFMA k substeps per step
-  constexpr int CH_PER_KS = NCH / KS;      // chunks moved per substep
-  static_assert(NCH % KS == 0, "chunks must split evenly over the substeps");
   for (int kt = 0; kt < nk; ++kt) {
+    // the next step's pieces go to the other stage, which every wave
+    // finished reading before the barrier that ended the previous step
+    if (kt + 1 < nk) issue(kb + kt + 1, (kt + 1) & 1);
     const char* sa = lds + (kt & 1) * STAGE_BYTES;
     const char* sb = sa + A_BYTES;
-    char* nxt = lds + ((kt + 1) & 1) * STAGE_BYTES;
     bf16x8_g av[2][FM], bv[2][FN];
     auto fetch = [&](int ks, bf16x8_g(&a)[FM], bf16x8_g(&bb)[FN]) {
       const int c = ks * 2 + half;
@@ -221,25 +244,12 @@ __global__ __launch_bounds__(64 * WAVES_M * WAVES_N) void gemm_tile_kernel(const
     for (int ks = 0; ks < KS; ++ks) {
       if (ks + 1 < KS) fetch(ks + 1, av[(ks + 1) & 1], bv[(ks + 1) & 1]);
 #pragma unroll
-      for (int i = 0; i < FM / 2; ++i)
-#pragma unroll
-        for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[ks & 1][i], bv[ks & 1][j], acc[i][j], 0, 0, 0);
-      __builtin_amdgcn_sched_barrier(0);
-      // unconditional: past the last step the loads read zeros (K bound) and
-      // land in a stage nothing reads, and the loop stays one basic block, so
-      // the compiler's load counting waits only for the chunk it stores
-#pragma unroll
-      for (int q = 0; q < CH_PER_KS; ++q) stash_chunk(ks * CH_PER_KS + q, nxt);
-#pragma unroll
-      for (int q = 0; q < CH_PER_KS; ++q) load_chunk(ks * CH_PER_KS + q, kb + kt + 2);
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int i = FM / 2; i < FM; ++i)
+      for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
           acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(av[ks & 1][i], bv[ks & 1][j], acc[i][j], 0, 0, 0);
     }
+    __builtin_amdgcn_s_waitcnt(0x0F70);  // this wave's pieces of step kt + 1 are in LDS
     __syncthreads();
   }
 
@@ -415,7 +425,7 @@ bool gemm_tile_split_supported(int64_t M, int64_t N, int64_t K, int64_t ldx, int
   const int64_t tiles = cdiv(M, TM) * cdiv(N, swiglu ? TN / 2 : TN);
   return M >= TM && M % TM == 0 && 2 * tiles <= device_cus() && cdiv(K, TK) >= 2 * SPLIT_MIN_STEPS && K % 8 == 0 &&
          ldx % 8 == 0 && ldx >= K && ldy >= N && M < (1LL << 31) && N < (1LL << 30) &&
-         ((M - 1) * ldx + K) * 2 < (1LL << 32) && w_rows * K * 2 < (1LL << 32);
+         ((M - 1) * ldx + K) * 2 < DMA_OOB && w_rows * K * 2 < DMA_OOB && K < (1LL << 27);
 }
 
 int launch_gemm_tile_split(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y,
@@ -432,7 +442,7 @@ bool gemm_tile_supported(int64_t M, int64_t N, int64_t K, int64_t ldx, int64_t l
   const int64_t w_rows = swiglu ? 2 * N : N;
   const int64_t tiles = cdiv(M, TM) * cdiv(N, swiglu ? TN / 2 : TN);
   return M >= TM && tiles >= 96 && K % 8 == 0 && ldx % 8 == 0 && ldx >= K && ldy >= N && M < (1LL << 31) &&
-         N < (1LL << 30) && ((M - 1) * ldx + K) * 2 < (1LL << 32) && w_rows * K * 2 < (1LL << 32);
+         N < (1LL << 30) && ((M - 1) * ldx + K) * 2 < DMA_OOB && w_rows * K * 2 < DMA_OOB && K < (1LL << 27);
 }
 
 int launch_gemm_tile(hipStream_t st, const void* x, int64_t ldx, const void* w, const void* bias, void* y, int64_t ldy,
