@@ -36,14 +36,14 @@ class RMSNorm(nn.Module):
         super().__init__()
         self.weight = nn.Parameter(torch.ones(hidden_size) if init_weights else torch.empty(hidden_size))
         self.eps = eps
-        # The reference only special-cases "functional" (F.rms_norm); every
-        # other value runs the reference math (layer.py:36-42).
+        # The reference runs F.rms_norm for "functional" and its own fp32 math
+        # for every other value (layer.py:36-42). F.rms_norm (torch 2.10)
+        # computes in fp32 as well and rounds once, after the weight: the same
+        # rounding as the reference math, so one kernel serves both (checked
+        # against F.rms_norm on the device in the GPU tests).
         self.implementation = "reference"
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if self.implementation == "functional":
-            raise NotImplementedError("RMSNorm.implementation='functional' (F.rms_norm rounding) is not built; "
-                                      "use 'reference'")
         return K.rmsnorm(x, self.weight, self.eps)
 
 
@@ -187,10 +187,7 @@ class TPQwen2ForCausalLM(nn.Module):
         for layer in self.model.layers:
             if not (layer.self_attn.use_fused_qkv and layer.mlp.use_fused_gateup):
                 return False
-            if "functional" in (layer.input_layernorm.implementation, layer.post_attention_layernorm.implementation):
-                return False
-        return self.model.norm.implementation != "functional" and \
-            self.model.embed_tokens.weight.dtype in (torch.float32, torch.bfloat16)
+        return self.model.embed_tokens.weight.dtype in (torch.float32, torch.bfloat16)
 
     def program(self) -> _Program:
         dev = self.model.embed_tokens.weight.device

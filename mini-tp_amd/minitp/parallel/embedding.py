@@ -2,9 +2,9 @@
 
 The embedding gathers rows with a HIP kernel; the LM head is a HIP linear;
 ``distributed_argmax`` at tp_size == 1 is the first-maximum argmax
-(embedding.py:146-147) as a HIP reduction. The multi-rank exchange encodings
-(bitpack / fp32 / fp64 / split, embedding.py:149-213) need collectives and
-are not built; their host-side guard still raises as the reference does.
+(embedding.py:146-147) as a HIP reduction. A context with tp_size > 1 is
+refused at construction: the multi-rank exchange encodings (bitpack / fp32 /
+fp64 / split, embedding.py:149-213) have no counterpart here.
 """
 
 from __future__ import annotations
@@ -13,9 +13,8 @@ import torch
 import torch.nn as nn
 
 from minitp import kernels as K
-from minitp.distributed import all_gather
 from minitp.distributed.context import ParallelContext
-from minitp.parallel.linear import shard_range
+from minitp.parallel.linear import require_tp1, shard_range
 
 ARGMAX_ENCODING = "bitpack"
 
@@ -26,6 +25,7 @@ class VocabParallelEmbedding(nn.Module):
         self.vocab_size = vocab_size
         self.hidden_size = hidden_size
         self.ctx = ctx
+        require_tp1(ctx, "VocabParallelEmbedding")
         self.vocab_start, self.vocab_end = shard_range(vocab_size, ctx.tp_rank, ctx.tp_size)
         n = self.vocab_end - self.vocab_start
         self.weight = nn.Parameter(torch.zeros(n, hidden_size) if init_weights else torch.empty(n, hidden_size))
@@ -34,8 +34,6 @@ class VocabParallelEmbedding(nn.Module):
         self.tp1_fast = True
 
     def forward(self, ids: torch.Tensor) -> torch.Tensor:
-        if self.ctx.tp_size != 1:
-            raise NotImplementedError("vocab-sharded embedding needs an all-reduce: tp_size > 1 is not built")
         return K.embedding(ids, self.weight)
 
 
@@ -47,26 +45,18 @@ class VocabParallelLMHead(nn.Module):
         self.hidden_size = hidden_size
         self.ctx = ctx
         self.gather_logits = gather_logits
+        require_tp1(ctx, "VocabParallelLMHead")
         self.vocab_start, self.vocab_end = shard_range(vocab_size, ctx.tp_rank, ctx.tp_size)
         n = self.vocab_end - self.vocab_start
         self.weight = nn.Parameter(torch.zeros(n, hidden_size) if init_weights else torch.empty(n, hidden_size))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        local = K.linear(x, self.weight)
-        if not self.gather_logits or self.ctx.tp_size == 1:
-            return local
-        out = torch.empty(*local.shape[:-1], self.vocab_size, dtype=local.dtype, device=local.device)
-        return all_gather(out, local, self.ctx.process_group)
+        # one rank holds the whole vocabulary: gathered logits are the local ones
+        return K.linear(x, self.weight)
 
     @torch.no_grad()
     def distributed_argmax(self, local_logits: torch.Tensor, encoding: str | None = None) -> torch.Tensor:
         """Greedy id [..., 1] (long): first maximum, NaN wins, like torch.argmax."""
-        if self.ctx.tp_size == 1:
-            return K.argmax(local_logits).unsqueeze(-1)
-        enc = encoding or ARGMAX_ENCODING
-        if enc == "fp32" and self.vocab_size > 2 ** 24:
-            raise ValueError(f"fp32 argmax encoding cannot represent ids >= 2**24 exactly "
-                             f"(vocab_size={self.vocab_size}); use the bitpack encoding")
-        if enc not in ("bitpack", "fp32", "fp64", "split"):
-            raise ValueError(f"unknown argmax encoding {enc!r}")
-        raise NotImplementedError("distributed argmax over tp_size > 1 needs an all-gather: not built on MI355X")
+        # one rank holds the whole vocabulary: the reference returns the local
+        # argmax before any encoding is looked at (embedding.py:146-147)
+        return K.argmax(local_logits).unsqueeze(-1)

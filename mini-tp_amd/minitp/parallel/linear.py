@@ -2,7 +2,9 @@
 
 Same constructor signatures, parameter names, layouts ([out, in] weights)
 and divisibility errors as the reference. Forward runs the minitp GEMV (few
-rows) or MFMA GEMM (many rows) kernel; at tp_size == 1 no collective runs.
+rows) or MFMA GEMM (many rows) kernel. This build runs tensor parallelism 1
+only: a context with tp_size > 1 is refused at construction, so no layer
+ever shards, splits its input or calls a collective.
 """
 
 from __future__ import annotations
@@ -11,8 +13,12 @@ import torch
 import torch.nn as nn
 
 from minitp import kernels as K
-from minitp.distributed import all_gather, all_reduce
 from minitp.distributed.context import ParallelContext
+
+
+def require_tp1(ctx: ParallelContext, what: str) -> None:
+    if ctx.tp_size != 1:
+        raise NotImplementedError(f"{what} at tp_size={ctx.tp_size}: this MI355X build runs tensor parallelism 1 only")
 
 
 def shard_range(size: int, tp_rank: int, tp_size: int) -> tuple[int, int]:
@@ -30,6 +36,7 @@ class ColumnParallelLinear(nn.Module):
         super().__init__()
         if output_size % ctx.tp_size != 0:
             raise ValueError(f"output_size={output_size} not divisible by tp_size={ctx.tp_size}")
+        require_tp1(ctx, "ColumnParallelLinear")
         self.input_size = input_size
         self.output_size = output_size
         self.ctx = ctx
@@ -45,11 +52,8 @@ class ColumnParallelLinear(nn.Module):
             nn.init.kaiming_uniform_(self.weight, a=5 ** 0.5)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        local = K.linear(x, self.weight, self.bias)
-        if not self.gather_output or self.ctx.tp_size == 1:
-            return local
-        out = torch.empty(*local.shape[:-1], self.output_size, dtype=local.dtype, device=local.device)
-        return all_gather(out, local, self.ctx.process_group)
+        # one rank holds every output column: gathering is the identity
+        return K.linear(x, self.weight, self.bias)
 
 
 class RowParallelLinear(nn.Module):
@@ -61,6 +65,7 @@ class RowParallelLinear(nn.Module):
         super().__init__()
         if input_size % ctx.tp_size != 0:
             raise ValueError(f"input_size={input_size} not divisible by tp_size={ctx.tp_size}")
+        require_tp1(ctx, "RowParallelLinear")
         self.input_size = input_size
         self.output_size = output_size
         self.ctx = ctx
@@ -76,11 +81,8 @@ class RowParallelLinear(nn.Module):
             nn.init.kaiming_uniform_(self.weight, a=5 ** 0.5)
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        if not self.input_is_parallel and self.ctx.tp_size > 1:
-            x = x.split(self.input_size_local, dim=-1)[self.ctx.tp_rank]
-        local = K.linear(x, self.weight)  # partial sum; bias after the reduce
-        if self.reduce_output and self.ctx.tp_size > 1:
-            local = all_reduce(local, self.ctx.process_group)
-        if self.bias is not None:
-            local = K.add_bias(local, self.bias)
-        return local
+        # one rank holds every input column, so the product is the whole sum
+        # (the reduction is the identity); the bias is still added after it,
+        # as its own rounding step
+        y = K.linear(x, self.weight)
+        return K.add_bias(y, self.bias) if self.bias is not None else y

@@ -17,10 +17,10 @@ by :func:`copy_plan` and carried out by three executors that cannot disagree
   crosses PCIe in the checkpoint's dtype and is converted on the device;
 * ``"legacy"``: the whole state dict is loaded on the host, then sliced.
 
-The shard arithmetic (``shard_len``, ``kv_head_rows``) is the reference's
-rank layout (weight_loader.py:40-67), kept for any ``tp``; the model itself
-runs ``tp_size == 1`` only, so at tp 1 every plan entry is a whole tensor.
-Every parameter must be written by the plan, or loading raises.
+The model runs ``tp_size == 1`` only, so every plan entry is a whole
+checkpoint tensor (the reference's per-rank slicing, weight_loader.py:40-67,
+has no counterpart here and a plan for another ``tp`` is refused). Every
+parameter must be written by the plan, or loading raises.
 """
 
 from __future__ import annotations
@@ -41,33 +41,6 @@ SINGLE_FILE = "model.safetensors"
 
 
 # ---------------------------------------------------------------------------
-# rank layout (weight_loader.py:40-67)
-
-
-def shard_len(size: int, rank: int, tp: int) -> tuple[int, int]:
-    """(start, length) of rank ``rank``'s contiguous share of ``size``; the
-    first ``size % tp`` ranks hold one extra element."""
-    base, extra = divmod(size, tp)
-    return rank * base + min(rank, extra), base + int(rank < extra)
-
-
-def kv_head_rows(num_kv_heads: int, head_dim: int, rank: int, tp: int) -> tuple[int, int]:
-    """(first row, rows) of this rank's K (or V) projection: a contiguous
-    block of heads when ``tp`` divides the KV heads, else the one head that
-    ``tp // num_kv_heads`` consecutive ranks replicate."""
-    if num_kv_heads % tp == 0:
-        per_rank = num_kv_heads // tp
-        return rank * per_rank * head_dim, per_rank * head_dim
-    replicas = tp // num_kv_heads
-    return (rank // replicas) * head_dim, head_dim
-
-
-def fused_qkv_local_sizes(cfg: ModelConfig, tp: int) -> tuple[int, int]:
-    """(q rows, k rows) = (v rows) of one rank's packed QKV parameter."""
-    return (cfg.num_attention_heads // tp) * cfg.head_dim, max(1, cfg.num_key_value_heads // tp) * cfg.head_dim
-
-
-# ---------------------------------------------------------------------------
 # the copy plan
 
 
@@ -83,16 +56,15 @@ class Copy:
 
 
 def copy_plan(cfg: ModelConfig, rank: int = 0, tp: int = 1, qkv_bias: bool = True) -> list[Copy]:
-    """Every copy that fills one rank's parameters from a Qwen2 checkpoint."""
+    """Every copy that fills the parameters from a Qwen2 checkpoint (tp 1)."""
+    if tp != 1 or rank != 0:
+        raise NotImplementedError(f"copy plan for rank {rank} of tp {tp}: this build loads tensor parallelism 1 only")
     plan: list[Copy] = []
     h, inter = cfg.hidden_size, cfg.intermediate_size
-    v0, vn = shard_len(cfg.vocab_size, rank, tp)
-    plan.append(Copy("model.embed_tokens.weight", 0, "model.embed_tokens.weight", 0, v0, vn))
-    q_rows, kv_rows = fused_qkv_local_sizes(cfg, tp)
-    q0, qn = shard_len(cfg.num_attention_heads * cfg.head_dim, rank, tp)
-    k0, kn = kv_head_rows(cfg.num_key_value_heads, cfg.head_dim, rank, tp)
-    h0, hn = shard_len(h, rank, tp)  # o_proj input columns
-    i0, inn = shard_len(inter, rank, tp)
+    plan.append(Copy("model.embed_tokens.weight", 0, "model.embed_tokens.weight", 0, 0, cfg.vocab_size))
+    q_rows = cfg.num_attention_heads * cfg.head_dim
+    kv_rows = cfg.num_key_value_heads * cfg.head_dim
+    q0, qn, k0, kn, h0, hn, i0, inn = 0, q_rows, 0, kv_rows, 0, h, 0, inter
     for i in range(cfg.num_hidden_layers):
         p = f"model.layers.{i}."
         for norm in ("input_layernorm", "post_attention_layernorm"):
@@ -106,11 +78,11 @@ def copy_plan(cfg: ModelConfig, rank: int = 0, tp: int = 1, qkv_bias: bool = Tru
                 plan.append(Copy(f"{p}self_attn.qkv_proj.bias", row, f"{src}.bias", 0, start, n, optional=True))
         plan.append(Copy(f"{p}self_attn.o_proj.weight", 0, f"{p}self_attn.o_proj.weight", 1, h0, hn))
         plan.append(Copy(f"{p}mlp.gate_up_proj.weight", 0, f"{p}mlp.gate_proj.weight", 0, i0, inn))
-        plan.append(Copy(f"{p}mlp.gate_up_proj.weight", inter // tp, f"{p}mlp.up_proj.weight", 0, i0, inn))
+        plan.append(Copy(f"{p}mlp.gate_up_proj.weight", inter, f"{p}mlp.up_proj.weight", 0, i0, inn))
         plan.append(Copy(f"{p}mlp.down_proj.weight", 0, f"{p}mlp.down_proj.weight", 1, i0, inn))
     plan.append(Copy("model.norm.weight", 0, "model.norm.weight", 0, 0, h))
     if not cfg.tie_word_embeddings:
-        plan.append(Copy("lm_head.weight", 0, "lm_head.weight", 0, v0, vn))
+        plan.append(Copy("lm_head.weight", 0, "lm_head.weight", 0, 0, cfg.vocab_size))
     return plan
 
 

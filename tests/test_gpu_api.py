@@ -197,3 +197,43 @@ def test_fused_projections_equal_separate_ones(rows):
     ug, uu = gu.forward_unfused(x.to(DEV))
     torch.testing.assert_close(gate, ug, atol=1e-5, rtol=1e-5)
     torch.testing.assert_close(up, uu, atol=1e-5, rtol=1e-5)
+
+
+@torch.inference_mode()
+@pytest.mark.parametrize("hidden", [896, 3584])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_functional_rmsnorm_matches_f_rms_norm(hidden, dtype):
+    """implementation="functional" runs F.rms_norm in the reference
+    (layer.py:36-38); here the native kernel serves it. Same rounding (fp32
+    math, one rounding after the weight); the sum of squares may add in
+    another order, so a bf16 result may sit one unit in the last place away."""
+    from minitp.layer import RMSNorm
+
+    g = torch.Generator(device=DEV).manual_seed(hidden)
+    x = (torch.randn(33, hidden, device=DEV, generator=g) * 3).to(dtype)
+    norm = RMSNorm(hidden, 1e-6).to(DEV, dtype)
+    norm.weight.copy_((torch.rand(hidden, device=DEV, generator=g) + 0.5).to(dtype))
+    norm.implementation = "functional"
+    got = norm(x)
+    want = F.rms_norm(x, (hidden,), norm.weight, 1e-6)
+    if dtype == torch.float32:
+        torch.testing.assert_close(got, want, atol=1e-6, rtol=1e-5)
+    else:
+        ulp = torch.finfo(torch.bfloat16).eps * want.float().abs().clamp_min(2 ** -126)
+        assert ((got.float() - want.float()).abs() <= ulp).all()
+        assert (got == want).float().mean().item() > 0.99
+
+
+@torch.inference_mode()
+def test_functional_norms_keep_the_native_program_and_its_ids():
+    from minitp.generation import generate_greedy
+
+    model = _tiny()
+    ids = torch.tensor([[5, 60, 7, 99, 120, 33]], device=DEV)
+    want = generate_greedy(model, ids, 6)
+    for layer in model.model.layers:
+        layer.input_layernorm.implementation = "functional"
+        layer.post_attention_layernorm.implementation = "functional"
+    model.model.norm.implementation = "functional"
+    assert model.native_path()
+    assert torch.equal(generate_greedy(model, ids, 6), want)

@@ -130,15 +130,16 @@ def test_rotary_tables_equal_reference_math_and_range_check():
         rot.apply(q, q, torch.tensor([128 + 5]))
 
 
-def test_argmax_encoding_guard_fires_before_any_collective():
+def test_parallel_layers_refuse_tensor_parallel_contexts():
     from minitp.distributed.context import ParallelContext
-    from minitp.parallel.embedding import VocabParallelLMHead
+    from minitp.parallel.embedding import VocabParallelEmbedding, VocabParallelLMHead
+    from minitp.parallel.linear import ColumnParallelLinear, RowParallelLinear
 
-    head = VocabParallelLMHead(4, 21_000_000, ParallelContext(0, 0, 2, 0, 2, torch.device("cpu"), None),
-                               init_weights=False)
-    logits = torch.full((1, 16), -1e30)
-    with pytest.raises(ValueError, match=r"2\*\*24"):
-        head.distributed_argmax(logits, encoding="fp32")
+    ctx = ParallelContext(0, 0, 2, 0, 2, torch.device("cpu"), None)
+    for make in (lambda: ColumnParallelLinear(8, 16, ctx), lambda: RowParallelLinear(16, 8, ctx),
+                 lambda: VocabParallelEmbedding(16, 4, ctx), lambda: VocabParallelLMHead(4, 16, ctx)):
+        with pytest.raises(NotImplementedError, match="tensor parallelism 1"):
+            make()
 
 
 def test_tp_greater_than_one_is_refused():

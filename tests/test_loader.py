@@ -203,27 +203,6 @@ def test_config_json_of_qwen25_05b(tmp_path):
 # rank layout (weight_loader.py:40-67)
 
 
-def test_shard_len_covers_every_row_once():
-    from minitp.weight_loader import shard_len
-
-    assert [shard_len(10, r, 3) for r in range(3)] == [(0, 4), (4, 3), (7, 3)]
-    for size in (1, 7, 64, 151936):
-        for tp in (1, 2, 3, 8):
-            parts = [shard_len(size, r, tp) for r in range(tp)]
-            assert parts[0][0] == 0 and sum(n for _, n in parts) == size
-            assert all(a + n == b for (a, n), (b, _) in zip(parts, parts[1:]))
-            assert max(n for _, n in parts) - min(n for _, n in parts) <= 1
-
-
-def test_kv_head_rows_shard_and_replicate():
-    from minitp.weight_loader import kv_head_rows
-
-    # 4 KV heads of 8 rows over 2 ranks: two heads each
-    assert [kv_head_rows(4, 8, r, 2) for r in range(2)] == [(0, 16), (16, 16)]
-    # 2 KV heads over 8 ranks: ranks 0-3 replicate head 0, ranks 4-7 head 1
-    assert [kv_head_rows(2, 8, r, 8) for r in range(8)] == [(0, 8)] * 4 + [(8, 8)] * 4
-
-
 def test_copy_plan_at_tp1_is_whole_tensors():
     from minitp.weight_loader import copy_plan
 
@@ -234,21 +213,8 @@ def test_copy_plan_at_tp1_is_whole_tensors():
         assert c.start == 0 and c.length == t.shape[c.dim], c
 
 
-def test_copy_plan_at_tp2_matches_the_rank_layout():
-    """Rank 1 of 2 with 2 KV heads: the second half of q rows, KV head 1,
-    the second half of o_proj's and down's input columns."""
+def test_copy_plan_refuses_other_tensor_parallel_layouts():
     from minitp.weight_loader import copy_plan
 
-    cfg = _cfg(kv_heads=2, layers=1)
-    plan = {(c.dest, c.src): c for c in copy_plan(cfg, rank=1, tp=2)}
-    q = plan[("model.layers.0.self_attn.qkv_proj.weight", "model.layers.0.self_attn.q_proj.weight")]
-    k = plan[("model.layers.0.self_attn.qkv_proj.weight", "model.layers.0.self_attn.k_proj.weight")]
-    v = plan[("model.layers.0.self_attn.qkv_proj.weight", "model.layers.0.self_attn.v_proj.weight")]
-    assert (q.dest_row, q.start, q.length) == (0, 16, 16)
-    assert (k.dest_row, k.start, k.length) == (16, 8, 8) and (v.dest_row, v.start, v.length) == (24, 8, 8)
-    o = plan[("model.layers.0.self_attn.o_proj.weight", "model.layers.0.self_attn.o_proj.weight")]
-    assert (o.dim, o.start, o.length) == (1, 16, 16)
-    up = plan[("model.layers.0.mlp.gate_up_proj.weight", "model.layers.0.mlp.up_proj.weight")]
-    assert (up.dest_row, up.start, up.length) == (24, 24, 24)
-    emb = plan[("model.embed_tokens.weight", "model.embed_tokens.weight")]
-    assert (emb.start, emb.length) == (12, 12)
+    with pytest.raises(NotImplementedError):
+        copy_plan(_cfg(), rank=1, tp=2)
