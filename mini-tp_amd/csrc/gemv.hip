@@ -2054,7 +2054,7 @@ int pick_k(hipStream_t st, const GemvArgs& a) {
 template <typename T, int PRO, int EPI>
 int pick_m(hipStream_t st, const GemvArgs& a) {
   if constexpr (sizeof(T) == 2) {
-    if (a.M > 4) return launch_mfma<PRO, EPI>(st, a);
+    if (a.M >= MF_MIN_ROWS) return launch_mfma<PRO, EPI>(st, a);
   }
   if (a.M == 1) return pick_k<T, 1, PRO, EPI>(st, a);
   if (a.M == 2) return pick_k<T, 2, PRO, EPI>(st, a);
@@ -2127,7 +2127,7 @@ int launch_gemv_part_swiglu(hipStream_t st, int dtype, const GemvArgs& a_in) {
 
 int64_t gemv_split_part_bytes(int64_t M) {
   const int64_t reg = (int64_t)SPLIT_MAX_TUPLES * SPLIT_MAX_SEG * 4 * R * sizeof(float);
-  return M > 4 && M <= 32 ? std::max<int64_t>(reg, 16LL << 20) : reg;
+  return M >= MF_MIN_ROWS && M <= 32 ? std::max<int64_t>(reg, 16LL << 20) : reg;
 }
 
 // Block count (and so partial count per row) of the LM-head argmax GEMV.
@@ -2138,8 +2138,8 @@ int64_t gemv_argmax_partials(int64_t N) { return std::min<int64_t>(cdiv(cdiv(N, 
 // that stages the input in LDS (up to 80 KiB). Other shapes run the GEMM.
 bool gemv_supported(int dtype, int64_t M, int64_t K) {
   const int v = dtype == MINITP_F32 ? 4 : 8;
-  // bf16 rows 5..32 run the MFMA form (K a multiple of 8, rows under 2 GiB)
-  if (dtype == MINITP_BF16 && M >= 5 && M <= 32) return K % v == 0 && K * 2 < (1LL << 31);
+  // bf16 rows MF_MIN_ROWS..32 run the MFMA form (K a multiple of 8, rows under 2 GiB)
+  if (gemv_mfma_rows(dtype, M)) return K % v == 0 && K * 2 < (1LL << 31);
   if (M < 1 || M > 4 || K % v != 0) return false;
   const int64_t nchunk = K / v;
   if (nchunk <= 128) return true;
@@ -2147,11 +2147,11 @@ bool gemv_supported(int dtype, int64_t M, int64_t K) {
   return M == 1 && K * 4 <= 80 * 1024;
 }
 
-// The RMSNorm prologue holds a wave's whole K range: on the MFMA form (bf16
-// rows 5..32) that is K <= 4 waves x 8 steps x 32.
+// The RMSNorm prologue holds a wave's whole K range: on the MFMA form that
+// is K <= 4 waves x 8 steps x 32.
 bool gemv_norm_supported(int dtype, int64_t M, int64_t K) {
   if (!gemv_supported(dtype, M, K)) return false;
-  return M <= 4 || K <= 4 * 32 * MF_ONE;
+  return !gemv_mfma_rows(dtype, M) || K <= 4 * 32 * MF_ONE;
 }
 
 int launch_gemv(hipStream_t st, int dtype, int pro, int epi, const GemvArgs& a) {

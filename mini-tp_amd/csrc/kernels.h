@@ -109,9 +109,16 @@ int launch_gemv_part_swiglu(hipStream_t st, int dtype, const GemvArgs& a);
 int64_t gemv_argmax_partials(int64_t N);
 int launch_gemv(hipStream_t st, int dtype, int pro, int epi, const GemvArgs& a);
 bool gemv_supported(int dtype, int64_t M, int64_t K);
+// bf16 rows MF_MIN_ROWS..32 run the MFMA forms (16-row operand tiles, rows
+// past M read as zeros); fewer rows and fp32 the register forms. At 3 and 4
+// rows the register forms' per-lane row budget leaves long rows (the 0.5B
+// down projection, K = 4,864) to the prompt GEMM: 0.5B decode at batch 4
+// took 1.44 ms a step that way, batch 5 on the MFMA forms 0.92.
+constexpr int MF_MIN_ROWS = 3;
+inline bool gemv_mfma_rows(int dtype, int64_t M) { return dtype == MINITP_BF16 && M >= MF_MIN_ROWS && M <= 32; }
 // Bytes of GemvArgs::split_part for products of M input rows (the register
 // form's SPLIT_MAX_TUPLES x SPLIT_MAX_SEG x 4 x 4 floats; 16 MiB for the
-// MFMA form's 16 x 32 tiles at M = 5..32).
+// MFMA form's 16 x 32 tiles).
 int64_t gemv_split_part_bytes(int64_t M);
 // ... and with the RMSNorm prologue (PRO_NORM)
 bool gemv_norm_supported(int dtype, int64_t M, int64_t K);

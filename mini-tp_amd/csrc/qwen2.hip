@@ -398,9 +398,9 @@ struct Qwen2Program {
         g.M = M;
         g.N = H;
         g.K = q_rows();
-        // (5..32 rows: the unsplit MFMA form; its one round trip beats the
+        // (MFMA rows: the unsplit MFMA form; its one round trip beats the
         // split form's three extra at K = 896)
-        if (M <= 4) split_bufs(g);
+        if (!gemv_mfma_rows(c.dtype, M)) split_bufs(g);
         if ((rc = launch_gemv(st, c.dtype, PRO_NONE, EPI_RESID, g))) return rc;
       } else {
         if ((rc = launch_gemm(st, c.dtype, w.attn, q_rows(), L(l, MINITP_W_O), nullptr, w.x, H, M, H, q_rows(),
@@ -456,7 +456,7 @@ struct Qwen2Program {
       }
     }
     // ---- final norm, LM head, greedy pick ----------------------------------------
-    if (!s.logits_all && gemv_supported(c.dtype, B, H) && B <= 4) {
+    if (!s.logits_all && gemv_supported(c.dtype, B, H) && !gemv_mfma_rows(c.dtype, B)) {
       GemvArgs g{};
       g.x = (const char*)w.x + (T - 1) * H * es();  // last position of each row
       g.ldx = T * H;
@@ -471,8 +471,8 @@ struct Qwen2Program {
       g.part_idx = w.part_idx;
       return launch_gemv(st, c.dtype, PRO_NORM, EPI_ARGMAX, g);
     }
-    if (!s.logits_all && B > 4 && gemv_norm_supported(c.dtype, B, H)) {
-      // batched rows (bf16, 5..32): the final norm and the LM head in one
+    if (!s.logits_all && gemv_mfma_rows(c.dtype, B) && gemv_norm_supported(c.dtype, B, H)) {
+      // batched rows (bf16 MFMA rows): the final norm and the LM head in one
       // MFMA GEMV whose blocks each normalize the rows once for many tuples,
       // storing the step's logits (read from the step state), then the argmax
       GemvArgs g{};

@@ -2,7 +2,7 @@
 layer runs the same kernels): the 7B decode shape with its untied LM head,
 batch-32 decode at the 0.5B shape (GEMM + batched attention paths) and the 7B
 prefill shape (MFMA GEMMs and prefill attention at 2 x 256 tokens), and
-batch-3 decode at the 0.5B shape (the small-batch GEMV path).
+batch-3 decode at the 0.5B shape (the MFMA GEMV forms at their fewest rows).
 
 Fixtures: tests/golden/{q7b2,q05b2_b32,q7b1_b2_p256}_*.npz, written by
 tests/golden/make_reference_vectors.py from the oracle (which reproduces the
