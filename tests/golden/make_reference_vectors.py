@@ -4,7 +4,7 @@ Run in the build container only (the reference is not present on GPU hosts):
 
     python tests/golden/make_reference_vectors.py tiny_fp32 tiny_bf16 q05b_fp32 q05b_bf16
     python tests/golden/make_reference_vectors.py q7b2_fp32 q7b2_bf16 q05b2_b32_fp32 q05b2_b32_bf16 q7b1_b2_p256_bf16
-    python tests/golden/make_reference_vectors.py q05b_b32_bf16 q7b_bf16 q7b_b4_p640_bf16
+    python tests/golden/make_reference_vectors.py q05b_b32_fp32 q05b_b32_bf16 q7b_fp32 q7b_bf16 q7b_b4_p640_bf16
     python tests/golden/make_reference_vectors.py tiny_chunked_fp32 tiny_eos_fp32
 
 It imports the reference package from /root/reference, builds
@@ -53,7 +53,9 @@ ORACLE_CASES = {
     # every layer, shorter prompts: batch-32 decode at the 0.5B shape, 7B
     # batch-1 decode, 7B 4-row prefill long enough for the long-prompt
     # attention kernel (4 x 28 heads x 5 query tiles of 128)
+    "q05b_b32_fp32": ("QWEN05B", 24, torch.float32, 32, 24, 8),
     "q05b_b32_bf16": ("QWEN05B", 24, torch.bfloat16, 32, 24, 8),
+    "q7b_fp32": ("QWEN7B", 28, torch.float32, 1, 16, 8),
     "q7b_bf16": ("QWEN7B", 28, torch.bfloat16, 1, 16, 8),
     "q7b_b4_p640_bf16": ("QWEN7B", 28, torch.bfloat16, 4, 640, 2),
 }

@@ -3,10 +3,10 @@ layer runs the same kernels): the 7B decode shape with its untied LM head,
 batch-32 decode at the 0.5B shape (GEMM + batched attention paths) and the 7B
 prefill shape (MFMA GEMMs and prefill attention at 2 x 256 tokens), and
 batch-3 decode at the 0.5B shape (the MFMA GEMV forms at their fewest rows).
-Three more cases run every layer of the model with shorter prompts than the
-workloads: batch-32 decode at the 0.5B shape (24 layers), 7B batch-1 decode
-and the 7B 4-row prefill at 640 tokens (28 layers; the long-prompt attention
-kernel serves it).
+More cases run every layer of the model with shorter prompts than the
+workloads: batch-32 decode at the 0.5B shape (24 layers, fp32 and bf16), 7B
+batch-1 decode (28 layers, fp32 and bf16) and the 7B 4-row prefill at 640
+tokens (bf16; the long-prompt attention kernel serves it).
 
 Fixtures: tests/golden/{q7b2,q05b2_b32,q05b2_b3,q7b1_b2_p256,q05b_b32,q7b,q7b_b4_p640}_*.npz, written by
 tests/golden/make_reference_vectors.py from the oracle (which reproduces the
@@ -36,7 +36,9 @@ CASES = {  # fixture: (shape key, layers, dtype)
     "q05b2_b3_bf16": ("qwen2.5-0.5b", 2, torch.bfloat16),
     "q7b1_b2_p256_bf16": ("qwen2.5-7b", 1, torch.bfloat16),
     # every layer of the model (shorter prompts than the workloads)
+    "q05b_b32_fp32": ("qwen2.5-0.5b", 24, torch.float32),
     "q05b_b32_bf16": ("qwen2.5-0.5b", 24, torch.bfloat16),
+    "q7b_fp32": ("qwen2.5-7b", 28, torch.float32),
     "q7b_bf16": ("qwen2.5-7b", 28, torch.bfloat16),
     "q7b_b4_p640_bf16": ("qwen2.5-7b", 28, torch.bfloat16),
 }
@@ -50,7 +52,7 @@ def _model(name):
     return synthetic.build_synthetic_model(cfg, dtype=dtype, device=DEV, seed=0)
 
 
-@pytest.mark.parametrize("name", ["q7b2_fp32", "q05b2_b32_fp32"])
+@pytest.mark.parametrize("name", ["q7b2_fp32", "q05b2_b32_fp32", "q05b_b32_fp32", "q7b_fp32"])
 def test_fp32_greedy_ids_exact_and_logits(name):
     from minitp.generation import generate_greedy
 
