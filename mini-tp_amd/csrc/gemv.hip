@@ -1016,7 +1016,7 @@ constexpr int mf_wave_stage() { return MF_X_STAGE > NT * MF_W_STAGE ? MF_X_STAGE
 template <int NT>
 constexpr int mf_stage_bytes() { return 4 * mf_wave_stage<NT>(); }
 
-template <int PRO, int EPI, int KSPLIT, int NT, int NB, bool MULTI>
+template <int PRO, int EPI, int KSPLIT, int NT, int NB, bool MULTI, bool HV = false>
 __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
   // A wave owns NT tuples that share each A fragment it loads, over a K
   // range of steps of 32. !MULTI: the range fits one batch of NB steps and
@@ -1024,7 +1024,12 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
   // kernel waits one memory round trip; the RMSNorm scale comes from the
   // same input registers. MULTI: batches of NB steps, each batch's loads
   // issued while the previous one is multiplied (no norm prologue).
+  // HV (half rows): a block takes one 16-row half of the input rows (one A
+  // fragment: half the input loads, norm work and MFMAs); blocks b and b + 8,
+  // on one XCD, share a tuple, so its weights come from that XCD's L2 the
+  // second time.
   constexpr int SLOTS = 4 / KSPLIT;
+  constexpr int NF = HV ? 1 : 2;  // A fragments (16-row halves) a block multiplies
   constexpr uint32_t OOBW = 0xffffffffu;
   static_assert(!(MULTI && PRO == PRO_NORM), "the norm prologue needs the K range in one batch");
   __shared__ float nrm[4][32];
@@ -1033,7 +1038,10 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
   const int kw = wave % KSPLIT, slot = wave / KSPLIT;
   const int M = (int)a.M;
   const int64_t K = a.K;
-  const int64_t t0 = ((int64_t)blockIdx.x * SLOTS + slot) * NT;
+  const int half = HV ? (int)((blockIdx.x >> 3) & 1) : 0;
+  const int64_t tblk = HV ? ((int64_t)(blockIdx.x >> 4) << 3) | (blockIdx.x & 7) : (int64_t)blockIdx.x;
+  const int64_t t0 = (tblk * SLOTS + slot) * NT;
+  auto frow = [&](int f) { return HV ? 16 * half : 16 * f; };  // first input row of fragment f
   const int64_t ntup = num_tuples16<EPI>(a);
   const int nidx = lane & 15, kq = lane >> 4;
   const int64_t w_rows = EPI == EPI_SWIGLU ? 2 * a.N : a.N;
@@ -1051,9 +1059,9 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
     const int64_t wrow = nidx < P16 ? ra[j] + nidx : rb[j] + (nidx - P16);
     wbase[j] = live && row_valid<EPI>(wrow, a) ? (uint32_t)(wrow * K * 2) : OOBW;
   }
-  const int m0 = nidx, m1 = 16 + nidx;
+  const int m0 = frow(0) + nidx, m1 = 16 + nidx;
   const uint32_t xb0 = m0 < M ? (uint32_t)((int64_t)m0 * a.ldx * 2) : OOBW;
-  const uint32_t xb1 = m1 < M ? (uint32_t)((int64_t)m1 * a.ldx * 2) : OOBW;
+  const uint32_t xb1 = !HV && m1 < M ? (uint32_t)((int64_t)m1 * a.ldx * 2) : OOBW;
   const int64_t nsteps = cdiv(K, 32), per = cdiv(nsteps, KSPLIT);
   const int64_t s_begin = kw * per, s_end = std::min(nsteps, s_begin + per);
   auto off = [&](uint32_t base, int64_t s) -> uint32_t {
@@ -1071,7 +1079,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       b.xa[i] = span_load16<0>(xr, off(xb0, s0 + i));
-      b.xc[i] = span_load16<0>(xr, off(xb1, s0 + i));
+      if constexpr (!HV) b.xc[i] = span_load16<0>(xr, off(xb1, s0 + i));
       if constexpr (PRO == PRO_NORM) b.nw[i] = span_load16<0>(nr, off(0u, s0 + i));
     }
   };
@@ -1083,12 +1091,13 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
   auto consume = [&](Batch& b) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
-      const bf16x8_m aa = __builtin_bit_cast(bf16x8_m, b.xa[i]), ac = __builtin_bit_cast(bf16x8_m, b.xc[i]);
+      const bf16x8_m aa = __builtin_bit_cast(bf16x8_m, b.xa[i]);
+      const bf16x8_m ac = __builtin_bit_cast(bf16x8_m, HV ? b.xa[i] : b.xc[i]);
 #pragma unroll
       for (int j = 0; j < NT; ++j) {
         const bf16x8_m bw = __builtin_bit_cast(bf16x8_m, b.w[i][j]);
         acc[j][0] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aa, bw, acc[j][0], 0, 0, 0);
-        acc[j][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac, bw, acc[j][1], 0, 0, 0);
+        if constexpr (!HV) acc[j][1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ac, bw, acc[j][1], 0, 0, 0);
       }
     }
   };
@@ -1104,8 +1113,8 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
   if constexpr (!MULTI) {
     // input rows first (the norm prologue needs them first), then weights
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const int q = lane + 64 * t, r = q >> 5, c = q & 31;
+    for (int t = 0; t < 8 * NF; ++t) {
+      const int q = lane + 64 * (t + 8 * half), r = q >> 5, c = q & 31;  // rows frow(0) ..
       const bool ok = r < M && c < nch;
       xl[t] = span_load16<0>(xr, ok ? (uint32_t)(((int64_t)r * a.ldx + kb + 8 * c) * 2) : OOBW);
     }
@@ -1141,10 +1150,10 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
     if constexpr (EPI == EPI_RESID) {
       const bf16* aux = (const bf16*)a.aux;
 #pragma unroll
-      for (int h = 0; h < 2; ++h)
+      for (int h = 0; h < NF; ++h)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int m = h * 16 + 4 * kq + r;
+          const int m = frow(h) + 4 * kq + r;
           const int mm = m < M ? m : 0;
           sv[j][h * 8 + r] = load_f32<bf16>(aux, mm * a.ldy + (oka ? row_a : 0));
           sv[j][h * 8 + 4 + r] = load_f32<bf16>(aux, mm * a.ldy + (okb ? row_b : 0));
@@ -1170,15 +1179,15 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
     };
 #pragma unroll
-    for (int t = 0; t < 16; ++t) {
-      const int q = lane + 64 * t;
+    for (int t = 0; t < 8 * NF; ++t) {
+      const int q = lane + 64 * (t + 8 * half);
       *(uint4*)(xs_lds + mf_slot(q >> 5, q & 31)) = xl[t];
     }
     wave_sync();
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       b0.xa[i] = *(const uint4*)(xs_lds + mf_slot(m0, 4 * i + kq));
-      b0.xc[i] = *(const uint4*)(xs_lds + mf_slot(m1, 4 * i + kq));
+      if constexpr (!HV) b0.xc[i] = *(const uint4*)(xs_lds + mf_slot(m1, 4 * i + kq));
     }
     wave_sync();
 #pragma unroll
@@ -1201,28 +1210,30 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
 #pragma unroll
       for (int i = 0; i < NB; ++i) {
         ss0 = dot_chunk<bf16>(b0.xa[i], nullptr, b0.xa[i], ss0);
-        ss1 = dot_chunk<bf16>(b0.xc[i], nullptr, b0.xc[i], ss1);
+        if constexpr (!HV) ss1 = dot_chunk<bf16>(b0.xc[i], nullptr, b0.xc[i], ss1);
       }
       ss0 += __shfl_xor(ss0, 16);
       ss0 += __shfl_xor(ss0, 32);
-      ss1 += __shfl_xor(ss1, 16);
-      ss1 += __shfl_xor(ss1, 32);
+      if constexpr (!HV) {
+        ss1 += __shfl_xor(ss1, 16);
+        ss1 += __shfl_xor(ss1, 32);
+      }
       if (kq == 0) {
         nrm[wave][m0] = ss0;
-        nrm[wave][m1] = ss1;
+        if constexpr (!HV) nrm[wave][m1] = ss1;
       }
       __syncthreads();
       float u0 = 0.f, u1 = 0.f;
       for (int k = 0; k < KSPLIT; ++k) {
         u0 += nrm[slot * KSPLIT + k][m0];
-        u1 += nrm[slot * KSPLIT + k][m1];
+        if constexpr (!HV) u1 += nrm[slot * KSPLIT + k][m1];
       }
       const float r0 = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(u0, (float)K), a.eps)));
-      const float r1 = __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(u1, (float)K), a.eps)));
+      const float r1 = HV ? 0.f : __fdiv_rn(1.0f, __fsqrt_rn(add_rn(__fdiv_rn(u1, (float)K), a.eps)));
 #pragma unroll
       for (int i = 0; i < NB; ++i) {
         b0.xa[i] = norm_chunk(b0.xa[i], b0.nw[i], r0);
-        b0.xc[i] = norm_chunk(b0.xc[i], b0.nw[i], r1);
+        if constexpr (!HV) b0.xc[i] = norm_chunk(b0.xc[i], b0.nw[i], r1);
       }
     }
     consume(b0);
@@ -1240,7 +1251,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < NT; ++j) {
       red[wave][j][0][lane] = acc[j][0];
-      red[wave][j][1][lane] = acc[j][1];
+      if constexpr (!HV) red[wave][j][1][lane] = acc[j][1];
     }
     __syncthreads();
     // every wave adds the K-split tiles in wave order (the same sums in
@@ -1249,7 +1260,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
 #pragma unroll
     for (int j = 0; j < NT; ++j)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < NF; ++h) {
         f32x4_m v = red[slot * KSPLIT][j][h][lane];
         for (int k = 1; k < KSPLIT; ++k) v += red[slot * KSPLIT + k][j][h][lane];
         acc[j][h] = v;
@@ -1261,7 +1272,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       pa0[r] = __shfl_xor(acc[j][0][r], 8);
-      pa1[r] = __shfl_xor(acc[j][1][r], 8);
+      pa1[r] = HV ? 0.f : __shfl_xor(acc[j][1][r], 8);
     }
     if (t0 + j >= ntup || nidx >= P16) continue;
     const int p = nidx;
@@ -1279,11 +1290,11 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
       side[3] = sv[j][5];
     }
 #pragma unroll
-    for (int h = 0; h < 2; ++h)
+    for (int h = 0; h < NF; ++h)
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         if (KSPLIT > 1 && r % KSPLIT != kw) continue;
-        const int m = h * 16 + 4 * kq + r;
+        const int m = frow(h) + 4 * kq + r;
         if (m >= M) continue;
         const float va = acc[j][h][r], vb = h ? pa1[r] : pa0[r];
         int64_t pos = 0;
@@ -1900,6 +1911,13 @@ int launch_mfma_split(hipStream_t st, const GemvArgs& a) {
 #ifndef MINITP_MF_LOOP_BLOCKS
 #define MINITP_MF_LOOP_BLOCKS 512
 #endif
+// Above 16 input rows the one-tuple MFMA form runs each 16-row half in a
+// block of its own (HV): half the input loads, RMSNorm work and MFMAs per
+// block on twice the blocks. 0.5B batch 32 (QKV 72 tuples, o_proj 56):
+// 1.123-1.125 -> 1.067-1.068 ms a step.
+#ifndef MINITP_MF_HALVES
+#define MINITP_MF_HALVES 1
+#endif
 template <int PRO, int EPI, int NT>
 int launch_mfma_nt(hipStream_t st, const GemvArgs& a, int64_t ntup) {
   const unsigned grid = (unsigned)cdiv(ntup, NT);
@@ -1920,11 +1938,19 @@ int launch_mfma_nt(hipStream_t st, const GemvArgs& a, int64_t ntup) {
     }
   }
   if (per_wave <= MF_ONE) {
-    auto kern = gemv_mfma_kernel<PRO, EPI, 4, NT, MF_ONE, false>;
     const int lds = mf_stage_bytes<NT>();
-    const int rc = ensure_lds_limit((const void*)kern, lds);
-    if (rc) return rc;
-    hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, a);
+    if (NT == 1 && a.M > 16 && MINITP_MF_HALVES) {
+      // each 16-row half of the input rows in a block of its own
+      auto kern = gemv_mfma_kernel<PRO, EPI, 4, NT, MF_ONE, false, true>;
+      const int rc = ensure_lds_limit((const void*)kern, lds);
+      if (rc) return rc;
+      hipLaunchKernelGGL(kern, dim3((unsigned)(cdiv(ntup, (int64_t)8) * 16)), dim3(256), lds, st, a);
+    } else {
+      auto kern = gemv_mfma_kernel<PRO, EPI, 4, NT, MF_ONE, false>;
+      const int rc = ensure_lds_limit((const void*)kern, lds);
+      if (rc) return rc;
+      hipLaunchKernelGGL(kern, dim3(grid), dim3(256), lds, st, a);
+    }
   } else if constexpr (PRO == PRO_NORM) {
     set_error("gemv: the RMSNorm prologue on MFMA serves K <= %d", 4 * 32 * MF_ONE);
     return MINITP_ERR_UNSUPPORTED;
