@@ -5,6 +5,7 @@ Run in the build container only (the reference is not present on GPU hosts):
     python tests/golden/make_reference_vectors.py tiny_fp32 tiny_bf16 q05b_fp32 q05b_bf16
     python tests/golden/make_reference_vectors.py q7b2_fp32 q7b2_bf16 q05b2_b32_fp32 q05b2_b32_bf16 q7b1_b2_p256_bf16
     python tests/golden/make_reference_vectors.py q05b_b32_fp32 q05b_b32_bf16 q7b_fp32 q7b_bf16 q7b_b4_p640_bf16
+    python tests/golden/make_reference_vectors.py q05b2_b20_bf16
     python tests/golden/make_reference_vectors.py tiny_chunked_fp32 tiny_eos_fp32
 
 It imports the reference package from /root/reference, builds
@@ -49,6 +50,7 @@ ORACLE_CASES = {
     "q05b2_b32_fp32": ("QWEN05B", 2, torch.float32, 32, 24, 8),  # batch-32 decode (GEMM + batched attention)
     "q05b2_b32_bf16": ("QWEN05B", 2, torch.bfloat16, 32, 24, 8),
     "q05b2_b3_bf16": ("QWEN05B", 2, torch.bfloat16, 3, 40, 24),  # small-batch decode GEMV path, batch 3
+    "q05b2_b20_bf16": ("QWEN05B", 2, torch.bfloat16, 20, 24, 8),  # 17-31 rows: the second 16-row half part-filled
     "q7b1_b2_p256_bf16": ("QWEN7B", 1, torch.bfloat16, 2, 256, 2),  # 7B prefill shape (MFMA GEMM + attention)
     # every layer, shorter prompts: batch-32 decode at the 0.5B shape, 7B
     # batch-1 decode, 7B 4-row prefill long enough for the long-prompt
