@@ -4,8 +4,8 @@ tests/test_loader_coverage.py of the reference.
 
 Each packed parameter is checked against ``torch.cat`` of the checkpoint's
 own tensors (the packing rule of fused.py:57-61, 102-104), the loaders
-against each other bit for bit, and the rank layout against hand-worked
-ranges.
+against each other bit for bit, and the copy plan at tensor parallelism 1
+(whole tensors; other layouts are refused).
 """
 
 import json
@@ -200,7 +200,7 @@ def test_config_json_of_qwen25_05b(tmp_path):
 
 
 # ---------------------------------------------------------------------------
-# rank layout (weight_loader.py:40-67)
+# the copy plan at tensor parallelism 1 (weight_loader.py:40-67 at tp_size 1)
 
 
 def test_copy_plan_at_tp1_is_whole_tensors():
