@@ -100,6 +100,10 @@ def parse(argv=None):
     ap.add_argument("--dominant-only", action="store_true",
                     help="only launch the dominant kernel, eagerly (no graphs), once per layer 4 times over, and "
                          "exit: the workload of the --pmc byte-counter passes")
+    ap.add_argument("--dominant-graph", type=int, default=0, metavar="REPS",
+                    help="only run the roofline's timing of the dominant kernel (one captured graph of a launch per "
+                         "layer, replayed REPS times), print its JSON and exit: the workload of the kernel-trace "
+                         "summary that the roofline's us_per_launch is checked against")
     ap.add_argument("--gemm", default="", metavar="M,N,K[,swiglu]",
                     help="only time one bf16 product y = x W^T (minitp_linear; swiglu: W is [2N, K] and y = "
                          "silu(gate) * up) 10 times after 3 warm-up calls, print one JSON line and exit")
@@ -346,7 +350,9 @@ def dominant_kernel(model, reps: int = 20) -> dict:
     launch re-reads a cache-resident matrix, no host launch cost), timed with
     HIP events on the stream the graph replays on. The kernel alone, not
     between its neighbours in the step: the step's own per-kernel durations
-    are in the rocprofv3 kernel-trace summary."""
+    are in the rocprofv3 kernel-trace summary of the decode, and
+    `--dominant-graph` runs this timing alone for a kernel-trace summary of
+    it."""
     import torch
 
     launch_all = _dominant_launcher(model)
@@ -669,11 +675,14 @@ def main(argv=None):
         with torch.inference_mode():
             print(json.dumps({"workload": args.workload, **measure_workload(args.workload)}), flush=True)
         return
-    if args.dominant_only or args.decode_only:
+    if args.dominant_only or args.decode_only or args.dominant_graph:
         from minitp.synthetic import QWEN05B, build_synthetic_model, synthetic_prompt
 
         with torch.inference_mode():
             model = build_synthetic_model(QWEN05B, dtype=torch.bfloat16, device="cuda", seed=0)
+            if args.dominant_graph:
+                print(json.dumps(dominant_kernel(model, args.dominant_graph)), flush=True)
+                return
             if args.dominant_only:
                 launch_all = _dominant_launcher(model)
                 for _ in range(4):
