@@ -419,3 +419,28 @@ def test_bench_windows_ttft_covers_prefill_and_selection():
     ids = torch.tensor([[5, 60, 7, 99, 120, 33]], device=DEV)
     prefill_s, ttft_s, sel_ms, steps = bench_one_iter(model, ids, 4)
     assert len(steps) == 3 and ttft_s + 1e-3 >= prefill_s + sel_ms / 1e3 - 2e-3
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_bench_timed_loop_produces_generate_greedy_ids(batch):
+    """The decode loop bench.py times (StepSource: a GenerationState with
+    last-position prompt logits and reused decode logits, append +
+    decode_step + select_next per step) computes the real generation: after
+    one generation its ids are generate_greedy's for the same prompt, and a
+    second back-to-back generation repeats them."""
+    import bench
+    from minitp.generation import generate_greedy
+
+    model = _synthetic("QWEN05B", torch.bfloat16)
+    g = torch.Generator().manual_seed(batch)
+    prompt = torch.randint(0, model.cfg.vocab_size, (batch, 16), generator=g).to(DEV)
+    new = 24
+    src = bench.StepSource(model, prompt, new)
+    src.run(new - 1)
+    first = src.state.out_ids.clone()
+    src.run(new - 1)
+    assert src.generations == 2
+    ref = generate_greedy(model, prompt, new, early_stop=False)
+    model.program().check_decode()
+    assert torch.equal(first, ref)
+    assert torch.equal(src.state.out_ids, ref)
