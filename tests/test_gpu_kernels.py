@@ -404,6 +404,29 @@ def test_decode_attention_bf16_grouped_mfma(ctx, b, hq, hkv, d):
     assert (err <= (ref.abs() + ref_abs) * 2 ** -8 + 1e-6).all(), err.max().item()
 
 
+@pytest.mark.parametrize("ctx,b,hq,hkv,d", [(16384, 1, 14, 2, 64), (32768, 1, 14, 2, 64), (32768, 1, 28, 4, 128),
+                                            (8192, 16, 14, 2, 64)])
+def test_decode_attention_bf16_long_context(ctx, b, hq, hkv, d):
+    """Decode at contexts up to the 0.5B / 7B RoPE table's 32,768 positions
+    (the most splits and the longest per-split spans; batch 16 x 2 KV heads on
+    the grouped MFMA form), against float64, cache rows past the context
+    poisoned; the bar of the grouped-form test."""
+    g = torch.Generator().manual_seed(ctx + b + d)
+    q = torch.randn(b, 1, hq, d, generator=g).bfloat16()
+    kc = torch.randn(b, hkv, ctx + 2, d, generator=g).bfloat16()
+    kc[:, :, ctx:] = float("nan")
+    vc = torch.randn(b, hkv, ctx + 2, d, generator=g).bfloat16()
+    vc[:, :, ctx:] = float("nan")
+    got = _k().attention(q.to(DEV), kc.to(DEV), vc.to(DEV), cache_len=ctx - 1).cpu().double()
+    ref = _ref_attention(q, kc, vc, ctx - 1)
+    vabs = vc.abs()
+    vabs[:, :, ctx:] = 0
+    ref_abs = _ref_attention(q, kc, vabs, ctx - 1)
+    err = (got - ref).abs()
+    assert torch.isfinite(got).all()
+    assert (err <= (ref.abs() + ref_abs) * 2 ** -8 + 1e-6).all(), err.max().item()
+
+
 def test_decode_attention_single_key_returns_v_and_zero_q_averages():
     b, hq, hkv, d, s = 1, 14, 2, 64, 10
     kc = torch.randn(b, hkv, s, d)
