@@ -232,3 +232,35 @@ def test_batch32_decode_to_context_2559_equals_whole_prompts():
     with torch.inference_mode():
         _teacher_forced(model, prompt, 2048, check)
     assert seen == [n - 1 for n in checkpoints]
+
+
+def test_long_context_decode_equals_whole_prompts():
+    """0.5B shapes (2 layers), batch 1, near the RoPE table's end: prefill(16,000)
+    plus 384 teacher-forced decode steps (contexts 16,001 .. 16,384: the o_proj
+    fold's attention walking 250+ chunks a block) against whole-prompt
+    prefills that end at the checkpoints 16,000, 16,001, 16,192 and 16,384
+    (the tile GEMM and the long-prompt attention; last rows)."""
+    from minitp import synthetic
+    from minitp.generation import GenerationState
+
+    cfg = dataclasses.replace(synthetic.QWEN05B, num_hidden_layers=2)
+    model = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device=DEV, seed=6)
+    prompt = synthetic.synthetic_prompt(cfg.vocab_size, 1, 16384, seed=11, device=DEV)
+    checkpoints = (16000, 16001, 16192, 16384)
+    whole = {}
+    for n in checkpoints:
+        whole[n - 1] = GenerationState(model, prompt[:, :n], 1, prefill_logits="last").prefill()[:, -1].float()
+        assert torch.isfinite(whole[n - 1]).all(), n
+    seen = []
+
+    def check(pos, logits):
+        if pos in whole:
+            err = (whole[pos] - logits.float()).abs().max().item()
+            print(f"batch 1, context {pos + 1}: max |logit diff| {err:.4f}")
+            assert torch.isfinite(logits).all() and err <= BF16_LOGIT_ATOL, pos
+            seen.append(pos)
+
+    with torch.inference_mode():
+        _teacher_forced(model, prompt, 16000, check)
+    model.program().check_decode()
+    assert seen == [n - 1 for n in checkpoints]
