@@ -5,6 +5,7 @@
 * explicit positions index the RoPE table like ``cos_cache[positions]``
   (rope.py:37-45): past the table raises IndexError, negative ones wrap;
 * a decode shape first run without a token pick still picks tokens later;
+* zero new tokens return the prompt after its forward (generation.py:150-171);
 * ColumnParallelLinear / RowParallelLinear / the fused projections equal
   ``F.linear`` (test_column_row_parallel.py:116-135,
   test_fused_projections.py:27-54), RowParallel's bias added after the
@@ -237,3 +238,18 @@ def test_functional_norms_keep_the_native_program_and_its_ids():
     model.model.norm.implementation = "functional"
     assert model.native_path()
     assert torch.equal(generate_greedy(model, ids, 6), want)
+
+
+@pytest.mark.parametrize("early_stop,eos", [(True, None), (False, None), (True, 5)])
+def test_zero_new_tokens_returns_the_prompt_after_its_prefill(early_stop, eos):
+    """generate_greedy(..., max_new_tokens=0) (generation.py:150-171): the
+    prompt's forward still runs (its K/V land in a caller's cache, which
+    advances by the prompt), no token is picked, and the prompt comes back."""
+    from minitp.generation import generate_greedy, make_kv_cache
+
+    model = _tiny()
+    prompt = torch.tensor([[3, 17, 256, 999, 41], [8, 1, 0, 77, 500]], device=DEV)
+    kv = make_kv_cache(model, 2, 5)
+    out = generate_greedy(model, prompt, 0, eos_token_id=eos, early_stop=early_stop, kv=kv)
+    assert torch.equal(out, prompt) and kv.seq_len == 5
+    assert torch.isfinite(kv.k[0][:, :, :5]).all() and torch.isfinite(kv.v[1][:, :, :5]).all()
