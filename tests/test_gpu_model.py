@@ -444,3 +444,23 @@ def test_bench_timed_loop_produces_generate_greedy_ids(batch):
     model.program().check_decode()
     assert torch.equal(first, ref)
     assert torch.equal(src.state.out_ids, ref)
+
+
+@pytest.mark.parametrize("batch,plen", [(1, 1), (2, 1), (1, 2)])
+def test_shortest_prompts_match_the_oracle(batch, plen):
+    """One- and two-token prompts (a one-token prompt's forward takes the
+    single-token launch sequence the decode steps use, with no cached rows),
+    tiny fp32: greedy ids equal the oracle's generate_greedy on the same
+    weights, bit for bit."""
+    from oracle import qwen2_ref as R
+
+    from minitp.generation import generate_greedy
+
+    shape, state = _oracle_state("TINY", torch.float32)
+    model = _model_from_state(shape, state, torch.float32)
+    g = torch.Generator().manual_seed(100 * batch + plen)
+    prompt = torch.randint(0, shape.vocab_size, (batch, plen), generator=g)
+    ref = R.generate_greedy(R.OracleQwen2(shape, state), prompt, 12, early_stop=False)
+    got = generate_greedy(model, prompt.to(DEV), 12, early_stop=False)
+    model.program().check_decode()
+    assert torch.equal(got.cpu(), ref)
