@@ -446,12 +446,13 @@ def test_bench_timed_loop_produces_generate_greedy_ids(batch):
     assert torch.equal(src.state.out_ids, ref)
 
 
-@pytest.mark.parametrize("batch,plen", [(1, 1), (2, 1), (1, 2)])
-def test_shortest_prompts_match_the_oracle(batch, plen):
+@pytest.mark.parametrize("batch,plen", [(1, 1), (2, 1), (1, 2), (40, 6), (64, 3)])
+def test_shortest_prompts_and_wide_batches_match_the_oracle(batch, plen):
     """One- and two-token prompts (a one-token prompt's forward takes the
-    single-token launch sequence the decode steps use, with no cached rows),
-    tiny fp32: greedy ids equal the oracle's generate_greedy on the same
-    weights, bit for bit."""
+    single-token launch sequence the decode steps use, with no cached rows)
+    and batches past the GEMV forms' 32 rows (40 and 64: decode products on
+    the GEMM), tiny fp32: greedy ids equal the oracle's generate_greedy on the
+    same weights, bit for bit."""
     from oracle import qwen2_ref as R
 
     from minitp.generation import generate_greedy
