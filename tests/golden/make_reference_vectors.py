@@ -51,6 +51,7 @@ ORACLE_CASES = {
     "q05b2_b32_bf16": ("QWEN05B", 2, torch.bfloat16, 32, 24, 8),
     "q05b2_b3_bf16": ("QWEN05B", 2, torch.bfloat16, 3, 40, 24),  # small-batch decode GEMV path, batch 3
     "q05b2_b20_bf16": ("QWEN05B", 2, torch.bfloat16, 20, 24, 8),  # 17-31 rows: the second 16-row half part-filled
+    "q05b2_b48_bf16": ("QWEN05B", 2, torch.bfloat16, 48, 24, 8),  # past 32 rows: decode products on the GEMM
     "q7b1_b2_p256_bf16": ("QWEN7B", 1, torch.bfloat16, 2, 256, 2),  # 7B prefill shape (MFMA GEMM + attention)
     # every layer, shorter prompts: batch-32 decode at the 0.5B shape, 7B
     # batch-1 decode, 7B 4-row prefill long enough for the long-prompt

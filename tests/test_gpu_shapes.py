@@ -2,14 +2,15 @@
 layer runs the same kernels): the 7B decode shape with its untied LM head,
 batch-32 decode at the 0.5B shape (GEMM + batched attention paths) and the 7B
 prefill shape (MFMA GEMMs and prefill attention at 2 x 256 tokens),
-batch-3 decode at the 0.5B shape (the MFMA GEMV forms at their fewest rows)
-and batch 20 (the one-tuple MFMA GEMVs' second 16-row half part-filled).
+batch-3 decode at the 0.5B shape (the MFMA GEMV forms at their fewest rows),
+batch 20 (the one-tuple MFMA GEMVs' second 16-row half part-filled) and batch
+48 (past the GEMV forms' 32 rows: the decode products on the GEMM).
 More cases run every layer of the model with shorter prompts than the
 workloads: batch-32 decode at the 0.5B shape (24 layers, fp32 and bf16), 7B
 batch-1 decode (28 layers, fp32 and bf16) and the 7B 4-row prefill at 640
 tokens (bf16; the long-prompt attention kernel serves it).
 
-Fixtures: tests/golden/{q7b2,q05b2_b32,q05b2_b3,q05b2_b20,q7b1_b2_p256,q05b_b32,q7b,q7b_b4_p640}_*.npz,
+Fixtures: tests/golden/{q7b2,q05b2_b32,q05b2_b3,q05b2_b20,q05b2_b48,q7b1_b2_p256,q05b_b32,q7b,q7b_b4_p640}_*.npz,
 written by tests/golden/make_reference_vectors.py from the oracle (which reproduces the
 reference bit for bit on the tiny and 0.5B cases). Bars as for the 0.5B
 model: fp32 greedy ids exact and logits within 1e-3; bf16 logits within 0.5,
@@ -36,6 +37,7 @@ CASES = {  # fixture: (shape key, layers, dtype)
     "q05b2_b32_bf16": ("qwen2.5-0.5b", 2, torch.bfloat16),
     "q05b2_b3_bf16": ("qwen2.5-0.5b", 2, torch.bfloat16),
     "q05b2_b20_bf16": ("qwen2.5-0.5b", 2, torch.bfloat16),
+    "q05b2_b48_bf16": ("qwen2.5-0.5b", 2, torch.bfloat16),
     "q7b1_b2_p256_bf16": ("qwen2.5-7b", 1, torch.bfloat16),
     # every layer of the model (shorter prompts than the workloads)
     "q05b_b32_fp32": ("qwen2.5-0.5b", 24, torch.float32),
@@ -71,7 +73,8 @@ def test_fp32_greedy_ids_exact_and_logits(name):
     print(f"{name}: ids exact; max logit err decode {err:.2e} prefill {err_p:.2e}")
 
 
-@pytest.mark.parametrize("name", ["q7b2_bf16", "q05b2_b32_bf16", "q05b2_b3_bf16", "q05b2_b20_bf16", "q7b1_b2_p256_bf16",
+@pytest.mark.parametrize("name", ["q7b2_bf16", "q05b2_b32_bf16", "q05b2_b3_bf16", "q05b2_b20_bf16", "q05b2_b48_bf16",
+                                  "q7b1_b2_p256_bf16",
                                   "q05b_b32_bf16",
                                   "q7b_bf16", "q7b_b4_p640_bf16"])
 def test_bf16_logits_teacher_forced(name):
