@@ -4,7 +4,9 @@ generate_greedy(early_stop=True, eos_token_id=e) (generation.py:133-171)
 against the oracle's loop, run live on the CPU: the same trimmed ids, the
 same KV fill cursor, and no KV row written past it (the cache is poisoned
 with NaN first, so a row written by a step queued past the stop shows up).
-Batches 1-3 run the fused GEMV program, batch 5 the GEMM one.
+Batches 1-3 run the fused GEMV program, batch 5 the GEMM one. On the bf16
+0.5B layer shape (batches 1, 4 and 40) the reference is the same model's
+fixed-length run cut at the stop.
 """
 
 import pytest
@@ -174,3 +176,44 @@ def test_early_stop_matches_the_reference_fixture():
         assert kv.seq_len == int(fx["seq_len"][i])
         for buf in kv.k + kv.v:
             assert torch.isnan(buf[:, :, kv.seq_len:]).all()
+
+
+@pytest.mark.parametrize("batch", [1, 4, 40])
+def test_bf16_q05b_early_stop_equals_the_fixed_length_run_cut_at_the_stop(batch):
+    """The device early stop on the bf16 0.5B layer shape (2 layers): batch 1
+    (the argmax GEMV epilogue), 4 (the MFMA LM head and the argmax kernels)
+    and 40 (the GEMM programs). Rows do not interact, so against the same
+    model's fixed-length run, with EOS = the token row 0 produces at step 5:
+    every row is its fixed-length row up to its first EOS and EOS after it,
+    the loop ends after the step at which the last row finished (or runs to
+    the end when a row never produces it), and the cache holds exactly the
+    rows of the steps run."""
+    import dataclasses
+
+    from minitp import synthetic
+    from minitp.generation import generate_greedy, make_kv_cache
+
+    cfg = dataclasses.replace(synthetic.QWEN05B, num_hidden_layers=2)
+    model = synthetic.build_synthetic_model(cfg, dtype=torch.bfloat16, device=DEV, seed=5)
+    t, n = 8, 24
+    half = synthetic.synthetic_prompt(cfg.vocab_size, 2, t, seed=13, device=DEV)
+    rows = [half[0]] * ((batch + 1) // 2) + [half[1]] * (batch // 2)  # two distinct prompts
+    prompt = torch.stack(rows) if batch > 1 else half[:1]
+    fixed = generate_greedy(model, prompt, n, early_stop=False).cpu()
+    eos = int(fixed[0, t + 5])
+    kv = make_kv_cache(model, batch, t + n)
+    kv.poison(float("nan"))
+    got = generate_greedy(model, prompt, n, eos_token_id=eos, early_stop=True, kv=kv).cpu()
+    gen = fixed[:, t:]
+    hit = gen == eos
+    first = [int(hit[r].int().argmax()) if hit[r].any() else None for r in range(batch)]
+    steps = n if any(f is None for f in first) else max(first) + 1
+    want = fixed[:, : t + steps].clone()
+    for r, f in enumerate(first):
+        if f is not None:
+            want[r, t + f + 1:] = eos
+    assert torch.equal(got, want), (got, want)
+    assert kv.seq_len == t + steps - 1
+    for buf in kv.k + kv.v:
+        assert torch.isfinite(buf[:, :, : kv.seq_len]).all()
+        assert torch.isnan(buf[:, :, kv.seq_len:]).all()
