@@ -27,6 +27,8 @@
 
 namespace minitp {
 
+static int device_cus();
+
 namespace {
 
 constexpr int P = 2;  // pairs per tuple (R = 4 rows)
@@ -66,28 +68,28 @@ __device__ __forceinline__ uint4 span_load16(__amdgpu_buffer_rsrc_t r, uint32_t 
 }
 
 
-template <int EPI>
+template <int EPI, int PP = P>
 __device__ __forceinline__ void tuple_rows(int64_t t, const GemvArgs& a, int64_t& ra, int64_t& rb) {
   if constexpr (EPI == EPI_SWIGLU) {
-    ra = t * P;
-    rb = a.N + t * P;
+    ra = t * PP;
+    rb = a.N + t * PP;
   } else if constexpr (is_qkv<EPI>()) {
     const int half = a.a.D / 2;
-    const int per_head = half / P;
+    const int per_head = half / PP;
     const int64_t head = t / per_head;
-    ra = head * a.a.D + (t % per_head) * P;
+    ra = head * a.a.D + (t % per_head) * PP;
     rb = ra + half;
   } else {
-    ra = t * R;
-    rb = t * R + P;
+    ra = t * 2 * PP;
+    rb = t * 2 * PP + PP;
   }
 }
 
-template <int EPI>
+template <int EPI, int PP = P>
 __host__ __device__ __forceinline__ int64_t num_tuples(const GemvArgs& a) {
-  if constexpr (EPI == EPI_SWIGLU) return a.N / P;
-  if constexpr (is_qkv<EPI>()) return (int64_t)(a.a.Hq + 2 * a.a.Hkv) * (a.a.D / 2) / P;
-  return cdiv(a.N, R);
+  if constexpr (EPI == EPI_SWIGLU) return a.N / PP;
+  if constexpr (is_qkv<EPI>()) return (int64_t)(a.a.Hq + 2 * a.a.Hkv) * (a.a.D / 2) / PP;
+  return cdiv(a.N, 2 * PP);
 }
 
 // Rows that exist in the weight matrix (contiguous tuples can overhang N).
@@ -135,7 +137,7 @@ __device__ __forceinline__ uint4 pack_bf16x8(const float* f) {
 // side[4..5]; RESID: both residual values. The single-token RoPE and the
 // residual loads are unconditional (clamped to rows that exist), so nothing
 // has to wait for them before the epilogue.
-template <typename T, int EPI>
+template <typename T, int EPI, int PP = P>
 __device__ __forceinline__ void load_side(const GemvArgs& a, int em, int ep, const int64_t* rows, const bool* rok,
                                           int64_t pos, float* side) {
   if constexpr (EPI == EPI_QKV_ROPE1) {
@@ -146,12 +148,12 @@ __device__ __forceinline__ void load_side(const GemvArgs& a, int em, int ep, con
     side[2] = a.st->rope_cos[i + D / 2];
     side[3] = a.st->rope_sin[i + D / 2];
     side[4] = load_f32<T>((const T*)a.bias, rows[ep]);
-    side[5] = load_f32<T>((const T*)a.bias, rows[P + ep]);
+    side[5] = load_f32<T>((const T*)a.bias, rows[PP + ep]);
   } else if constexpr (EPI == EPI_QKV_ROPE) {
     const int D = a.a.D;
     const int64_t head = rows[ep] / D;
     side[4] = load_f32<T>((const T*)a.bias, rows[ep]);
-    side[5] = load_f32<T>((const T*)a.bias, rows[P + ep]);
+    side[5] = load_f32<T>((const T*)a.bias, rows[PP + ep]);
     if (head < a.a.Hq + a.a.Hkv) {
       const int i = (int)(rows[ep] % D);
       if (pos >= 0 && pos < a.max_pos) {
@@ -165,7 +167,7 @@ __device__ __forceinline__ void load_side(const GemvArgs& a, int em, int ep, con
     const T* aux = (const T*)a.aux;
     const int64_t m = em < a.M ? em : 0;
     side[0] = load_f32<T>(aux, m * a.ldy + (rok[ep] ? rows[ep] : 0));
-    side[1] = load_f32<T>(aux, m * a.ldy + (rok[P + ep] ? rows[P + ep] : 0));
+    side[1] = load_f32<T>(aux, m * a.ldy + (rok[PP + ep] ? rows[PP + ep] : 0));
   }
 }
 
@@ -271,8 +273,10 @@ __device__ __forceinline__ uint4 lds_chunk16(const float* xs, int64_t c) {
   }
 }
 
-template <typename T, int MM, int KSPLIT, int JMAX, int PRO, int EPI>
+template <typename T, int MM, int KSPLIT, int JMAX, int PRO, int EPI, int PP = P>
 __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
+  // PP pairs (2 PP rows) a tuple: the names P and R below are this kernel's
+  constexpr int P = PP, R = 2 * PP;
   constexpr int V = Vec<T>::N;
   constexpr int SLOTS = 4 / KSPLIT;
   constexpr bool NORM = PRO != PRO_NONE;
@@ -287,7 +291,7 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
   const int kw = wave % KSPLIT, slot = wave / KSPLIT;
   const int M = (int)a.M;
   const int64_t nchunk = a.K / V;
-  const int64_t ntup = num_tuples<EPI>(a);
+  const int64_t ntup = num_tuples<EPI, PP>(a);
   const int64_t tstride = (int64_t)gridDim.x * SLOTS;
   const uint4* W = (const uint4*)a.w;
   const uint32_t row_bytes = (uint32_t)(a.K * (int64_t)sizeof(T));
@@ -305,7 +309,7 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
   auto set_rows = [&](int64_t tt) {
     int64_t ra = 0, rb = 0;
     const bool ok = tt < ntup;
-    if (ok) tuple_rows<EPI>(tt, a, ra, rb);
+    if (ok) tuple_rows<EPI, PP>(tt, a, ra, rb);
 #pragma unroll
     for (int p = 0; p < P; ++p) {
       rows[p] = ra + p;
@@ -388,9 +392,9 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
   int64_t pos = 0;
   if constexpr (EPI == EPI_QKV_ROPE) {
     if (em < M && a.a.T > 1) pos = a.st->args.positions[em % a.a.T];
-    if (em < M && t < ntup) load_side<T, EPI>(a, em, ep, rows, rok, pos, side);
+    if (em < M && t < ntup) load_side<T, EPI, PP>(a, em, ep, rows, rok, pos, side);
   } else {
-    load_side<T, EPI>(a, em, ep, rows, rok, pos, side);
+    load_side<T, EPI, PP>(a, em, ep, rows, rok, pos, side);
   }
 
   // ---- 3b. PRO_PART_NORM: x + sum of the partials (in row order) ------------
@@ -573,7 +577,7 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
             va = acc[m][p];
             vb = acc[m][P + p];
           }
-      if (cur_t != (int64_t)blockIdx.x * SLOTS + slot) load_side<T, EPI>(a, em, ep, cur_rows, cur_ok, pos, side);
+      if (cur_t != (int64_t)blockIdx.x * SLOTS + slot) load_side<T, EPI, PP>(a, em, ep, cur_rows, cur_ok, pos, side);
       finish_pair<T, EPI>(a, em, cur_rows[ep], cur_rows[P + ep], cur_ok[ep], cur_ok[P + ep], va, vb, side, pos);
     }
   }
@@ -1979,17 +1983,32 @@ int launch_mfma(hipStream_t st, const GemvArgs& a) {
   }
 }
 
-template <typename T, int MM, int KSPLIT, int JMAX, int PRO, int EPI>
-int launch_reg(hipStream_t st, const GemvArgs& a) {
+template <typename T, int MM, int KSPLIT, int JMAX, int PRO, int EPI, int PP>
+int launch_reg_pp(hipStream_t st, const GemvArgs& a) {
   const int64_t slots = 4 / KSPLIT;
   const int64_t cap = EPI == EPI_ARGMAX ? gemv_argmax_partials(a.N) : a.max_grid > 0 ? a.max_grid : MAX_GRID;
-  const int grid = (int)std::min<int64_t>(cdiv(num_tuples<EPI>(a), slots), cap);
-  hipLaunchKernelGGL((gemv_reg_kernel<T, MM, KSPLIT, JMAX, PRO, EPI>), dim3(grid), dim3(256), 0, st, a);
+  const int grid = (int)std::min<int64_t>(cdiv(num_tuples<EPI, PP>(a), slots), cap);
+  hipLaunchKernelGGL((gemv_reg_kernel<T, MM, KSPLIT, JMAX, PRO, EPI, PP>), dim3(grid), dim3(256), 0, st, a);
   MINITP_LAUNCH_CHECK();
   if constexpr (EPI == EPI_ARGMAX) {
     return launch_argmax_merge(st, a.part_val, a.part_idx, grid, a.M, nullptr, 0, a.st);
   }
   return MINITP_OK;
+}
+
+// Tuples of one pair (two rows, twice the blocks) where tuples of P pairs
+// would leave CUs without a block: at the 0.5B decode shape QKV 72 -> 144
+// blocks (3.42 -> 3.26 us) and down 224 -> 448 (4.15 -> 3.95 us); the
+// larger launches (gate/up 7.01 -> 7.52 us, the LM head 42.6 -> 43.1 us)
+// keep P pairs. The same per-row sums either way, so the results are the
+// same bit for bit.
+template <typename T, int MM, int KSPLIT, int JMAX, int PRO, int EPI>
+int launch_reg(hipStream_t st, const GemvArgs& a) {
+  if constexpr (EPI != EPI_ARGMAX && PRO != PRO_PART_NORM) {
+    if (cdiv(num_tuples<EPI>(a), (int64_t)(4 / KSPLIT)) < device_cus())
+      return launch_reg_pp<T, MM, KSPLIT, JMAX, PRO, EPI, 1>(st, a);
+  }
+  return launch_reg_pp<T, MM, KSPLIT, JMAX, PRO, EPI, P>(st, a);
 }
 
 template <typename T, int MM, int PRO, int EPI>
