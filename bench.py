@@ -310,7 +310,7 @@ def measure_workload(name: str, model=None) -> dict:
 # the dominant kernel
 
 
-DOMINANT = "gemv_reg_kernel<minitp::bf16, 1, 1, 2, 2, 2>"  # PRO_PART_NORM, EPI_SWIGLU: rocprofv3's name for it
+DOMINANT = "gemv_reg_kernel<minitp::bf16, 1, 1, 2, 2, 2, 2>"  # PRO_PART_NORM, EPI_SWIGLU, 2 pairs a tuple: rocprofv3's name
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gate_up_gemv_q05b_decode_traffic.json")
 
 
