@@ -231,7 +231,8 @@ struct OprojArgs {
 };
 // W_o row slices a model asks for: more slices re-run each head's attention
 // more often but give each block fewer rows (0.5B: 4 slices 0.524 ms a
-// token, 8 0.518, 16 0.517).
+// token, 8 0.518, 16 0.517; with the later kernels 16 0.502, 18 0.503, 32
+// 0.533).
 constexpr int OPROJ_SLICES = 16;
 bool attn_oproj_supported(int dtype, const AttnShape& a, int64_t H, int slices);
 int attn_oproj_rows(int dtype, const AttnShape& a, int64_t H, int slices);
