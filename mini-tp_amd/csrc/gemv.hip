@@ -416,12 +416,14 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
           sum[3] = add_rn(sum[3], __uint_as_float(pv[h].w));
         }
       }
-      T* xo = (T*)a.x_out;
+      float v[4];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float v = round_to<T>(add_rn(xres[e], round_to<T>(sum[e])));
-        xs[e0 + e] = v;
-        if (blockIdx.x == 0) store_f32<T>(xo, e0 + e, v);
+      for (int e = 0; e < 4; ++e) v[e] = round_to<T>(add_rn(xres[e], round_to<T>(sum[e])));
+      *(float4*)(xs + e0) = make_float4(v[0], v[1], v[2], v[3]);  // one LDS write
+      if (blockIdx.x == 0) {
+        T* xo = (T*)a.x_out;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) store_f32<T>(xo, e0 + e, v[e]);
       }
     }
     __syncthreads();
