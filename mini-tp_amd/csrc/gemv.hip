@@ -76,8 +76,8 @@ __device__ __forceinline__ void tuple_rows(int64_t t, const GemvArgs& a, int64_t
   } else if constexpr (is_qkv<EPI>()) {
     const int half = a.a.D / 2;
     const int per_head = half / PP;
-    const int64_t head = t / per_head;
-    ra = head * a.a.D + (t % per_head) * PP;
+    const int t32 = (int)t;  // tuple and row indices fit 32 bits: 32-bit division
+    ra = (int64_t)(t32 / per_head) * a.a.D + (t32 % per_head) * PP;
     rb = ra + half;
   } else {
     ra = t * 2 * PP;
@@ -142,7 +142,7 @@ __device__ __forceinline__ void load_side(const GemvArgs& a, int em, int ep, con
                                           int64_t pos, float* side) {
   if constexpr (EPI == EPI_QKV_ROPE1) {
     const int D = a.a.D;
-    const int i = (int)(rows[ep] % D);
+    const int i = (int)rows[ep] % D;
     side[0] = a.st->rope_cos[i];
     side[1] = a.st->rope_sin[i];
     side[2] = a.st->rope_cos[i + D / 2];
@@ -151,11 +151,11 @@ __device__ __forceinline__ void load_side(const GemvArgs& a, int em, int ep, con
     side[5] = load_f32<T>((const T*)a.bias, rows[PP + ep]);
   } else if constexpr (EPI == EPI_QKV_ROPE) {
     const int D = a.a.D;
-    const int64_t head = rows[ep] / D;
+    const int head = (int)rows[ep] / D;
     side[4] = load_f32<T>((const T*)a.bias, rows[ep]);
     side[5] = load_f32<T>((const T*)a.bias, rows[PP + ep]);
     if (head < a.a.Hq + a.a.Hkv) {
-      const int i = (int)(rows[ep] % D);
+      const int i = (int)rows[ep] % D;
       if (pos >= 0 && pos < a.max_pos) {
         side[0] = a.cos_tab[pos * D + i];
         side[1] = a.sin_tab[pos * D + i];
@@ -194,8 +194,8 @@ __device__ __forceinline__ void finish_pair(const GemvArgs& a, int m, int64_t ro
     const StepState* st = a.st;
     const AttnShape& s = a.a;
     const int D = s.D, half = D / 2;
-    const int64_t head = row_a / D;
-    const int i = (int)(row_a % D);
+    const int head = (int)row_a / D;
+    const int i = (int)row_a % D;
     const int b = m / s.T, tt = m % s.T;
     if (head < s.Hq + s.Hkv) {
       // rotate(x) = x * cos + rotate_half(x) * sin in fp32, each multiply
@@ -298,8 +298,8 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
 
   // Load order matters: vector loads retire in issue order, so what the
   // prologue consumes (input rows, RMSNorm weight) is requested first, then
-  // the weights, then the epilogue's side inputs; the norm math overlaps the
-  // weight loads still in flight. Lane l's 16-byte chunk j of a row sits at
+  // the epilogue's side inputs and the weights; the norm math overlaps the
+  // loads still in flight. Lane l's 16-byte chunk j of a row sits at
   // byte offset (kw * 64 + l + j * 64 * KSPLIT) * 16; chunks past the row end
   // read zeros.
   int64_t t = (int64_t)blockIdx.x * SLOTS + slot;
@@ -380,21 +380,22 @@ __global__ __launch_bounds__(256) void gemv_reg_kernel(GemvArgs a) {
     }
   }
 
-  // ---- 2. the first tuple's weights -----------------------------------------
+  // ---- 2. the first tuple's side inputs and weights ----------------------------
+  // Side inputs that need no loaded value first (the single-token RoPE rows,
+  // the bias, the residual): issued here, ahead of the prologue math, they
+  // arrive with the weights instead of a round trip after the norm. The
+  // multi-token RoPE reads its position first, so it follows the weights.
+  const int em = lane / P, ep = lane % P;  // this lane finishes pair ep of row em
+  float side[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  int64_t pos = 0;
+  if constexpr (EPI != EPI_QKV_ROPE) load_side<T, EPI, PP>(a, em, ep, rows, rok, pos, side);
   load_w();
   // Keep the scheduler from sinking the weight loads below the prologue math
   // (and the waits for the input rows that math needs).
   __builtin_amdgcn_sched_barrier(0);
-
-  // ---- 3. the epilogue's side inputs for the first tuple -----------------------
-  const int em = lane / P, ep = lane % P;  // this lane finishes pair ep of row em
-  float side[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  int64_t pos = 0;
   if constexpr (EPI == EPI_QKV_ROPE) {
     if (em < M && a.a.T > 1) pos = a.st->args.positions[em % a.a.T];
     if (em < M && t < ntup) load_side<T, EPI, PP>(a, em, ep, rows, rok, pos, side);
-  } else {
-    load_side<T, EPI, PP>(a, em, ep, rows, rok, pos, side);
   }
 
   // ---- 3b. PRO_PART_NORM: x + sum of the partials (in row order) ------------
@@ -787,8 +788,8 @@ __global__ __launch_bounds__(256) void gemv_lds_kernel(GemvArgs a) {
                 const StepState* st = a.st;
                 const AttnShape& s = a.a;
                 const int D = s.D, half = D / 2;
-                const int64_t head = row_a / D;
-                const int i = (int)(row_a % D);
+                const int head = (int)row_a / D;
+                const int i = (int)row_a % D;
                 const int b = m / s.T, tt = m % s.T;
                 if (head < s.Hq + s.Hkv) {
                   // rotate(x) = x * cos + rotate_half(x) * sin, fp32, each op
@@ -976,8 +977,8 @@ __device__ __forceinline__ void tuple16_rows(int64_t t, const GemvArgs& a, int64
   } else if constexpr (is_qkv<EPI>()) {
     const int half = a.a.D / 2;
     const int per_head = half / P16;
-    const int64_t head = t / per_head;
-    ra = head * a.a.D + (t % per_head) * P16;
+    const int t32 = (int)t;  // 32-bit division
+    ra = (int64_t)(t32 / per_head) * a.a.D + (t32 % per_head) * P16;
     rb = ra + half;
   } else {
     ra = t * 2 * P16;
@@ -1168,7 +1169,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
       sv[j][0] = load_f32<bf16>((const bf16*)a.bias, oka ? row_a : 0);
       sv[j][1] = load_f32<bf16>((const bf16*)a.bias, okb ? row_b : 0);
       if constexpr (EPI == EPI_QKV_ROPE1) {
-        const int D = a.a.D, i = (int)(row_a % D);
+        const int D = a.a.D, i = (int)row_a % D;
         sv[j][2] = a.st->rope_cos[i];
         sv[j][3] = a.st->rope_sin[i];
         sv[j][4] = a.st->rope_cos[i + D / 2];
@@ -1305,9 +1306,9 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
         const float va = acc[j][h][r], vb = h ? pa1[r] : pa0[r];
         int64_t pos = 0;
         if constexpr (EPI == EPI_QKV_ROPE) {
-          const int D = a.a.D, i = (int)(row_a % D);
+          const int D = a.a.D, i = (int)row_a % D;
           pos = a.st->args.positions[m % a.a.T];
-          if (row_a / D < a.a.Hq + a.a.Hkv && pos >= 0 && pos < a.max_pos) {
+          if ((int)row_a / D < a.a.Hq + a.a.Hkv && pos >= 0 && pos < a.max_pos) {
             side[0] = a.cos_tab[pos * D + i];
             side[1] = a.sin_tab[pos * D + i];
             side[2] = a.cos_tab[pos * D + i + D / 2];
@@ -1678,7 +1679,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_split_kernel(GemvArgs a, int ns
       sv[j][0] = load_f32<bf16>((const bf16*)a.bias, oka ? row_a : 0);
       sv[j][1] = load_f32<bf16>((const bf16*)a.bias, okb ? row_b : 0);
       if constexpr (EPI == EPI_QKV_ROPE1) {
-        const int D = a.a.D, i = (int)(row_a % D);
+        const int D = a.a.D, i = (int)row_a % D;
         sv[j][2] = a.st->rope_cos[i];
         sv[j][3] = a.st->rope_sin[i];
         sv[j][4] = a.st->rope_cos[i + D / 2];
@@ -1822,9 +1823,9 @@ __global__ __launch_bounds__(256) void gemv_mfma_split_kernel(GemvArgs a, int ns
           const float va = acc[j][h][r], vb = h ? pa1[r] : pa0[r];
           int64_t pos = 0;
           if constexpr (EPI == EPI_QKV_ROPE) {
-            const int D = a.a.D, i = (int)(row_a % D);
+            const int D = a.a.D, i = (int)row_a % D;
             pos = a.st->args.positions[m % a.a.T];
-            if (row_a / D < a.a.Hq + a.a.Hkv && pos >= 0 && pos < a.max_pos) {
+            if ((int)row_a / D < a.a.Hq + a.a.Hkv && pos >= 0 && pos < a.max_pos) {
               side[0] = a.cos_tab[pos * D + i];
               side[1] = a.sin_tab[pos * D + i];
               side[2] = a.cos_tab[pos * D + i + D / 2];
