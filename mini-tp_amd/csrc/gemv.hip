@@ -895,6 +895,11 @@ __global__ __launch_bounds__(256) void gemv_split_kernel(GemvArgs a, int nseg, u
 #pragma unroll
     for (int j = 0; j < JMAX; ++j) xb[m][j] = span_load16<0>(xr, coff[j]);
   }
+  // the epilogue's side inputs, loaded now (by the lanes of wave 0 that may
+  // finish a pair), not after the last block has seen every count
+  const int em = lane / P, ep = lane % P;
+  float side[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  if (kw == 0 && em < M) load_side<T, EPI>(a, em, ep, rows, rok, 0, side);
 
   float acc[MM][R];
 #pragma unroll
@@ -941,7 +946,6 @@ __global__ __launch_bounds__(256) void gemv_split_kernel(GemvArgs a, int nseg, u
 
   // ---- the last block: segment sums in order, then the epilogue -----------
   // (device-coherent loads, issued after every count was seen)
-  const int em = lane / P, ep = lane % P;
   if (em >= M) return;
   const float* tp = a.split_part + t * nseg * (MM * R);
   float va = 0.f, vb = 0.f;
@@ -949,8 +953,6 @@ __global__ __launch_bounds__(256) void gemv_split_kernel(GemvArgs a, int nseg, u
     va += __hip_atomic_load(tp + s * (MM * R) + em * R + ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     vb += __hip_atomic_load(tp + s * (MM * R) + em * R + P + ep, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
-  float side[6] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-  load_side<T, EPI>(a, em, ep, rows, rok, 0, side);
   finish_pair<T, EPI>(a, em, rows[ep], rows[P + ep], rok[ep], rok[P + ep], va, vb, side, 0);
 }
 
