@@ -1436,6 +1436,9 @@ __global__ __launch_bounds__(256) void gemv_mfma_loop_kernel(GemvArgs a) {
   }
 #pragma unroll
   for (int j = 0; j < MF_LOOP_PD; ++j) load_w(blockIdx.x + j * (int64_t)gridDim.x, wl[j]);
+  // Keep the scheduler from moving the input rows' LDS writes, and the waits
+  // for those rows, above the weight loads.
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- A fragments through the wave's LDS stage, normalized once ----------
   uint4 xa[NB], xc[NB];
