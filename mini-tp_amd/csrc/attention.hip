@@ -52,6 +52,25 @@ struct DecodeArgs {
   OprojArgs op;  // decode_attn_kernel<..., NLW > 0>: the folded o_proj
 };
 
+// The caches and cache_len of a decode launch: from the step state inside a
+// forward (one branch, the three fields loaded together rather than one
+// dependent scalar load per use), else the launch's own values.
+struct DecodeKV {
+  const void* k;
+  const void* v;
+  int64_t cache_len;
+};
+__device__ __forceinline__ DecodeKV decode_kv(const DecodeArgs& a, int64_t layer_off, int64_t elem_bytes) {
+  DecodeKV r{a.k, a.v, a.cache_len};
+  if (a.st != nullptr) {
+    const StepArgs& sa = a.st->args;
+    r.cache_len = sa.cache_len;
+    r.k = (const char*)sa.k_cache + layer_off * elem_bytes;
+    r.v = (const char*)sa.v_cache + layer_off * elem_bytes;
+  }
+  return r;
+}
+
 // 16-byte load of streamed weights (read once per step: non-temporal).
 __device__ __forceinline__ uint4 weight_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 2));
@@ -196,16 +215,17 @@ __global__ __launch_bounds__(NW * 64) void decode_attn_kernel(DecodeArgs a) {
   const int split = NLW > 0 ? 0 : (int)blockIdx.y, nsplit = NLW > 0 ? 1 : (int)gridDim.y;
   const int h0 = blockIdx.z * HP;  // first query head (within the group) of this block
   const int nh = std::min(HP, G - h0);
-  const int64_t ctx = (a.st ? a.st->args.cache_len : a.cache_len) + 1;
+  const int64_t layer_off = (int64_t)a.layer * s.B * s.Hkv * s.S * D;
+  const DecodeKV kv = decode_kv(a, layer_off, (int64_t)sizeof(T));
+  const int64_t ctx = kv.cache_len + 1;
   const int64_t nchunk = cdiv(ctx, CP);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int col = lane % LPR, grow = lane / LPR;
   const int rbase = col / DUP;
   const bool owner = col % DUP == 0;
 
-  const int64_t layer_off = (int64_t)a.layer * s.B * s.Hkv * s.S * D;
-  const T* kc = (const T*)(a.st ? a.st->args.k_cache : a.k) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
-  const T* vc = (const T*)(a.st ? a.st->args.v_cache : a.v) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
+  const T* kc = (const T*)kv.k + (int64_t)bh * s.S * D;
+  const T* vc = (const T*)kv.v + (int64_t)bh * s.S * D;
 
   // The context's K / V rows through resources that end at row ctx (rows past
   // it read zeros, so the loads are unconditional), and this wave's first
@@ -496,7 +516,9 @@ __global__ __launch_bounds__(NWM * 64) void decode_attn_mfma_kernel(DecodeArgs a
   const int G = s.Hq / s.Hkv;
   const int bh = blockIdx.x, b = bh / s.Hkv, g = bh % s.Hkv;
   const int split = blockIdx.y, nsplit = gridDim.y;
-  const int64_t ctx = (a.st ? a.st->args.cache_len : a.cache_len) + 1;
+  const int64_t layer_off = (int64_t)a.layer * s.B * s.Hkv * s.S * D;
+  const DecodeKV kv = decode_kv(a, layer_off, 2);
+  const int64_t ctx = kv.cache_len + 1;
   // the wave index made explicitly uniform: the tile loop then runs on scalar
   // branches, and the compiler counts the loads in flight across it exactly
   const int tid = threadIdx.x, lane = tid & 63, w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -508,9 +530,8 @@ __global__ __launch_bounds__(NWM * 64) void decode_attn_mfma_kernel(DecodeArgs a
   const int64_t span = cdiv(tiles, (int64_t)nsplit);
   const int64_t t_begin = split * span, t_end = std::min(tiles, t_begin + span);
 
-  const int64_t layer_off = (int64_t)a.layer * s.B * s.Hkv * s.S * D;
-  const bf16* kc = (const bf16*)(a.st ? a.st->args.k_cache : a.k) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
-  const bf16* vc = (const bf16*)(a.st ? a.st->args.v_cache : a.v) + (a.st ? layer_off : 0) + (int64_t)bh * s.S * D;
+  const bf16* kc = (const bf16*)kv.k + (int64_t)bh * s.S * D;
+  const bf16* vc = (const bf16*)kv.v + (int64_t)bh * s.S * D;
   const uint32_t kv_bytes = (uint32_t)(ctx * D * 2);  // rows past the context read zeros
   const __amdgpu_buffer_rsrc_t kr = span_rsrc(kc, kv_bytes), vr = span_rsrc(vc, kv_bytes);
 
