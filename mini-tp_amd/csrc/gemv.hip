@@ -1612,30 +1612,16 @@ __global__ __launch_bounds__(256) void gemv_mfma_split_kernel(GemvArgs a, int ns
   const __amdgpu_buffer_rsrc_t wr = span_rsrc(a.w, (uint32_t)(w_rows * K * 2));
   const __amdgpu_buffer_rsrc_t xr = span_rsrc(a.x, (uint32_t)(((int64_t)(M - 1) * a.ldx + K) * 2));
   int64_t ra[NT], rb[NT];
-  uint32_t wbase[NT];
 #pragma unroll
   for (int j = 0; j < NT; ++j) {
-    const bool live = t0 + j < ntup;
     ra[j] = rb[j] = 0;
-    if (live) tuple16_rows<EPI>(t0 + j, a, ra[j], rb[j]);
-    const int64_t wrow = nidx < P16 ? ra[j] + nidx : rb[j] + (nidx - P16);
-    wbase[j] = live && row_valid<EPI>(wrow, a) ? (uint32_t)(wrow * K * 2) : OOBW;
+    if (t0 + j < ntup) tuple16_rows<EPI>(t0 + j, a, ra[j], rb[j]);
   }
   const int m0 = nidx, m1 = 16 + nidx;
-  const uint32_t xb0 = m0 < M ? (uint32_t)((int64_t)m0 * a.ldx * 2) : OOBW;
-  const uint32_t xb1 = m1 < M ? (uint32_t)((int64_t)m1 * a.ldx * 2) : OOBW;
   const int64_t nsteps = cdiv(K, 32);
   const int64_t sb = (int64_t)seg * seg_steps, se = std::min(nsteps, sb + seg_steps);
   const int64_t per = cdiv((int64_t)seg_steps, 4);
   const int64_t s_begin = sb + kw * per, s_end = std::min(se, s_begin + per);
-  auto off = [&](uint32_t base, int64_t s) -> uint32_t {
-    const int64_t k = s * 32 + kq * 8;
-    return (base != OOBW && s < s_end && k < K) ? base + (uint32_t)(k * 2) : OOBW;
-  };
-  (void)off;
-  (void)wbase;
-  (void)xb0;
-  (void)xb1;
   // the wave's K range staged through LDS as in gemv_mfma_kernel:
   // coalesced loads (input rows first), swizzled wave-private tiles
   extern __shared__ __attribute__((aligned(16))) char mf_stage[];
