@@ -1398,15 +1398,16 @@ __global__ __launch_bounds__(256) void gemv_mfma_loop_kernel(GemvArgs a) {
 #endif
 #if MINITP_MF_LOOP_STAGE
     // tuple t's rows are tuple 0's moved by t x (rows a tuple) x K: the
-    // offsets are a per-lane base plus one uniform step. Rows past the
-    // product read zeros (past the buffer's end) or, for SwiGLU gate rows
-    // past N, up rows whose outputs are never stored.
+    // offsets are a per-lane base plus one uniform step. Prefetches past the
+    // last tuple read zeros (their SwiGLU gate rows would land on up rows).
+    // In the last tuple, rows past the product read zeros (past the buffer's
+    // end) or, for SwiGLU gate rows past N, up rows whose outputs are never
+    // stored.
     (void)ra;
     (void)rb;
-    (void)live;
     const uint32_t tof = (uint32_t)t * wstep;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) wl[u] = span_load16<W_AUX>(wr, wok[u] ? wbase[u] + tof : OOBW);
+    for (int u = 0; u < 8; ++u) wl[u] = span_load16<W_AUX>(wr, live && wok[u] ? wbase[u] + tof : OOBW);
 #else
     // straight into the operand layout: row nidx, chunk 4 i + kq
     const int64_t wrow = nidx < P16 ? ra + nidx : rb + (nidx - P16);
