@@ -41,10 +41,16 @@ __device__ __forceinline__ uint4 gemm_load16(__amdgpu_buffer_rsrc_t r, uint32_t 
   const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
   return make_uint4(v.x, v.y, v.z, v.w);
 }
-constexpr int GEMM_W_AUX = MINITP_NT_LOADS ? 2 : 0;
+// weight loads of gemm_kernel: plain (non-temporal measured slower: 0.5B
+// 128-token TTFT 1.41-1.42 against 1.38 ms, 7B 512 tokens 11.55 against 11.28)
+#ifndef MINITP_GEMM_NT_LOADS
+#define MINITP_GEMM_NT_LOADS 0
+#endif
+constexpr int GEMM_W_AUX = MINITP_GEMM_NT_LOADS ? 2 : 0;
 // chunks in flight: register budget of the prefetch (LA + LB uint4 each)
 // (one chunk ahead measured best at the 0.5B prompt and 7B prefill shapes;
-// deeper prefetch costs occupancy)
+// two to four chunks were slower, also in a form whose loop the compiler
+// counts exactly, waiting only for the chunk it stashes next)
 #ifndef MINITP_GEMM_DEPTH_LARGE
 #define MINITP_GEMM_DEPTH_LARGE 1
 #endif

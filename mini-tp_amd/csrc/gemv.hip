@@ -61,6 +61,14 @@ constexpr bool is_qkv() {
 // Cache-policy bits of the weight loads: nt (read once per step) when
 // MINITP_NT_LOADS is set.
 constexpr int W_AUX = MINITP_NT_LOADS ? 2 : 0;
+// The MFMA GEMVs (5-32 input rows) stage their weights through LDS; their
+// loads take their own cache policy: plain. Batch-32 step, three runs each:
+// 1.035-1.037 ms plain against 1.040-1.042 non-temporal (the batch-1 register
+// GEMVs keep non-temporal loads: 0.548 ms a token plain against 0.496).
+#ifndef MINITP_MF_NT_LOADS
+#define MINITP_MF_NT_LOADS 0
+#endif
+constexpr int MF_W_AUX = MINITP_MF_NT_LOADS ? 2 : 0;
 template <int AUX>
 __device__ __forceinline__ uint4 span_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
@@ -1084,7 +1092,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
-      for (int j = 0; j < NT; ++j) b.w[i][j] = span_load16<W_AUX>(wr, off(wbase[j], s0 + i));
+      for (int j = 0; j < NT; ++j) b.w[i][j] = span_load16<MF_W_AUX>(wr, off(wbase[j], s0 + i));
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       b.xa[i] = span_load16<0>(xr, off(xb0, s0 + i));
@@ -1138,7 +1146,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
         const int q = lane + 64 * t, r = q >> 5, c = q & 31;
         const int64_t wrow = r < P16 ? ra[j] + r : rb[j] + (r - P16);
         const bool ok = t0 + j < ntup && row_valid<EPI>(wrow, a) && c < nch;
-        wl[j][t] = span_load16<W_AUX>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
+        wl[j][t] = span_load16<MF_W_AUX>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
       }
   } else {
     issue(b0, s_begin);
@@ -1407,7 +1415,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_loop_kernel(GemvArgs a) {
     (void)rb;
     const uint32_t tof = (uint32_t)t * wstep;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) wl[u] = span_load16<W_AUX>(wr, live && wok[u] ? wbase[u] + tof : OOBW);
+    for (int u = 0; u < 8; ++u) wl[u] = span_load16<MF_W_AUX>(wr, live && wok[u] ? wbase[u] + tof : OOBW);
 #else
     // straight into the operand layout: row nidx, chunk 4 i + kq
     const int64_t wrow = nidx < P16 ? ra + nidx : rb + (nidx - P16);
@@ -1415,7 +1423,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_loop_kernel(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int c = 4 * i + kq;
-      wl[i] = span_load16<W_AUX>(wr, rok && c < nch ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
+      wl[i] = span_load16<MF_W_AUX>(wr, rok && c < nch ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
     }
 #endif
   };
@@ -1643,7 +1651,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_split_kernel(GemvArgs a, int ns
       const int q = lane + 64 * t, r = q >> 5, c = q & 31;
       const int64_t wrow = r < P16 ? ra[j] + r : rb[j] + (r - P16);
       const bool ok = t0 + j < ntup && row_valid<EPI>(wrow, a) && c < nch;
-      wl[j][t] = span_load16<W_AUX>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
+      wl[j][t] = span_load16<MF_W_AUX>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
     }
   // the epilogue's side inputs, loaded underneath the weights (only the
   // block that finishes a group uses them)
