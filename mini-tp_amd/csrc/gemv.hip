@@ -61,14 +61,16 @@ constexpr bool is_qkv() {
 // Cache-policy bits of the weight loads: nt (read once per step) when
 // MINITP_NT_LOADS is set.
 constexpr int W_AUX = MINITP_NT_LOADS ? 2 : 0;
-// The MFMA GEMVs (5-32 input rows) stage their weights through LDS; their
-// loads take their own cache policy: plain. Batch-32 step, three runs each:
-// 1.035-1.037 ms plain against 1.040-1.042 non-temporal (the batch-1 register
-// GEMVs keep non-temporal loads: 0.548 ms a token plain against 0.496).
-#ifndef MINITP_MF_NT_LOADS
-#define MINITP_MF_NT_LOADS 0
+// The MFMA GEMVs (3-32 input rows) load their weights non-temporal up to
+// MINITP_MF_PLAIN_ROWS input rows and plain above (the kernels take the
+// policy as a template argument; the half-row form, which serves more than 16
+// rows, loads plain). 0.5B, 2,048-token prompts, ms a step non-temporal /
+// plain: batch 3 0.909 / 0.958, 4 0.905 / 0.973, 8 0.903 / 0.927, 16 0.960 /
+// 0.958, 32 1.040-1.042 / 1.035-1.037; 7B batch 3-8 the same either way.
+#ifndef MINITP_MF_PLAIN_ROWS
+#define MINITP_MF_PLAIN_ROWS 16
 #endif
-constexpr int MF_W_AUX = MINITP_MF_NT_LOADS ? 2 : 0;
+constexpr int AUX_NT = 2;  // buffer-op cache policy: non-temporal
 template <int AUX>
 __device__ __forceinline__ uint4 span_load16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
   const u32x4 v = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX));
@@ -1046,6 +1048,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
   // on one XCD, share a tuple, so its weights come from that XCD's L2 the
   // second time.
   constexpr int SLOTS = 4 / KSPLIT;
+  constexpr int WAUX = HV ? 0 : AUX_NT;  // weight-load policy (more than 16 rows: plain)
   constexpr int NF = HV ? 1 : 2;  // A fragments (16-row halves) a block multiplies
   constexpr uint32_t OOBW = 0xffffffffu;
   static_assert(!(MULTI && PRO == PRO_NORM), "the norm prologue needs the K range in one batch");
@@ -1092,7 +1095,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < NB; ++i)
 #pragma unroll
-      for (int j = 0; j < NT; ++j) b.w[i][j] = span_load16<MF_W_AUX>(wr, off(wbase[j], s0 + i));
+      for (int j = 0; j < NT; ++j) b.w[i][j] = span_load16<WAUX>(wr, off(wbase[j], s0 + i));
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       b.xa[i] = span_load16<0>(xr, off(xb0, s0 + i));
@@ -1146,7 +1149,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_kernel(GemvArgs a) {
         const int q = lane + 64 * t, r = q >> 5, c = q & 31;
         const int64_t wrow = r < P16 ? ra[j] + r : rb[j] + (r - P16);
         const bool ok = t0 + j < ntup && row_valid<EPI>(wrow, a) && c < nch;
-        wl[j][t] = span_load16<MF_W_AUX>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
+        wl[j][t] = span_load16<WAUX>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
       }
   } else {
     issue(b0, s_begin);
@@ -1357,7 +1360,7 @@ constexpr int MF_ONE = 8;
 #ifndef MINITP_MF_LOOP_STAGE
 #define MINITP_MF_LOOP_STAGE 1
 #endif
-template <int PRO, int EPI>
+template <int PRO, int EPI, int WAUX>
 __global__ __launch_bounds__(256) void gemv_mfma_loop_kernel(GemvArgs a) {
   static_assert(EPI == EPI_STORE || EPI == EPI_SWIGLU, "the tuple loop serves the store and SwiGLU epilogues");
   constexpr int MF_LOOP_PD = MINITP_MF_LOOP_PD;  // tuples whose weight loads are in flight
@@ -1415,7 +1418,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_loop_kernel(GemvArgs a) {
     (void)rb;
     const uint32_t tof = (uint32_t)t * wstep;
 #pragma unroll
-    for (int u = 0; u < 8; ++u) wl[u] = span_load16<MF_W_AUX>(wr, live && wok[u] ? wbase[u] + tof : OOBW);
+    for (int u = 0; u < 8; ++u) wl[u] = span_load16<WAUX>(wr, live && wok[u] ? wbase[u] + tof : OOBW);
 #else
     // straight into the operand layout: row nidx, chunk 4 i + kq
     const int64_t wrow = nidx < P16 ? ra + nidx : rb + (nidx - P16);
@@ -1423,7 +1426,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_loop_kernel(GemvArgs a) {
 #pragma unroll
     for (int i = 0; i < NB; ++i) {
       const int c = 4 * i + kq;
-      wl[i] = span_load16<MF_W_AUX>(wr, rok && c < nch ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
+      wl[i] = span_load16<WAUX>(wr, rok && c < nch ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
     }
 #endif
   };
@@ -1604,7 +1607,7 @@ __device__ __forceinline__ f32x4_m load16_dev(__amdgpu_buffer_rsrc_t r, uint32_t
   return __builtin_bit_cast(f32x4_m, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX_SC1));
 }
 
-template <int EPI, int NT>
+template <int EPI, int NT, int WAUX>
 __global__ __launch_bounds__(256) void gemv_mfma_split_kernel(GemvArgs a, int nseg, int seg_steps) {
   constexpr uint32_t OOBW = 0xffffffffu;
   __shared__ f32x4_m red[4][NT][2][64];
@@ -1651,7 +1654,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_split_kernel(GemvArgs a, int ns
       const int q = lane + 64 * t, r = q >> 5, c = q & 31;
       const int64_t wrow = r < P16 ? ra[j] + r : rb[j] + (r - P16);
       const bool ok = t0 + j < ntup && row_valid<EPI>(wrow, a) && c < nch;
-      wl[j][t] = span_load16<MF_W_AUX>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
+      wl[j][t] = span_load16<WAUX>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
     }
   // the epilogue's side inputs, loaded underneath the weights (only the
   // block that finishes a group uses them)
@@ -1886,7 +1889,7 @@ bool mf_split_ok(const GemvArgs& a) {
 template <int EPI, int NT>
 int launch_mfma_split_nt(hipStream_t st, const GemvArgs& a, const MfSplit& g) {
   const dim3 grid((unsigned)g.groups, (unsigned)g.nseg);
-  auto kern = gemv_mfma_split_kernel<EPI, NT>;
+  auto kern = a.M > MINITP_MF_PLAIN_ROWS ? gemv_mfma_split_kernel<EPI, NT, 0> : gemv_mfma_split_kernel<EPI, NT, AUX_NT>;
   const int lds = mf_stage_bytes<NT>();
   const int rc = ensure_lds_limit((const void*)kern, lds);
   if (rc) return rc;
@@ -1938,7 +1941,7 @@ int launch_mfma_nt(hipStream_t st, const GemvArgs& a, int64_t ntup) {
     const int64_t w_bytes = (EPI == EPI_SWIGLU ? 2 : 1) * a.N * a.K * 2;
     if (per_wave <= MF_ONE && NT == 1 && ntup >= MINITP_MF_LOOP_MIN && w_bytes < (1LL << 30)) {
       // many tuples: several a block, the input rows' prologue shared
-      auto kern = gemv_mfma_loop_kernel<PRO, EPI>;
+      auto kern = a.M > MINITP_MF_PLAIN_ROWS ? gemv_mfma_loop_kernel<PRO, EPI, 0> : gemv_mfma_loop_kernel<PRO, EPI, AUX_NT>;
       const int lds = 4 * MF_X_STAGE;
       const int rc = ensure_lds_limit((const void*)kern, lds);
       if (rc) return rc;
