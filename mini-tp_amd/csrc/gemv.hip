@@ -62,11 +62,14 @@ constexpr bool is_qkv() {
 // MINITP_NT_LOADS is set.
 constexpr int W_AUX = MINITP_NT_LOADS ? 2 : 0;
 // The MFMA GEMVs (3-32 input rows) load their weights non-temporal up to
-// MINITP_MF_PLAIN_ROWS input rows and plain above (the kernels take the
+// MINITP_MF_PLAIN_ROWS input rows and plain above (the tuple loop takes the
 // policy as a template argument; the half-row form, which serves more than 16
-// rows, loads plain). 0.5B, 2,048-token prompts, ms a step non-temporal /
-// plain: batch 3 0.909 / 0.958, 4 0.905 / 0.973, 8 0.903 / 0.927, 16 0.960 /
-// 0.958, 32 1.040-1.042 / 1.035-1.037; 7B batch 3-8 the same either way.
+// rows, loads plain), except the split-K form, non-temporal at every row
+// count. 0.5B, 2,048-token prompts, ms a step non-temporal / plain for all of
+// them: batch 3 0.909 / 0.958, 4 0.905 / 0.973, 8 0.903 / 0.927, 16 0.960 /
+// 0.958, 32 1.040-1.042 / 1.035-1.037; 7B batch 3-8 the same either way. At
+// batch 32 the split-K form non-temporal with the others plain: 1.033-1.035
+// against 1.037-1.044 ms.
 #ifndef MINITP_MF_PLAIN_ROWS
 #define MINITP_MF_PLAIN_ROWS 16
 #endif
@@ -1607,7 +1610,7 @@ __device__ __forceinline__ f32x4_m load16_dev(__amdgpu_buffer_rsrc_t r, uint32_t
   return __builtin_bit_cast(f32x4_m, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, AUX_SC1));
 }
 
-template <int EPI, int NT, int WAUX>
+template <int EPI, int NT>
 __global__ __launch_bounds__(256) void gemv_mfma_split_kernel(GemvArgs a, int nseg, int seg_steps) {
   constexpr uint32_t OOBW = 0xffffffffu;
   __shared__ f32x4_m red[4][NT][2][64];
@@ -1654,7 +1657,7 @@ __global__ __launch_bounds__(256) void gemv_mfma_split_kernel(GemvArgs a, int ns
       const int q = lane + 64 * t, r = q >> 5, c = q & 31;
       const int64_t wrow = r < P16 ? ra[j] + r : rb[j] + (r - P16);
       const bool ok = t0 + j < ntup && row_valid<EPI>(wrow, a) && c < nch;
-      wl[j][t] = span_load16<WAUX>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
+      wl[j][t] = span_load16<AUX_NT>(wr, ok ? (uint32_t)((wrow * K + kb + 8 * c) * 2) : OOBW);
     }
   // the epilogue's side inputs, loaded underneath the weights (only the
   // block that finishes a group uses them)
@@ -1889,7 +1892,7 @@ bool mf_split_ok(const GemvArgs& a) {
 template <int EPI, int NT>
 int launch_mfma_split_nt(hipStream_t st, const GemvArgs& a, const MfSplit& g) {
   const dim3 grid((unsigned)g.groups, (unsigned)g.nseg);
-  auto kern = a.M > MINITP_MF_PLAIN_ROWS ? gemv_mfma_split_kernel<EPI, NT, 0> : gemv_mfma_split_kernel<EPI, NT, AUX_NT>;
+  auto kern = gemv_mfma_split_kernel<EPI, NT>;
   const int lds = mf_stage_bytes<NT>();
   const int rc = ensure_lds_limit((const void*)kern, lds);
   if (rc) return rc;
