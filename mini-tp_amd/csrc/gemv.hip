@@ -64,8 +64,8 @@ constexpr int W_AUX = MINITP_NT_LOADS ? 2 : 0;
 // The MFMA GEMVs (3-32 input rows) load their weights non-temporal up to
 // MINITP_MF_PLAIN_ROWS input rows and plain above (the tuple loop takes the
 // policy as a template argument; the half-row form, which serves more than 16
-// rows, loads plain), except the split-K form, non-temporal at every row
-// count. 0.5B, 2,048-token prompts, ms a step non-temporal / plain for all of
+// rows, loads plain), except the split-K form and the plain-store tuple loop
+// (the LM head), non-temporal at every row count. 0.5B, 2,048-token prompts, ms a step non-temporal / plain for all of
 // them: batch 3 0.909 / 0.958, 4 0.905 / 0.973, 8 0.903 / 0.927, 16 0.960 /
 // 0.958, 32 1.040-1.042 / 1.035-1.037; 7B batch 3-8 the same either way. At
 // batch 32 the split-K form non-temporal with the others plain: 1.033-1.035
@@ -1944,7 +1944,10 @@ int launch_mfma_nt(hipStream_t st, const GemvArgs& a, int64_t ntup) {
     const int64_t w_bytes = (EPI == EPI_SWIGLU ? 2 : 1) * a.N * a.K * 2;
     if (per_wave <= MF_ONE && NT == 1 && ntup >= MINITP_MF_LOOP_MIN && w_bytes < (1LL << 30)) {
       // many tuples: several a block, the input rows' prologue shared
-      auto kern = a.M > MINITP_MF_PLAIN_ROWS ? gemv_mfma_loop_kernel<PRO, EPI, 0> : gemv_mfma_loop_kernel<PRO, EPI, AUX_NT>;
+      // (weights plain above 16 rows for the gate/up; the LM head's 272 MB
+      // stream stays non-temporal: 53 against 58 us at batch 32, kernel trace)
+      auto kern = a.M > MINITP_MF_PLAIN_ROWS && EPI == EPI_SWIGLU ? gemv_mfma_loop_kernel<PRO, EPI, 0>
+                                                                  : gemv_mfma_loop_kernel<PRO, EPI, AUX_NT>;
       const int lds = 4 * MF_X_STAGE;
       const int rc = ensure_lds_limit((const void*)kern, lds);
       if (rc) return rc;
