@@ -62,14 +62,14 @@ constexpr bool is_qkv() {
 // MINITP_NT_LOADS is set.
 constexpr int W_AUX = MINITP_NT_LOADS ? 2 : 0;
 // The MFMA GEMVs (3-32 input rows) load their weights non-temporal up to
-// MINITP_MF_PLAIN_ROWS input rows and plain above (the tuple loop takes the
-// policy as a template argument; the half-row form, which serves more than 16
-// rows, loads plain), except the split-K form and the plain-store tuple loop
-// (the LM head), non-temporal at every row count. 0.5B, 2,048-token prompts, ms a step non-temporal / plain for all of
-// them: batch 3 0.909 / 0.958, 4 0.905 / 0.973, 8 0.903 / 0.927, 16 0.960 /
-// 0.958, 32 1.040-1.042 / 1.035-1.037; 7B batch 3-8 the same either way. At
-// batch 32 the split-K form non-temporal with the others plain: 1.033-1.035
-// against 1.037-1.044 ms.
+// MINITP_MF_PLAIN_ROWS input rows and plain above (the half-row form, which
+// serves more than 16 rows, and the SwiGLU tuple loop), except the split-K
+// form and the plain-store tuple loop (the LM head), non-temporal at every
+// row count. 0.5B, 2,048-token prompts, ms a step with all of them
+// non-temporal / plain: batch 3 0.909 / 0.958, 4 0.905 / 0.973, 8 0.903 /
+// 0.927, 16 0.960 / 0.958, 32 1.040-1.042 / 1.035-1.037; 7B batch 3-8 the
+// same either way. At batch 32, the split-K form non-temporal with the
+// others plain: 1.033-1.035 against 1.037-1.044 ms.
 #ifndef MINITP_MF_PLAIN_ROWS
 #define MINITP_MF_PLAIN_ROWS 16
 #endif
